@@ -1,0 +1,165 @@
+/*
+ * qdc_hip.h -- C ABI of libqdc_hip.so: the fused per-layer row kernels of the
+ * Qwen3.5 hybrid backbone forward, hand-written HIP for MI355X (gfx950).
+ *
+ * Conventions shared by every device entry point:
+ *  - Tensors are device pointers to row-major data; "[rows, width]" here is the
+ *    reference's column-major (width, rows) Julia matrix in the same memory.
+ *    Strides ("tok", "head", "ld") are in elements, not bytes.
+ *  - dtype selects the element type of every activation and weight argument of
+ *    the call (QDC_F32 or QDC_BF16).  Arithmetic is fp32; bf16 results are
+ *    rounded to nearest even.  RoPE tables are always fp32.
+ *  - The library never allocates or frees memory, keeps no pointer after
+ *    return, has no mutable global state and never synchronises: work is
+ *    enqueued on `stream` (0 = the null stream of the current device) and the
+ *    caller keeps every buffer alive until that stream has completed it.
+ *  - Return value: 0 on success; a negative qdc_status for an argument error
+ *    detected on the host before anything is enqueued; a positive hipError_t
+ *    when the launch itself failed.
+ *  - Unaligned pointers/strides or unusual widths are accepted and take a
+ *    slower general kernel; the fast kernels need 16-byte alignment.
+ */
+#ifndef QDC_HIP_H
+#define QDC_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    QDC_F32 = 0,
+    QDC_BF16 = 1
+} qdc_dtype;
+
+typedef enum {
+    QDC_OK = 0,
+    QDC_ERR_NULL = -1,        /* a required pointer is NULL                  */
+    QDC_ERR_SHAPE = -2,       /* negative / zero / inconsistent dimensions    */
+    QDC_ERR_DTYPE = -3,       /* unsupported dtype or dtype combination       */
+    QDC_ERR_RANGE = -4,       /* token id or position outside its table       */
+    QDC_ERR_ALIAS = -5        /* an output overlaps an input it may not alias */
+} qdc_status;
+
+/* Library version string ("qdc_hip <major>.<minor>.<patch>"). */
+const char *qdc_version(void);
+/* Human-readable text for a status returned by any entry point. */
+const char *qdc_status_string(int32_t status);
+
+/*
+ * Embedding gather: out[t, :] = table[ids[t], :] for t < n_ids.
+ * Replaces native_gather / gather_kernel! (ext/amdgpu_workspace.jl:206-236;
+ * generic src/backbone.jl:55, CPU :56-64).  A pure copy: bf16->bf16 and
+ * f32->f32 move bits, bf16->f32 widens by <<16 (src/safetensors.jl:28-30), so
+ * results are bit-exact.  ids are device int32, 0-based.  Ids are validated on
+ * the host beforehand as in the reference (qdc_check_ids); an id outside
+ * [0, vocab) that reaches the kernel writes a zero row and, when error_flag is
+ * not NULL, sets *error_flag = 1 (device int32, cleared by the caller).
+ */
+int32_t qdc_embedding_gather(void *out, int32_t out_dtype, const void *table, int32_t table_dtype,
+                             const int32_t *ids, int64_t n_ids, int64_t vocab, int64_t hidden,
+                             int32_t *error_flag, hipStream_t stream);
+
+/*
+ * Host-side id check of check_sequence / native_gather (src/backbone.jl:417-418,
+ * ext/amdgpu_workspace.jl:223-224): QDC_OK when every ids[t] is in [0, vocab),
+ * QDC_ERR_RANGE otherwise.  `ids` is host memory.
+ */
+int32_t qdc_check_ids(const int64_t *ids, int64_t n_ids, int64_t vocab);
+
+/*
+ * RMSNorm of `rows` rows of `width`: s = 1/sqrt(sum(x^2)/width + eps);
+ * out = (x*s)*(1+w) if centered (zero-centred weight), else (x*s)*w.
+ * Replaces native_rms / rms_kernel! (ext/amdgpu_workspace.jl:113-149; generic
+ * src/backbone.jl:200-204; CPU cpu_rms! src/backbone_cpu.jl:333-350).  Serves
+ * the input, post-attention and final norms, per-head q/k rows without RoPE
+ * (rows = tokens*heads, width = head_dim) and, with centered = 0, the plain
+ * DeltaNet output norm.  Row r reads x + r*ld_x and writes out + r*ld_out;
+ * out may equal x.
+ */
+int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows, int64_t width,
+                    int64_t ld_x, int64_t ld_out, float eps, int32_t centered, int32_t dtype,
+                    hipStream_t stream);
+
+/*
+ * residual = x + mixed; out = zero-centred RMSNorm(residual) with weight.
+ * Replaces native_residual_rms (ext/amdgpu_workspace.jl:157-166; generic
+ * src/backbone.jl:347-350; CPU src/backbone_cpu.jl:321-328) in one pass.
+ * Contiguous rows of `width`.  residual may equal x or mixed; out may equal
+ * x or mixed; out and residual must differ.
+ */
+int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x, const void *mixed,
+                             const void *weight, int64_t rows, int64_t width, float eps,
+                             int32_t dtype, hipStream_t stream);
+
+/*
+ * Per-head zero-centred RMSNorm fused with half-split partial RoPE, for the Q
+ * heads and the K heads of full attention in one launch.
+ * Replaces prepare_head_kernel! (ext/amdgpu_attention.jl:1-43, launches
+ * :122-147); generic native_rms + native_rope (src/backbone.jl:200-235); CPU
+ * cpu_full_rms! + cpu_full_rope! (src/backbone_cpu.jl:113-136).
+ *   Q row (t, h), h < heads:    in  q_in  + t*q_in_tok  + h*q_in_head
+ *                               out q_out + t*q_out_tok + h*q_out_head
+ *   K row (t, g), g < kv_heads: likewise with k_*.
+ * q_in_head = 2*head_dim reads q straight out of the interleaved q||gate
+ * projection (src/backbone.jl:226-227).  For i < rotary_dim/2 the pair
+ * (i, i+rotary_dim/2) is rotated by the angle of position
+ * p = pos_offset + t % seq_len:  a' = a*cos - b*sin, b' = b*cos + a*sin, with
+ * cos_table/sin_table fp32 [table_len, rotary_dim/2] (see qdc_rope_tables);
+ * dims >= rotary_dim pass through normalised.  heads or kv_heads may be 0 to
+ * process only one side (its pointers may then be NULL).  Outputs must not
+ * overlap inputs unless out == in with identical strides.
+ */
+int32_t qdc_qk_norm_rope(void *q_out, void *k_out, const void *q_in, const void *k_in,
+                         const void *q_norm, const void *k_norm, const float *cos_table,
+                         const float *sin_table, int64_t tokens, int64_t heads, int64_t kv_heads,
+                         int64_t head_dim, int64_t rotary_dim, int64_t seq_len, int64_t pos_offset,
+                         int64_t table_len, int64_t q_in_tok, int64_t q_in_head, int64_t q_out_tok,
+                         int64_t q_out_head, int64_t k_in_tok, int64_t k_in_head, int64_t k_out_tok,
+                         int64_t k_out_head, float eps, int32_t dtype, hipStream_t stream);
+
+/*
+ * Host-side RoPE tables, fp32 [n_pos, rotary_dim/2] each, built the way the
+ * reference CPU path builds them (cpu_full_workspace src/backbone_cpu.jl:90-111):
+ * freq_i = 1/theta^(2i/rotary_dim) and angle = freq_i*pos in fp32, cos/sin of
+ * that fp32 angle correctly rounded to fp32.  Host memory; the caller copies
+ * them to the device once per (rotary_dim, theta, length).
+ */
+int32_t qdc_rope_tables(float *cos_table, float *sin_table, int64_t n_pos, int64_t rotary_dim,
+                        float theta);
+
+/*
+ * Gated RMSNorm of the DeltaNet output, per (token, head) row of `width`:
+ * out = ((x*s)*w)*silu(z), silu(z) = z/(1+exp(-z)), not centred.
+ * Replaces the two-pass native_rms(...; centered=false) + broadcast
+ * (ext/amdgpu_delta.jl:181-184; generic src/backbone.jl:339-341; CPU
+ * cpu_delta_gate_output! ext/QwenDecisionCoreLoopVectorizationExt.jl:373-390).
+ * Row (t, h) reads x + t*x_tok + h*width and z + t*z_tok + h*width (z may sit
+ * inside the packed projection) and writes out + t*out_tok + h*width.
+ * out may equal x.
+ */
+int32_t qdc_gated_rmsnorm(void *out, const void *x, const void *z, const void *weight,
+                          int64_t tokens, int64_t heads, int64_t width, int64_t x_tok,
+                          int64_t z_tok, int64_t out_tok, float eps, int32_t dtype,
+                          hipStream_t stream);
+
+/*
+ * SwiGLU: out[t, i] = silu(gate[t, i]) * up[t, i] for i < width.
+ * Replaces mlp_gate_kernel! (ext/amdgpu_mlp.jl:63-75; generic native_mlp_gate!
+ * src/backbone.jl:352-355; CPU cpu_portable_gate!
+ * ext/QwenDecisionCoreLoopVectorizationExt.jl:189-215).  For the packed
+ * gate||up GEMM output pass gate = packed, up = packed + width,
+ * ld_gate = ld_up = 2*width; out is the down-projection input.
+ * out may equal gate or up when its stride equals theirs.
+ */
+int32_t qdc_swiglu(void *out, const void *gate, const void *up, int64_t tokens, int64_t width,
+                   int64_t ld_gate, int64_t ld_up, int64_t ld_out, int32_t dtype,
+                   hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,196 @@
+"""CPU restatement of ``backbone_hidden`` for end-to-end parity checks.
+
+TEST INFRASTRUCTURE ONLY (see ``qdc_oracle.py``).  The in-scope row ops go
+through the C oracle; the GEMMs, attention and the DeltaNet recurrence are
+numpy fp32 restatements of the reference's generic and CPU paths.
+
+Weights are a dict of float32 numpy arrays keyed by the checkpoint names with
+the ``language_model.`` prefix removed (``layers.0.mlp.gate_proj.weight`` ...),
+laid out as stored (PyTorch ``[out, in]``), which is the reference's Julia
+``(in, out)`` matrix in the same memory.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import qdc_oracle as ops
+
+F32 = np.float32
+FLOATMAX = np.finfo(np.float32).max
+
+
+def config_from_text_config(cfg: dict) -> dict:
+    """Config parsing of ``QwenBackbone`` (``src/backbone.jl:84-106``)."""
+    if cfg.get("attention_bias", False):
+        raise ValueError("Attention biases are not supported.")
+    if cfg.get("hidden_act", "silu") != "silu":
+        raise ValueError("Expected SiLU activation.")
+    rope = cfg["rope_parameters"]
+    if rope.get("rope_type", "default") != "default":
+        raise ValueError("Only default RoPE is supported.")
+    out = dict(
+        hidden=int(cfg["hidden_size"]),
+        head_dim=int(cfg["head_dim"]),
+        heads=int(cfg["num_attention_heads"]),
+        kv_heads=int(cfg["num_key_value_heads"]),
+        key_heads=int(cfg["linear_num_key_heads"]),
+        value_heads=int(cfg["linear_num_value_heads"]),
+        key_dim=int(cfg["linear_key_head_dim"]),
+        value_dim=int(cfg["linear_value_head_dim"]),
+        eps=float(F32(cfg["rms_norm_eps"])),
+        rope_theta=float(F32(rope["rope_theta"])),
+        # only rope_parameters.partial_rotary_factor is read (src/backbone.jl:101)
+        rotary_dim=int(cfg["head_dim"] * rope.get("partial_rotary_factor", 1.0)),
+        layer_types=list(cfg["layer_types"]),
+    )
+    if out["value_heads"] % out["key_heads"]:
+        raise ValueError("Value heads must be a multiple of key heads.")
+    if out["heads"] % out["kv_heads"]:
+        raise ValueError("Query heads must be a multiple of KV heads.")
+    return out
+
+
+def _silu(x):
+    return ops.silu(x)
+
+
+def _sigmoid(x):
+    x = x.astype(F32)
+    with np.errstate(over="ignore"):
+        return F32(1) / (F32(1) + np.exp(-x))
+
+
+def _softplus(x):
+    """``native_softplus`` (``src/backbone.jl:198``)."""
+    x = x.astype(F32)
+    return np.maximum(x, F32(0)) + np.log1p(np.exp(-np.abs(x))).astype(F32)
+
+
+def _linear(x, w):
+    """``native_linear``: y[T, out] = x[T, in] @ W[out, in]^T in fp32."""
+    return (x @ w.T).astype(F32)
+
+
+def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, tables):
+    """``full_attention`` (``src/backbone.jl:224-262``) on ``x [T, hidden]``."""
+    T = x.shape[0]
+    hd, H, KV = cfg["head_dim"], cfg["heads"], cfg["kv_heads"]
+    qgate = _linear(x, W[p + "self_attn.q_proj.weight"]).reshape(T, H, 2 * hd)
+    cos, sin = tables
+    q = ops.qk_norm_rope(qgate[:, :, :hd], W[p + "self_attn.q_norm.weight"], cos, sin,
+                         cfg["rotary_dim"], cfg["eps"])
+    kp = _linear(x, W[p + "self_attn.k_proj.weight"]).reshape(T, KV, hd)
+    k = ops.qk_norm_rope(kp, W[p + "self_attn.k_norm.weight"], cos, sin, cfg["rotary_dim"], cfg["eps"])
+    v = _linear(x, W[p + "self_attn.v_proj.weight"]).reshape(T, KV, hd)
+    # scores_mask[i (key), j (query)] (src/backbone.jl:237-242)
+    keys = np.arange(T)[:, None]
+    queries = np.arange(T)[None, :]
+    smask = np.where((keys <= queries) & (mask[:, None] == 1), F32(0), F32(-FLOATMAX)).astype(F32)
+    groups = H // KV
+    out = np.empty((T, H * hd), F32)
+    scale = F32(np.sqrt(F32(hd)))
+    for h in range(H):
+        kv = h // groups
+        scores = (k[:, kv, :] @ q[:, h, :].T).astype(F32) / scale + smask  # [key, query]
+        with np.errstate(over="ignore", invalid="ignore"):
+            probs = np.exp(scores - scores.max(axis=0, keepdims=True)).astype(F32)
+        probs /= probs.sum(axis=0, keepdims=True)
+        values = (probs.T @ v[:, kv, :]).astype(F32)  # [query, hd]
+        gate = _sigmoid(qgate[:, h, hd:])
+        out[:, h * hd:(h + 1) * hd] = values * gate
+    return _linear(out, W[p + "self_attn.o_proj.weight"])
+
+
+def causal_depthwise(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """``causal_depthwise`` (``src/backbone.jl:264-276``): x [T, C], w [C, K], then SiLU."""
+    T, C = x.shape
+    K = w.shape[1]
+    out = np.zeros((T, C), F32)
+    for index in range(K):
+        lag = K - 1 - index
+        if lag >= T:
+            continue
+        out[lag:, :] += x[:T - lag, :] * w[:, index][None, :]
+    return _silu(out)
+
+
+def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict):
+    """Gated DeltaNet, recurrent form of the CPU default path.
+
+    ``cpu_delta_prepare`` (``src/backbone_cpu.jl:465-499``) and
+    ``cpu_delta_recurrent_heads!`` / ``cpu_delta_recurrent_step!``
+    (``src/backbone_cpu.jl:680-759``), which equals the chunked generic form
+    ``delta_attention`` (``src/backbone.jl:284-345``) up to rounding."""
+    T = x.shape[0]
+    kd, kh, vd, vh = cfg["key_dim"], cfg["key_heads"], cfg["value_dim"], cfg["value_heads"]
+    masked = (x * mask.astype(F32)[:, None]).astype(F32)
+    qkv = _linear(masked, W[p + "linear_attn.in_proj_qkv.weight"])
+    conv = W[p + "linear_attn.conv1d.weight"]
+    conv = conv.reshape(conv.shape[0], conv.shape[-1])
+    mixed = causal_depthwise(qkv, conv)
+    kw = kd * kh
+    q = mixed[:, :kw].reshape(T, kh, kd)
+    k = mixed[:, kw:2 * kw].reshape(T, kh, kd)
+    v = mixed[:, 2 * kw:].reshape(T, vh, vd)
+    q = (q / (np.sqrt((q * q).sum(-1, keepdims=True) + F32(1e-6)) * np.sqrt(F32(kd)))).astype(F32)
+    k = (k / (np.sqrt((k * k).sum(-1, keepdims=True) + F32(1e-6)) * F32(1))).astype(F32)
+    z = _linear(masked, W[p + "linear_attn.in_proj_z.weight"]).reshape(T, vh, vd)
+    beta = _sigmoid(_linear(masked, W[p + "linear_attn.in_proj_b.weight"]))
+    a_decay = (F32(-1) * np.exp(W[p + "linear_attn.A_log"].astype(F32))).astype(F32)
+    decay = (a_decay * _softplus(_linear(masked, W[p + "linear_attn.in_proj_a.weight"])
+                                 + W[p + "linear_attn.dt_bias"])).astype(F32)
+    groups = vh // kh
+    kidx = np.arange(vh) // groups
+    state = np.zeros((vh, vd, kd), F32)
+    result = np.empty((T, vh, vd), F32)
+    for t in range(T):
+        factor = np.exp(decay[t]).astype(F32)                     # [vh]
+        kt = k[t, kidx]                                            # [vh, kd]
+        qt = q[t, kidx]
+        proj = np.einsum("hvk,hk->hv", state, kt).astype(F32)
+        proj = (beta[t][:, None] * (v[t] - factor[:, None] * proj)).astype(F32)
+        state = (factor[:, None, None] * state + proj[:, :, None] * kt[:, None, :]).astype(F32)
+        result[t] = np.einsum("hvk,hk->hv", state, qt)
+    out = ops.gated_rms(result, z, W[p + "linear_attn.norm.weight"], cfg["eps"])
+    return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
+
+
+def check_sequence(ids, mask, vocab):
+    """``check_sequence`` (``src/backbone.jl:413-422``)."""
+    ids = np.asarray(ids)
+    mask = np.asarray(mask)
+    if ids.size != mask.size:
+        raise ValueError("Input IDs and mask must have identical lengths.")
+    if ids.size == 0:
+        raise ValueError("Inputs must not be empty.")
+    if ids.min() < 0 or ids.max() >= vocab:
+        raise ValueError("Token ID is outside the vocabulary.")
+    if not np.isin(mask, (0, 1)).all():
+        raise ValueError("Mask values must be zero or one.")
+
+
+def backbone_hidden(W: dict, cfg: dict, ids, mask) -> np.ndarray:
+    """``backbone_hidden`` (``src/backbone.jl:433-460``) -> ``[T, hidden]`` fp32."""
+    embed = W["embed_tokens.weight"]
+    check_sequence(ids, mask, embed.shape[0])
+    ids = np.asarray(ids, dtype=np.int32).reshape(-1)
+    mask = np.asarray(mask, dtype=np.int64).reshape(-1)
+    T = ids.size
+    h = ops.gather(embed, ids)
+    tables = ops.rope_tables(T, cfg["rotary_dim"], cfg["rope_theta"]) if cfg["rotary_dim"] else (
+        np.zeros((T, 0), F32), np.zeros((T, 0), F32))
+    eps = cfg["eps"]
+    for i, kind in enumerate(cfg["layer_types"]):
+        p = f"layers.{i}."
+        normed = ops.rms(h, W[p + "input_layernorm.weight"], eps)
+        if kind == "full_attention":
+            mixed = full_attention(W, p, normed, mask, cfg, tables)
+        elif kind == "linear_attention":
+            mixed = delta_attention(W, p, normed, mask, cfg)
+        else:
+            raise ValueError(f"Unsupported layer type {kind}.")
+        residual, normed = ops.residual_rms(h, mixed, W[p + "post_attention_layernorm.weight"], eps)
+        gate = _linear(normed, W[p + "mlp.gate_proj.weight"])
+        up = _linear(normed, W[p + "mlp.up_proj.weight"])
+        h = (residual + _linear(ops.swiglu(gate, up), W[p + "mlp.down_proj.weight"])).astype(F32)
+    return ops.rms(h, W["norm.weight"], eps)

@@ -1,0 +1,144 @@
+// qdc_common.hpp -- shared device helpers for the CDNA4 (gfx950) row kernels.
+//
+// Data moves in 16-byte chunks (global_load/store_dwordx4): 4 fp32 or 8 bf16
+// values.  Arithmetic is fp32; bf16 is widened by a shift and narrowed with the
+// hardware round-to-nearest-even pack (v_cvt_pk_bf16_f32), which equals the
+// reference's RNE formula (src/safetensors.jl:37-42) on every finite value.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qdc_hip.h"
+
+namespace qdc {
+
+typedef uint16_t bf16_t;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // 4 wavefronts per workgroup
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static constexpr int kVec = 4;  // elements per 16-byte chunk
+};
+template <> struct Elem<bf16_t> {
+    static constexpr int kVec = 8;
+};
+
+// ---------------------------------------------------------------- scalars --
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+    f32x2 p = {v, 0.0f};
+    bf16x2 b = __builtin_convertvector(p, bf16x2);
+    return (bf16_t)(__builtin_bit_cast(uint32_t, b) & 0xffffu);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    f32x2 p = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2));
+}
+
+// ------------------------------------------------------ 16-byte chunk I/O --
+// `p` must be 16-byte aligned.  Values land in / come from v[0..kVec).
+__device__ __forceinline__ void load_chunk(const float *p, float (&v)[4]) {
+    const f32x4 r = *reinterpret_cast<const f32x4 *>(p);
+    v[0] = r.x; v[1] = r.y; v[2] = r.z; v[3] = r.w;
+}
+__device__ __forceinline__ void load_chunk(const bf16_t *p, float (&v)[8]) {
+    const u32x4 r = *reinterpret_cast<const u32x4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(r[i] << 16);
+        v[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ void store_chunk(float *p, const float (&v)[4]) {
+    f32x4 r = {v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4 *>(p) = r;
+}
+__device__ __forceinline__ void store_chunk(bf16_t *p, const float (&v)[8]) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4 *>(p) = r;
+}
+
+// ------------------------------------------------------------- reductions --
+// Sum over aligned groups of N lanes (N a power of two <= 64) of a wavefront.
+template <int N> __device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int offset = N / 2; offset >= 1; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+    return v;
+}
+
+// 1/sqrt(sum/width + eps) in fp32, the reference's operation order
+// (src/backbone_cpu.jl:344): divide, add, square root, reciprocal.
+__device__ __forceinline__ float rms_scale(float sum_squares, float width, float eps) {
+    return 1.0f / __builtin_sqrtf(sum_squares / width + eps);
+}
+
+// silu(x) = x * (1/(1 + exp(-x))) (src/backbone.jl:196-197).  exp(-x) is
+// computed as exp2(-x*log2(e)) on the hardware transcendental unit and the
+// reciprocal with v_rcp_f32: both within ~1 ulp, ample for the 1e-5 relative
+// bar.  Overflow of exp for x < -88 gives 1/inf = 0 and x*0 = -0, as on the CPU.
+__device__ __forceinline__ float silu(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// ------------------------------------------------------ integer division --
+// Division of n < 2^31 by a fixed divisor d >= 1 with one multiply-high, add
+// and shift (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, sec. 4): l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1,  q = (mulhi(n, m) + n) >> l.
+struct FastDiv {
+    uint32_t d, m, l;
+};
+
+static inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint64_t m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+    return FastDiv{d, (uint32_t)m, l};
+}
+
+__host__ __device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv &f) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return (__umulhi(n, f.m) + n) >> f.l;
+#else
+    return (uint32_t)((((uint64_t)n * f.m) >> 32) + n) >> f.l;
+#endif
+}
+
+// Internal dispatch result: no fast-path kernel fits the shape.
+constexpr int32_t kNoFastPath = INT32_MIN;
+
+// --------------------------------------------------------- host helpers ---
+static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+static inline int64_t elem_size(int32_t dtype) { return dtype == QDC_BF16 ? 2 : 4; }
+static inline bool valid_dtype(int32_t dtype) { return dtype == QDC_F32 || dtype == QDC_BF16; }
+
+// Launch status: a positive hipError_t when the launch failed, else 0.
+static inline int32_t launch_status() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? QDC_OK : (int32_t)e;
+}
+
+static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Byte ranges [a, a+na) and [b, b+nb) intersect.
+static inline bool overlaps(const void *a, int64_t na, const void *b, int64_t nb) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return na > 0 && nb > 0 && x < y + (uintptr_t)nb && y < x + (uintptr_t)na;
+}
+
+}  // namespace qdc

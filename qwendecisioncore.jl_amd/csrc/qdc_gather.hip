@@ -1,0 +1,156 @@
+// qdc_gather.hip -- embedding gather (token id -> row copy) for gfx950, plus
+// the host-side id check and the library's version/status strings.
+//
+// Fast path: one wavefront per token row, 16-byte chunks, U chunks per lane in
+// flight before the first store.  bf16->bf16 and f32->f32 move bits;
+// bf16->f32 widens each value by a 16-bit shift, so results are bit-exact.
+#include "qdc_common.hpp"
+
+namespace qdc {
+namespace {
+
+constexpr int kUnroll = 4;
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void gather_fast(TO *__restrict__ out,
+                                                      const TI *__restrict__ table,
+                                                      const int32_t *__restrict__ ids,
+                                                      int64_t n_ids, int64_t vocab,
+                                                      int64_t hidden, int32_t *error_flag) {
+    constexpr int V = Elem<TI>::kVec;  // input elements per 16-byte chunk
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    if (row >= n_ids) return;  // uniform per wavefront
+    const int64_t id = ids[row];
+    TO *dst = out + row * hidden;
+    const int64_t chunks = hidden / V;
+    if (id < 0 || id >= vocab) {
+        for (int64_t c = lane; c < chunks; c += kWave) {
+            float zero[V] = {};
+            if constexpr (sizeof(TI) == sizeof(TO)) {
+                store_chunk(reinterpret_cast<TI *>(dst) + c * V, zero);
+            } else {
+                float lo[4] = {}, hi[4] = {};
+                store_chunk(dst + c * V, lo);
+                store_chunk(dst + c * V + 4, hi);
+            }
+        }
+        if (lane == 0 && error_flag) atomicOr(error_flag, 1);
+        return;
+    }
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(table + id * hidden);
+    for (int64_t base = 0; base < chunks; base += kWave * kUnroll) {
+        u32x4 r[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t c = base + u * kWave + lane;
+            if (c < chunks) r[u] = src[c];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t c = base + u * kWave + lane;
+            if (c >= chunks) continue;
+            if constexpr (sizeof(TI) == sizeof(TO)) {
+                reinterpret_cast<u32x4 *>(dst)[c] = r[u];
+            } else {  // bf16 -> f32: 8 values -> two 16-byte stores
+                u32x4 lo, hi;
+                lo[0] = r[u][0] << 16; lo[1] = r[u][0] & 0xffff0000u;
+                lo[2] = r[u][1] << 16; lo[3] = r[u][1] & 0xffff0000u;
+                hi[0] = r[u][2] << 16; hi[1] = r[u][2] & 0xffff0000u;
+                hi[2] = r[u][3] << 16; hi[3] = r[u][3] & 0xffff0000u;
+                u32x4 *d = reinterpret_cast<u32x4 *>(dst) + 2 * c;
+                d[0] = lo;
+                d[1] = hi;
+            }
+        }
+    }
+}
+
+// One wavefront per row, element by element; any alignment and width.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void gather_general(TO *__restrict__ out,
+                                                         const TI *__restrict__ table,
+                                                         const int32_t *__restrict__ ids,
+                                                         int64_t n_ids, int64_t vocab,
+                                                         int64_t hidden, int32_t *error_flag) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    if (row >= n_ids) return;
+    const int64_t id = ids[row];
+    TO *dst = out + row * hidden;
+    const bool ok = id >= 0 && id < vocab;
+    const TI *src = table + (ok ? id : 0) * hidden;
+    for (int64_t i = lane; i < hidden; i += kWave) {
+        if constexpr (sizeof(TI) == sizeof(TO)) {
+            dst[i] = ok ? src[i] : TO(0);
+        } else {
+            dst[i] = ok ? to_f32(src[i]) : 0.0f;
+        }
+    }
+    if (!ok && lane == 0 && error_flag) atomicOr(error_flag, 1);
+}
+
+template <typename TI, typename TO>
+int32_t launch(void *out, const void *table, const int32_t *ids, int64_t n_ids, int64_t vocab,
+               int64_t hidden, int32_t *error_flag, bool fast, hipStream_t stream) {
+    const int64_t blocks = ceil_div(n_ids, kBlock / kWave);
+    if (fast && hidden % Elem<TI>::kVec == 0)
+        hipLaunchKernelGGL((gather_fast<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+                           (TO *)out, (const TI *)table, ids, n_ids, vocab, hidden, error_flag);
+    else
+        hipLaunchKernelGGL((gather_general<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0,
+                           stream, (TO *)out, (const TI *)table, ids, n_ids, vocab, hidden,
+                           error_flag);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace qdc
+
+using namespace qdc;
+
+extern "C" const char *qdc_version(void) { return "qdc_hip 0.1.0"; }
+
+extern "C" const char *qdc_status_string(int32_t status) {
+    switch (status) {
+        case QDC_OK: return "ok";
+        case QDC_ERR_NULL: return "a required pointer is NULL";
+        case QDC_ERR_SHAPE: return "invalid or inconsistent dimensions";
+        case QDC_ERR_DTYPE: return "unsupported dtype";
+        case QDC_ERR_RANGE: return "token id or position outside its table";
+        case QDC_ERR_ALIAS: return "an output overlaps an input it may not alias";
+        default: break;
+    }
+    return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+}
+
+extern "C" int32_t qdc_check_ids(const int64_t *ids, int64_t n_ids, int64_t vocab) {
+    if (n_ids < 0 || vocab < 0) return QDC_ERR_SHAPE;
+    if (n_ids > 0 && !ids) return QDC_ERR_NULL;
+    for (int64_t t = 0; t < n_ids; ++t)
+        if (ids[t] < 0 || ids[t] >= vocab) return QDC_ERR_RANGE;
+    return QDC_OK;
+}
+
+extern "C" int32_t qdc_embedding_gather(void *out, int32_t out_dtype, const void *table,
+                                        int32_t table_dtype, const int32_t *ids, int64_t n_ids,
+                                        int64_t vocab, int64_t hidden, int32_t *error_flag,
+                                        hipStream_t stream) {
+    if (!valid_dtype(out_dtype) || !valid_dtype(table_dtype)) return QDC_ERR_DTYPE;
+    if (table_dtype == QDC_F32 && out_dtype == QDC_BF16) return QDC_ERR_DTYPE;  // not a copy
+    if (n_ids < 0 || vocab < 0 || hidden < 0) return QDC_ERR_SHAPE;
+    if (n_ids == 0 || hidden == 0) return QDC_OK;
+    if (vocab == 0) return QDC_ERR_RANGE;
+    if (!out || !table || !ids) return QDC_ERR_NULL;
+    const int64_t ti = elem_size(table_dtype), to = elem_size(out_dtype);
+    if (overlaps(out, n_ids * hidden * to, table, vocab * hidden * ti) ||
+        overlaps(out, n_ids * hidden * to, ids, n_ids * 4))
+        return QDC_ERR_ALIAS;
+    const bool fast = aligned16(out) && aligned16(table) && (hidden * ti) % 16 == 0;
+    if (table_dtype == QDC_F32)
+        return launch<float, float>(out, table, ids, n_ids, vocab, hidden, error_flag, fast, stream);
+    if (out_dtype == QDC_BF16)
+        return launch<bf16_t, bf16_t>(out, table, ids, n_ids, vocab, hidden, error_flag, fast,
+                                      stream);
+    return launch<bf16_t, float>(out, table, ids, n_ids, vocab, hidden, error_flag, fast, stream);
+}

@@ -1,0 +1,318 @@
+// qdc_rope.hip -- per-head zero-centred RMSNorm fused with half-split partial
+// RoPE for the Q and K heads of full attention (one launch for both), and the
+// host-side RoPE table builder.
+//
+// Fast path (head_dim*sizeof(T) <= 1024 bytes, rotary_dim/2 a multiple of the
+// 16-byte chunk): a group of LPR = head_dim/chunk lanes owns one (token, head)
+// row, one 16-byte chunk per lane.  The row is normalised in registers; the
+// rotation partner of a lane's chunk (the same offset in the other half of the
+// rotary block) lives in lane l +/- half/chunk of the same group and is fetched
+// with a lane permute, so every input byte is read from HBM once and every
+// output byte written once.  cos/sin come from small fp32 tables (L2-resident)
+// built on the host exactly as the reference CPU path builds them.
+//
+// General path (any shape/alignment): one wavefront per row; the normalised
+// rotary block is staged in LDS so in-place operation stays correct.
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+#include "qdc_common.hpp"
+
+namespace qdc {
+namespace {
+
+template <typename T> struct Side {
+    const T *in;
+    T *out;
+    const T *w;
+    int64_t in_tok, in_head, out_tok, out_head;
+    int64_t rows;  // tokens * heads of this side
+    FastDiv heads;
+};
+
+template <typename T> struct QKArgs {
+    Side<T> q, k;
+    const float *cos, *sin;
+    int64_t q_blocks;  // workgroups covering the Q rows; the rest cover K
+    FastDiv seq_len;
+    int64_t pos_offset;
+    int32_t half;      // rotary_dim / 2
+    int32_t dim;
+    float eps;
+};
+
+template <typename T, int LPR>
+__global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
+    constexpr int V = Elem<T>::kVec;
+    constexpr int RPB = kBlock / LPR;
+    const bool is_k = (int64_t)blockIdx.x >= a.q_blocks;
+    const Side<T> &sd = is_k ? a.k : a.q;
+    const int64_t block = is_k ? (int64_t)blockIdx.x - a.q_blocks : (int64_t)blockIdx.x;
+    const int lane = threadIdx.x % LPR;
+    const int group_base = (threadIdx.x % kWave) - lane;  // first lane of this row group
+    const int64_t row = block * RPB + threadIdx.x / LPR;
+    const bool active = row < sd.rows;
+
+    uint32_t t = 0, h = 0;
+    float v[V] = {};
+    float ss = 0.0f;
+    if (active) {
+        t = fastdiv((uint32_t)row, sd.heads);
+        h = (uint32_t)row - t * sd.heads.d;
+        load_chunk(sd.in + (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head + lane * V, v);
+#pragma unroll
+        for (int j = 0; j < V; ++j) ss += v[j] * v[j];
+    }
+    ss = group_sum<LPR>(ss);
+    const float s = rms_scale(ss, (float)a.dim, a.eps);
+    float wv[V];
+    load_chunk(sd.w + lane * V, wv);
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = (v[j] * s) * (1.0f + wv[j]);
+
+    // Partner chunk of the rotation, fetched from the owning lane.  Every lane
+    // takes part in the permute (inactive rows included) so it stays uniform.
+    const int hc = a.half / V;  // chunks per half of the rotary block
+    const bool rotary = lane < 2 * hc;
+    const int src = rotary ? (lane < hc ? lane + hc : lane - hc) : lane;
+    float p[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) p[j] = __shfl(v[j], group_base + src, kWave);
+    if (!active) return;
+
+    if (rotary) {
+        const uint32_t tq = fastdiv(t, a.seq_len);
+        const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
+        const int i0 = (lane < hc ? lane : lane - hc) * V;
+        const float *cp = a.cos + pos * a.half + i0;
+        const float *sp = a.sin + pos * a.half + i0;
+        float c[V], sn[V];
+#pragma unroll
+        for (int j = 0; j < V; j += 4) {
+            float c4[4], s4[4];
+            load_chunk(cp + j, c4);
+            load_chunk(sp + j, s4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                c[j + q] = c4[q];
+                sn[j + q] = s4[q];
+            }
+        }
+        if (lane < hc) {
+#pragma unroll
+            for (int j = 0; j < V; ++j) v[j] = v[j] * c[j] - p[j] * sn[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < V; ++j) v[j] = v[j] * c[j] + p[j] * sn[j];
+        }
+    }
+    store_chunk(sd.out + (int64_t)t * sd.out_tok + (int64_t)h * sd.out_head + lane * V, v);
+}
+
+constexpr int kMaxGeneralRotary = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void qk_norm_rope_general(QKArgs<T> a) {
+    __shared__ float staged[kBlock / kWave][kMaxGeneralRotary];
+    const bool is_k = (int64_t)blockIdx.x >= a.q_blocks;
+    const Side<T> &sd = is_k ? a.k : a.q;
+    const int64_t block = is_k ? (int64_t)blockIdx.x - a.q_blocks : (int64_t)blockIdx.x;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int64_t row = block * (kBlock / kWave) + wave;
+    const bool active = row < sd.rows;  // uniform per wavefront
+    const int dim = a.dim, half = a.half;
+    float *st = staged[wave];
+
+    const T *in = sd.in;
+    T *out = sd.out;
+    float s = 0.0f;
+    int64_t pos = 0;
+    if (active) {
+        const uint32_t t = fastdiv((uint32_t)row, sd.heads);
+        const uint32_t h = (uint32_t)row - t * sd.heads.d;
+        in += (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head;
+        out += (int64_t)t * sd.out_tok + (int64_t)h * sd.out_head;
+        const uint32_t tq = fastdiv(t, a.seq_len);
+        pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
+        float ss = 0.0f;
+        for (int i = lane; i < dim; i += kWave) {
+            const float v = to_f32(in[i]);
+            ss += v * v;
+        }
+        ss = group_sum<kWave>(ss);
+        s = rms_scale(ss, (float)dim, a.eps);
+        for (int i = lane; i < 2 * half; i += kWave) st[i] = (to_f32(in[i]) * s) * (1.0f + to_f32(sd.w[i]));
+    }
+    __syncthreads();
+    if (active) {
+        for (int i = lane; i < dim; i += kWave) {
+            float o;
+            if (i < half) {
+                const float c = a.cos[pos * half + i], sn = a.sin[pos * half + i];
+                o = st[i] * c - st[i + half] * sn;
+            } else if (i < 2 * half) {
+                const float c = a.cos[pos * half + i - half], sn = a.sin[pos * half + i - half];
+                o = st[i] * c + st[i - half] * sn;
+            } else {
+                o = (to_f32(in[i]) * s) * (1.0f + to_f32(sd.w[i]));
+            }
+            out[i] = from_f32<T>(o);
+        }
+    }
+}
+
+template <typename T>
+int32_t launch(QKArgs<T> a, bool fast, hipStream_t stream) {
+    constexpr int V = Elem<T>::kVec;
+    const int64_t chunks = a.dim / V;
+    if (fast && a.dim % V == 0 && a.half % V == 0 && chunks <= kWave &&
+        (chunks & (chunks - 1)) == 0) {
+        const int64_t rpb = kBlock / chunks;
+        a.q_blocks = ceil_div(a.q.rows, rpb);
+        const int64_t blocks = a.q_blocks + ceil_div(a.k.rows, rpb);
+#define QDC_QK(LPR)                                                                          \
+    case LPR:                                                                                \
+        hipLaunchKernelGGL((qk_norm_rope_fast<T, LPR>), dim3((uint32_t)blocks), dim3(kBlock), 0, \
+                           stream, a);                                                       \
+        return launch_status();
+        switch (chunks) {
+            QDC_QK(1)
+            QDC_QK(2)
+            QDC_QK(4)
+            QDC_QK(8)
+            QDC_QK(16)
+            QDC_QK(32)
+            QDC_QK(64)
+            default:
+                break;
+        }
+#undef QDC_QK
+    }
+    // the general kernel stages the rotary block of each row in LDS
+    if (2 * a.half > kMaxGeneralRotary) return QDC_ERR_SHAPE;
+    const int64_t rpb = kBlock / kWave;
+    a.q_blocks = ceil_div(a.q.rows, rpb);
+    const int64_t blocks = a.q_blocks + ceil_div(a.k.rows, rpb);
+    hipLaunchKernelGGL((qk_norm_rope_general<T>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+                       a);
+    return launch_status();
+}
+
+// Byte extent of a strided [tokens, heads, dim] view.
+int64_t span_bytes(int64_t tokens, int64_t heads, int64_t dim, int64_t tok, int64_t head,
+                   int64_t es) {
+    return ((tokens - 1) * tok + (heads - 1) * head + dim) * es;
+}
+
+}  // namespace
+}  // namespace qdc
+
+using namespace qdc;
+
+extern "C" int32_t qdc_rope_tables(float *cos_table, float *sin_table, int64_t n_pos,
+                                   int64_t rotary_dim, float theta) {
+    if (n_pos < 0 || rotary_dim < 0 || rotary_dim % 2) return QDC_ERR_SHAPE;
+    if (n_pos == 0 || rotary_dim == 0) return QDC_OK;
+    if (!cos_table || !sin_table) return QDC_ERR_NULL;
+    const int64_t half = rotary_dim / 2;
+    for (int64_t i = 0; i < half; ++i) {
+        // Float32 `^`, `inv`, `*` as in src/backbone_cpu.jl:92-95; Julia's Float32
+        // pow/cos/sin evaluate in Float64 and round once.
+        const float exponent = (float)(2 * i) / (float)rotary_dim;
+        const float power = (float)std::pow((double)theta, (double)exponent);
+        const float freq = 1.0f / power;
+        for (int64_t p = 0; p < n_pos; ++p) {
+            const float angle = freq * (float)p;
+            cos_table[p * half + i] = (float)std::cos((double)angle);
+            sin_table[p * half + i] = (float)std::sin((double)angle);
+        }
+    }
+    return QDC_OK;
+}
+
+extern "C" int32_t qdc_qk_norm_rope(void *q_out, void *k_out, const void *q_in, const void *k_in,
+                                    const void *q_norm, const void *k_norm,
+                                    const float *cos_table, const float *sin_table, int64_t tokens,
+                                    int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                    int64_t rotary_dim, int64_t seq_len, int64_t pos_offset,
+                                    int64_t table_len, int64_t q_in_tok, int64_t q_in_head,
+                                    int64_t q_out_tok, int64_t q_out_head, int64_t k_in_tok,
+                                    int64_t k_in_head, int64_t k_out_tok, int64_t k_out_head,
+                                    float eps, int32_t dtype, hipStream_t stream) {
+    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
+    if (tokens < 0 || heads < 0 || kv_heads < 0 || head_dim <= 0 || rotary_dim < 0 ||
+        rotary_dim % 2 || rotary_dim > head_dim || seq_len <= 0 || pos_offset < 0 ||
+        table_len < 0)
+        return QDC_ERR_SHAPE;
+    if (head_dim > INT32_MAX || seq_len >= ((int64_t)1 << 31) ||
+        tokens * heads >= ((int64_t)1 << 31) || tokens * kv_heads >= ((int64_t)1 << 31))
+        return QDC_ERR_SHAPE;
+    if (tokens == 0 || (heads == 0 && kv_heads == 0)) return QDC_OK;
+    if (heads > 0 && (!q_out || !q_in || !q_norm)) return QDC_ERR_NULL;
+    if (kv_heads > 0 && (!k_out || !k_in || !k_norm)) return QDC_ERR_NULL;
+    if (rotary_dim > 0) {
+        if (!cos_table || !sin_table) return QDC_ERR_NULL;
+        if (pos_offset + std::min(tokens, seq_len) > table_len) return QDC_ERR_RANGE;
+    }
+    const int64_t es = elem_size(dtype);
+    // Strides must keep rows apart: head stride >= head_dim, token stride spans the heads.
+    auto strides_ok = [&](int64_t n, int64_t tok, int64_t head) {
+        return n == 0 || (head >= head_dim && tok >= (n - 1) * head + head_dim);
+    };
+    if (!strides_ok(heads, q_in_tok, q_in_head) || !strides_ok(heads, q_out_tok, q_out_head) ||
+        !strides_ok(kv_heads, k_in_tok, k_in_head) || !strides_ok(kv_heads, k_out_tok, k_out_head))
+        return QDC_ERR_SHAPE;
+    struct View {
+        const void *p;
+        int64_t bytes, tok, head;
+    };
+    const View qi{q_in, heads ? span_bytes(tokens, heads, head_dim, q_in_tok, q_in_head, es) : 0,
+                  q_in_tok, q_in_head};
+    const View qo{q_out, heads ? span_bytes(tokens, heads, head_dim, q_out_tok, q_out_head, es) : 0,
+                  q_out_tok, q_out_head};
+    const View ki{k_in, kv_heads ? span_bytes(tokens, kv_heads, head_dim, k_in_tok, k_in_head, es) : 0,
+                  k_in_tok, k_in_head};
+    const View ko{k_out,
+                  kv_heads ? span_bytes(tokens, kv_heads, head_dim, k_out_tok, k_out_head, es) : 0,
+                  k_out_tok, k_out_head};
+    // An output may coincide exactly with its own input (in place); any other
+    // overlap between an output and an input or the other output is rejected.
+    auto clash = [](const View &o, const View &i, bool own) {
+        if (own && o.p == i.p && o.tok == i.tok && o.head == i.head) return false;
+        return overlaps(o.p, o.bytes, i.p, i.bytes);
+    };
+    if (clash(qo, qi, true) || clash(qo, ki, false) || clash(ko, ki, true) ||
+        clash(ko, qi, false) || overlaps(qo.p, qo.bytes, ko.p, ko.bytes))
+        return QDC_ERR_ALIAS;
+
+    const bool fast = aligned16(q_out) && aligned16(q_in) && aligned16(q_norm) &&
+                      aligned16(k_out) && aligned16(k_in) && aligned16(k_norm) &&
+                      aligned16(cos_table) && aligned16(sin_table) &&
+                      ((q_in_tok | q_in_head | q_out_tok | q_out_head | k_in_tok | k_in_head |
+                        k_out_tok | k_out_head) *
+                       es) % 16 == 0 &&
+                      (rotary_dim / 2) % 4 == 0;
+    if (!fast && rotary_dim > kMaxGeneralRotary) return QDC_ERR_SHAPE;
+
+    auto fill = [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        QKArgs<T> a{};
+        a.q = Side<T>{(const T *)q_in, (T *)q_out, (const T *)q_norm, q_in_tok, q_in_head,
+                      q_out_tok, q_out_head, tokens * heads, make_fastdiv((uint32_t)std::max<int64_t>(heads, 1))};
+        a.k = Side<T>{(const T *)k_in, (T *)k_out, (const T *)k_norm, k_in_tok, k_in_head,
+                      k_out_tok, k_out_head, tokens * kv_heads,
+                      make_fastdiv((uint32_t)std::max<int64_t>(kv_heads, 1))};
+        a.cos = cos_table;
+        a.sin = sin_table;
+        a.seq_len = make_fastdiv((uint32_t)seq_len);
+        a.pos_offset = pos_offset;
+        a.half = (int32_t)(rotary_dim / 2);
+        a.dim = (int32_t)head_dim;
+        a.eps = eps;
+        return launch<T>(a, fast, stream);
+    };
+    if (dtype == QDC_BF16) return fill((bf16_t *)nullptr);
+    return fill((float *)nullptr);
+}

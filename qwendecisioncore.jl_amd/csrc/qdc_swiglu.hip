@@ -1,0 +1,113 @@
+// qdc_swiglu.hip -- SwiGLU out = silu(gate) * up for gfx950.
+//
+// Fast path: the [tokens, width] output is cut into 16-byte chunks numbered
+// row-major; each thread handles kUnroll chunks spaced one workgroup apart,
+// issuing all gate/up loads before any arithmetic.  Token/column of a chunk
+// come from one multiply-high division by the chunks-per-row count, so gate
+// and up may be separate tensors or the two halves of the packed gate||up
+// GEMM output (ld = 2*width) without any extra copy.
+#include <algorithm>
+
+#include "qdc_common.hpp"
+
+namespace qdc {
+namespace {
+
+constexpr int kUnroll = 4;
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_fast(T *out, const T *gate, const T *up,
+                                                      uint32_t total_chunks, FastDiv per_row,
+                                                      int64_t ld_gate, int64_t ld_up,
+                                                      int64_t ld_out) {
+    constexpr int V = Elem<T>::kVec;
+    const uint32_t base = blockIdx.x * (uint32_t)(kBlock * kUnroll) + threadIdx.x;
+    float g[kUnroll][V], u[kUnroll][V];
+    int64_t oo[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const uint32_t idx = base + (uint32_t)(k * kBlock);
+        oo[k] = -1;
+        if (idx < total_chunks) {
+            const uint32_t t = fastdiv(idx, per_row);
+            const int64_t col = (int64_t)(idx - t * per_row.d) * V;
+            load_chunk(gate + (int64_t)t * ld_gate + col, g[k]);
+            load_chunk(up + (int64_t)t * ld_up + col, u[k]);
+            oo[k] = (int64_t)t * ld_out + col;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        if (oo[k] < 0) continue;
+        float o[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) o[j] = silu(g[k][j]) * u[k][j];
+        store_chunk(out + oo[k], o);
+    }
+}
+
+// Element-wise, any width/stride/alignment.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_general(T *out, const T *gate, const T *up,
+                                                         int64_t tokens, int64_t width,
+                                                         int64_t ld_gate, int64_t ld_up,
+                                                         int64_t ld_out) {
+    const int64_t total = tokens * width;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * kBlock) {
+        const int64_t t = i / width, c = i - t * width;
+        const float g = to_f32(gate[t * ld_gate + c]);
+        const float u = to_f32(up[t * ld_up + c]);
+        out[t * ld_out + c] = from_f32<T>(silu(g) * u);
+    }
+}
+
+template <typename T>
+int32_t launch(void *out, const void *gate, const void *up, int64_t tokens, int64_t width,
+               int64_t ld_gate, int64_t ld_up, int64_t ld_out, bool fast, hipStream_t stream) {
+    constexpr int V = Elem<T>::kVec;
+    const int64_t chunks = tokens * (width / V);
+    if (fast && width % V == 0 && chunks < ((int64_t)1 << 31)) {
+        const int64_t blocks = ceil_div(chunks, kBlock * kUnroll);
+        hipLaunchKernelGGL((swiglu_fast<T>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+                           (T *)out, (const T *)gate, (const T *)up, (uint32_t)chunks,
+                           make_fastdiv((uint32_t)(width / V)), ld_gate, ld_up, ld_out);
+    } else {
+        const int64_t blocks = std::min<int64_t>(ceil_div(tokens * width, kBlock), 1 << 20);
+        hipLaunchKernelGGL((swiglu_general<T>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+                           (T *)out, (const T *)gate, (const T *)up, tokens, width, ld_gate, ld_up,
+                           ld_out);
+    }
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace qdc
+
+using namespace qdc;
+
+extern "C" int32_t qdc_swiglu(void *out, const void *gate, const void *up, int64_t tokens,
+                              int64_t width, int64_t ld_gate, int64_t ld_up, int64_t ld_out,
+                              int32_t dtype, hipStream_t stream) {
+    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
+    if (tokens < 0 || width < 0) return QDC_ERR_SHAPE;
+    if (tokens == 0 || width == 0) return QDC_OK;
+    if (!out || !gate || !up) return QDC_ERR_NULL;
+    if (ld_gate < width || ld_up < width || ld_out < width) return QDC_ERR_SHAPE;
+    if (width >= ((int64_t)1 << 31)) return QDC_ERR_SHAPE;
+    const int64_t es = elem_size(dtype);
+    const int64_t span_o = ((tokens - 1) * ld_out + width) * es;
+    // In place is allowed only element-for-element (same base and stride).
+    if (!(out == gate && ld_out == ld_gate) &&
+        overlaps(out, span_o, gate, ((tokens - 1) * ld_gate + width) * es))
+        return QDC_ERR_ALIAS;
+    if (!(out == up && ld_out == ld_up) &&
+        overlaps(out, span_o, up, ((tokens - 1) * ld_up + width) * es))
+        return QDC_ERR_ALIAS;
+    const bool fast = aligned16(out) && aligned16(gate) && aligned16(up) &&
+                      (ld_gate * es) % 16 == 0 && (ld_up * es) % 16 == 0 &&
+                      (ld_out * es) % 16 == 0;
+    if (dtype == QDC_BF16)
+        return launch<bf16_t>(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, fast, stream);
+    return launch<float>(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, fast, stream);
+}

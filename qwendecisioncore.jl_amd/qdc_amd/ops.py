@@ -1,0 +1,274 @@
+"""Device operators of the fused row kernels, on PyTorch-ROCm tensors.
+
+Names and argument meanings follow the reference's operator interface for this
+path (the generic functions the AMDGPU extension overrides):
+
+==========================  ====================================================
+``native_gather``           ``src/backbone.jl:55``; AMDGPU ``ext/amdgpu_workspace.jl:219-236``
+``native_rms``              ``src/backbone.jl:200-204``; AMDGPU ``ext/amdgpu_workspace.jl:130-149``
+``native_residual_rms``     ``src/backbone.jl:347-350``; AMDGPU ``ext/amdgpu_workspace.jl:157-166``
+``prepare_heads``           q/k norm + RoPE of ``full_attention`` (``src/backbone.jl:226-235``;
+                            AMDGPU ``prepare_head_kernel!`` ``ext/amdgpu_attention.jl:1-43``)
+``native_gated_rms``        ``src/backbone.jl:339-341``; AMDGPU ``ext/amdgpu_delta.jl:181-184``
+``native_mlp_gate``         ``native_mlp_gate!`` ``src/backbone.jl:352-355``; AMDGPU
+                            ``mlp_gate_kernel!`` ``ext/amdgpu_mlp.jl:63-75``
+==========================  ====================================================
+
+Tensors are row-major ``[rows, width]`` (the reference's column-major
+``(width, rows)``).  Every call enqueues one kernel of ``libqdc_hip.so`` on the
+tensor device's current PyTorch stream; torch supplies device memory and the
+stream only.  dtype is float32 or bfloat16 (fp32 arithmetic either way).
+Argument errors raise ``ValueError`` before anything is enqueued, as the
+reference raises ``ArgumentError`` / ``DimensionMismatch``.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+_DTYPES = {torch.float32: _lib.QDC_F32, torch.bfloat16: _lib.QDC_BF16}
+
+
+def _dtype_code(*tensors) -> int:
+    dt = tensors[0].dtype
+    for t in tensors:
+        if t.dtype != dt:
+            raise ValueError(f"dtype mismatch: {dt} vs {t.dtype}")
+    if dt not in _DTYPES:
+        raise ValueError(f"unsupported dtype {dt}; expected float32 or bfloat16")
+    return _DTYPES[dt]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _device(*tensors) -> None:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError("device tensors required (torch.device('cuda'))")
+    for t in tensors:
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+
+
+def _rows_view(x: torch.Tensor):
+    """(rows, width, row_stride) of a tensor whose rows are its last axis,
+    contiguous within a row and evenly strided between rows."""
+    if x.dim() == 0:
+        raise ValueError("expected at least one dimension")
+    width = x.shape[-1]
+    if x.numel() == 0:
+        return 0, width, max(width, 1)
+    if x.dim() == 1:
+        return 1, width, width
+    if width > 1 and x.stride(-1) != 1:
+        raise ValueError("rows must be contiguous in their last axis")
+    flat = x.reshape(-1, width) if not x.is_contiguous() else x.view(-1, width)
+    if flat.data_ptr() != x.data_ptr():
+        raise ValueError("rows must be evenly strided (a view, not a copy)")
+    return flat.shape[0], width, flat.stride(0) if flat.shape[0] > 1 else width
+
+
+# ------------------------------------------------------------------ gather --
+def native_gather(embedding: torch.Tensor, ids, out: torch.Tensor | None = None,
+                  out_dtype: torch.dtype | None = None,
+                  error_flag: torch.Tensor | None = None) -> torch.Tensor:
+    """``hidden[t, :] = embedding[ids[t], :]`` (0-based ids), bit-exact.
+
+    ``embedding`` is the ``[vocab, hidden]`` table.  Host ids (a sequence or numpy
+    array) are range-checked first (``src/backbone.jl:417-418``) and uploaded as
+    int32, as the reference AMDGPU path does; a device int32 tensor is used as is
+    (then an out-of-range id writes a zero row and sets ``error_flag``)."""
+    _device(embedding)
+    vocab, hidden = embedding.shape
+    if isinstance(ids, torch.Tensor) and ids.device.type == "cuda":
+        if ids.dtype != torch.int32 or not ids.is_contiguous():
+            raise ValueError("device ids must be a contiguous int32 tensor")
+        dev_ids = ids
+    else:
+        host = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))
+        check(lib().qdc_check_ids(host.ctypes.data, host.size, vocab), "native_gather")
+        dev_ids = torch.from_numpy(host.astype(np.int32)).to(embedding.device, non_blocking=False)
+    n = dev_ids.numel()
+    out_dtype = out_dtype or embedding.dtype
+    if out is None:
+        out = torch.empty((n, hidden), dtype=out_dtype, device=embedding.device)
+    if out.shape != (n, hidden) or not out.is_contiguous() or out.dtype != out_dtype:
+        raise ValueError("out must be a contiguous [n_ids, hidden] tensor of out_dtype")
+    if not embedding.is_contiguous():
+        raise ValueError("embedding must be contiguous")
+    flag = 0
+    if error_flag is not None:
+        _device(error_flag)
+        if error_flag.dtype != torch.int32:
+            raise ValueError("error_flag must be int32")
+        flag = error_flag.data_ptr()
+    check(lib().qdc_embedding_gather(out.data_ptr(), _DTYPES[out_dtype], embedding.data_ptr(),
+                                     _dtype_code(embedding), dev_ids.data_ptr(), n, vocab, hidden,
+                                     flag, _stream(embedding)), "native_gather")
+    return out
+
+
+# ------------------------------------------------------------------ norms ---
+def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool = True,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm over the last axis: ``(x*s)*(1+w)`` (centred) or ``(x*s)*w``."""
+    _device(x, weight)
+    code = _dtype_code(x, weight)
+    rows, width, ld_x = _rows_view(x)
+    if weight.numel() != width or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous vector of the row width")
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if out.shape != x.shape:
+        raise ValueError("out must have the shape of x")
+    orows, _, ld_out = _rows_view(out)
+    check(lib().qdc_rmsnorm(out.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, width, ld_x,
+                            ld_out, eps, int(bool(centered)), code, _stream(x)), "native_rms")
+    return out
+
+
+def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tensor, eps: float,
+                        residual: torch.Tensor | None = None,
+                        out: torch.Tensor | None = None):
+    """``residual = x + mixed``; returns ``(residual, rms(residual))`` in one pass."""
+    _device(x, mixed, weight)
+    code = _dtype_code(x, mixed, weight)
+    if x.shape != mixed.shape or not x.is_contiguous() or not mixed.is_contiguous():
+        raise ValueError("x and mixed must be contiguous tensors of one shape")
+    width = x.shape[-1]
+    rows = x.numel() // width if width else 0
+    if weight.numel() != width:
+        raise ValueError("weight must be a vector of the row width")
+    residual = torch.empty_like(x) if residual is None else residual
+    out = torch.empty_like(x) if out is None else out
+    for t in (residual, out):
+        if t.shape != x.shape or not t.is_contiguous() or t.dtype != x.dtype:
+            raise ValueError("residual/out must be contiguous tensors like x")
+    check(lib().qdc_residual_rmsnorm(residual.data_ptr(), out.data_ptr(), x.data_ptr(),
+                                     mixed.data_ptr(), weight.data_ptr(), rows, width, eps, code,
+                                     _stream(x)), "native_residual_rms")
+    return residual, out
+
+
+def native_gated_rms(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """``((x*s)*w)*silu(z)`` per ``[tokens, heads, width]`` row, not centred.
+
+    ``z`` may be a strided view (heads contiguous inside each token), e.g. the
+    z block of a packed projection."""
+    _device(x, z, weight)
+    code = _dtype_code(x, z, weight)
+    if x.dim() != 3 or z.shape != x.shape:
+        raise ValueError("x and z must be [tokens, heads, width]")
+    tokens, heads, width = x.shape
+    for t in (x, z):
+        if t.stride(2) != 1 or (heads > 1 and t.stride(1) != width):
+            raise ValueError("heads must be contiguous within a token")
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if out.shape != x.shape or out.stride(2) != 1 or (heads > 1 and out.stride(1) != width):
+        raise ValueError("out must be [tokens, heads, width] with contiguous heads")
+    tok = lambda t: t.stride(0) if tokens > 1 else heads * width  # noqa: E731
+    check(lib().qdc_gated_rmsnorm(out.data_ptr(), x.data_ptr(), z.data_ptr(), weight.data_ptr(),
+                                  tokens, heads, width, tok(x), tok(z), tok(out), eps, code,
+                                  _stream(x)), "native_gated_rms")
+    return out
+
+
+# ------------------------------------------------------------------- RoPE ---
+def rope_tables(n_pos: int, rotary_dim: int, theta: float, device) -> tuple:
+    """fp32 ``[n_pos, rotary_dim//2]`` cos/sin tables built on the host the way
+    the reference CPU path builds them (``src/backbone_cpu.jl:90-111``), then
+    copied to ``device``."""
+    half = rotary_dim // 2
+    cos = np.empty((n_pos, half), np.float32)
+    sin = np.empty((n_pos, half), np.float32)
+    check(lib().qdc_rope_tables(cos.ctypes.data, sin.ctypes.data, n_pos, rotary_dim, theta),
+          "rope_tables")
+    return (torch.from_numpy(cos).to(device), torch.from_numpy(sin).to(device))
+
+
+def prepare_heads(q: torch.Tensor | None, k: torch.Tensor | None, q_norm, k_norm, tables,
+                  rotary_dim: int, eps: float, seq_len: int | None = None, pos_offset: int = 0,
+                  q_out: torch.Tensor | None = None, k_out: torch.Tensor | None = None):
+    """Per-head zero-centred RMSNorm + half-split partial RoPE of Q and K heads.
+
+    ``q`` ``[tokens, heads, head_dim]`` and ``k`` ``[tokens, kv_heads, head_dim]``
+    are (possibly strided) views: ``qgate.view(T, H, 2*hd)[:, :, :hd]`` reads q
+    straight out of the q||gate projection.  Token ``t`` uses position
+    ``pos_offset + t % seq_len``.  Returns ``(q_out, k_out)`` (contiguous unless
+    given)."""
+    ref = q if q is not None else k
+    if ref is None:
+        raise ValueError("q or k required")
+    tokens, _, head_dim = ref.shape
+    seq_len = max(tokens, 1) if seq_len is None else seq_len
+    cos, sin = tables if rotary_dim else (None, None)
+
+    def side(x, norm, out):
+        if x is None:
+            return None, None, 0, (0, 0, 0, 0)
+        _device(x, norm)
+        if x.dim() != 3 or x.shape[0] != tokens or x.shape[2] != head_dim or x.stride(2) != 1:
+            raise ValueError("q/k must be [tokens, heads, head_dim] with contiguous rows")
+        if out is None:
+            out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        if out.shape != x.shape or out.stride(2) != 1:
+            raise ValueError("q_out/k_out must match q/k")
+        return x, out, x.shape[1], (x.stride(0), x.stride(1), out.stride(0), out.stride(1))
+
+    qi, qo, heads, qs = side(q, q_norm, q_out)
+    ki, ko, kv_heads, ks = side(k, k_norm, k_out)
+    code = _dtype_code(*[t for t in (qi, ki, q_norm if qi is not None else None,
+                                     k_norm if ki is not None else None) if t is not None])
+    ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+    check(lib().qdc_qk_norm_rope(ptr(qo), ptr(ko), ptr(qi), ptr(ki),
+                                 ptr(q_norm if qi is not None else None),
+                                 ptr(k_norm if ki is not None else None),
+                                 ptr(cos) if rotary_dim else 0, ptr(sin) if rotary_dim else 0,
+                                 tokens, heads, kv_heads, head_dim, rotary_dim, seq_len,
+                                 pos_offset, cos.shape[0] if rotary_dim else 0, *qs, *ks, eps,
+                                 code, _stream(ref)), "prepare_heads")
+    return qo, ko
+
+
+# ----------------------------------------------------------------- SwiGLU ---
+def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate) * up`` on ``[tokens, width]`` views (contiguous rows).
+
+    ``native_mlp_gate!`` writes into ``gate``; here ``out=gate`` does the same
+    (allowed when the strides agree).  For the packed gate||up GEMM output pass
+    ``packed[:, :I]`` and ``packed[:, I:]``."""
+    _device(gate, up)
+    code = _dtype_code(gate, up)
+    if gate.dim() != 2 or up.shape != gate.shape:
+        raise ValueError("gate and up must be [tokens, width]")
+    tokens, width = gate.shape
+    for t in (gate, up):
+        if width > 1 and t.stride(1) != 1:
+            raise ValueError("rows must be contiguous")
+    if out is None:
+        out = torch.empty((tokens, width), dtype=gate.dtype, device=gate.device)
+    if out.shape != gate.shape or (width > 1 and out.stride(1) != 1):
+        raise ValueError("out must be [tokens, width] with contiguous rows")
+    ld = lambda t: t.stride(0) if tokens > 1 else width  # noqa: E731
+    check(lib().qdc_swiglu(out.data_ptr(), gate.data_ptr(), up.data_ptr(), tokens, width,
+                           ld(gate), ld(up), ld(out), code, _stream(gate)), "native_mlp_gate")
+    return out
+
+
+def check_ids(ids: Sequence[int], vocab: int) -> None:
+    """Host id check of ``check_sequence`` (``src/backbone.jl:417-418``)."""
+    host = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))
+    status = lib().qdc_check_ids(host.ctypes.data, host.size, vocab)
+    if status == -4:
+        raise ValueError("Token ID is outside the vocabulary.")
+    check(status, "check_ids")

@@ -1,0 +1,100 @@
+"""Backbone weights as a name -> array dict, keyed like the checkpoint with the
+``language_model.`` prefix removed and stored as in the file (PyTorch
+``[out, in]``, i.e. the reference's Julia ``(in, out)`` in the same memory).
+
+``read_checkpoint`` follows ``read_native_weights`` (``src/safetensors.jl:3-35``)
+and the name canonicalisation of ``QwenBackbone`` (``src/backbone.jl:107-134``);
+``random_weights`` builds the synthetic random-init backbones.
+"""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+
+from .config import BackboneConfig
+
+
+def layer_shapes(cfg: BackboneConfig, index: int) -> dict:
+    """Tensor shapes of one layer, checkpoint layout."""
+    p = f"layers.{index}."
+    H, I = cfg.hidden, cfg.intermediate
+    shapes = {
+        p + "input_layernorm.weight": (H,),
+        p + "post_attention_layernorm.weight": (H,),
+        p + "mlp.gate_proj.weight": (I, H),
+        p + "mlp.up_proj.weight": (I, H),
+        p + "mlp.down_proj.weight": (H, I),
+    }
+    kind = cfg.layer_types[index]
+    if kind == "full_attention":
+        hd = cfg.head_dim
+        shapes.update({
+            p + "self_attn.q_proj.weight": (2 * hd * cfg.heads, H),
+            p + "self_attn.k_proj.weight": (hd * cfg.kv_heads, H),
+            p + "self_attn.v_proj.weight": (hd * cfg.kv_heads, H),
+            p + "self_attn.o_proj.weight": (H, hd * cfg.heads),
+            p + "self_attn.q_norm.weight": (hd,),
+            p + "self_attn.k_norm.weight": (hd,),
+        })
+    elif kind == "linear_attention":
+        kw = cfg.key_dim * cfg.key_heads
+        vw = cfg.value_dim * cfg.value_heads
+        shapes.update({
+            p + "linear_attn.in_proj_qkv.weight": (2 * kw + vw, H),
+            p + "linear_attn.in_proj_z.weight": (vw, H),
+            p + "linear_attn.in_proj_a.weight": (cfg.value_heads, H),
+            p + "linear_attn.in_proj_b.weight": (cfg.value_heads, H),
+            p + "linear_attn.conv1d.weight": (2 * kw + vw, 1, cfg.conv_kernel),
+            p + "linear_attn.A_log": (cfg.value_heads,),
+            p + "linear_attn.dt_bias": (cfg.value_heads,),
+            p + "linear_attn.norm.weight": (cfg.value_dim,),
+            p + "linear_attn.out_proj.weight": (H, vw),
+        })
+    else:
+        raise ValueError(f"Unsupported layer type {kind}.")
+    return shapes
+
+
+def all_shapes(cfg: BackboneConfig) -> dict:
+    shapes = {"embed_tokens.weight": (cfg.vocab, cfg.hidden)}
+    for i in range(len(cfg.layer_types)):
+        shapes.update(layer_shapes(cfg, i))
+    shapes["norm.weight"] = (cfg.hidden,)
+    return shapes
+
+
+def random_weights(cfg: BackboneConfig, seed: int = 0, std: float = 0.02) -> dict:
+    """Every tensor ~ N(0, std) in fp32 from ``numpy.random.default_rng(seed)``,
+    drawn in the order of :func:`all_shapes` (deterministic across machines)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in all_shapes(cfg).items():
+        out[name] = (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+    return out
+
+
+def read_checkpoint(directory: str) -> dict:
+    """Load every ``language_model.*`` tensor of a local safetensors checkpoint
+    (single file or sharded index) widened to fp32 (``src/safetensors.jl:28-30``)."""
+    from safetensors.numpy import load_file  # safe loader: no code from the file is run
+
+    single = os.path.join(directory, "model.safetensors")
+    if os.path.isfile(single):
+        files = ["model.safetensors"]
+    else:
+        with open(os.path.join(directory, "model.safetensors.index.json")) as f:
+            files = sorted(set(json.load(f)["weight_map"].values()))
+    out = {}
+    for fname in files:
+        if os.path.isabs(fname) or ".." in fname.split("/"):
+            raise ValueError(f"Unsafe shard path {fname}.")
+        for name, value in load_file(os.path.join(directory, fname)).items():
+            at = name.find("language_model.")
+            if at < 0:
+                continue
+            if value.dtype == np.uint16:  # raw bf16 bits
+                value = (value.astype(np.uint32) << 16).view(np.float32)
+            out[name[at + len("language_model."):]] = np.asarray(value, dtype=np.float32)
+    return out

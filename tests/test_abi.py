@@ -1,0 +1,194 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+declared in include/qdc_hip.h, and rejects bad arguments on the host (with the
+documented status) before anything would be enqueued.  Only calls that fail
+validation are made, so no kernel is ever launched here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from oracle import qdc_oracle as O
+from qdc_amd import _lib
+
+HEADER = os.path.join(ROOT, "include", "qdc_hip.h")
+F32, BF16 = _lib.QDC_F32, _lib.QDC_BF16
+NULL_S = None
+FAKE = 0x10000  # a non-null, 16-byte aligned address never dereferenced by validation
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qdc_\w+)\s*\(", text, re.M)))
+
+
+def test_exports_match_header():
+    lib = _lib.lib()
+    names = declared()
+    assert len(names) == 10, names
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert set(_lib.SIGNATURES) == set(names)
+    assert _lib.version().startswith("qdc_hip ")
+
+
+def test_status_strings():
+    for code, name in _lib.STATUS.items():
+        assert _lib.status_string(code)
+    assert "NULL" in _lib.status_string(-1)
+
+
+def test_rope_tables_match_oracle_bitwise():
+    for n_pos, rd, theta in ((2048, 64, 1e7), (128, 16, 1e7), (65, 4, 1e4), (7, 2, 10.0)):
+        cos = np.empty((n_pos, rd // 2), np.float32)
+        sin = np.empty((n_pos, rd // 2), np.float32)
+        assert _lib.lib().qdc_rope_tables(cos.ctypes.data, sin.ctypes.data, n_pos, rd, theta) == 0
+        oc, os_ = O.rope_tables(n_pos, rd, theta)
+        assert np.array_equal(cos, oc) and np.array_equal(sin, os_)
+    lib = _lib.lib()
+    assert lib.qdc_rope_tables(None, None, 4, 3, 1e4) == -2
+    assert lib.qdc_rope_tables(None, None, 4, 4, 1e4) == -1
+    assert lib.qdc_rope_tables(None, None, 0, 4, 1e4) == 0
+
+
+def test_check_ids():
+    lib = _lib.lib()
+    ids = np.array([0, 5, 4095], np.int64)
+    assert lib.qdc_check_ids(ids.ctypes.data, 3, 4096) == 0
+    assert lib.qdc_check_ids(ids.ctypes.data, 3, 4095) == -4
+    neg = np.array([3, -1], np.int64)
+    assert lib.qdc_check_ids(neg.ctypes.data, 2, 10) == -4
+    assert lib.qdc_check_ids(None, 0, 10) == 0
+    assert lib.qdc_check_ids(None, 2, 10) == -1
+
+
+def test_rmsnorm_validation():
+    lib = _lib.lib()
+    rms = lambda *a: lib.qdc_rmsnorm(*a, None)  # noqa: E731
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, 7) == -3
+    assert rms(FAKE, FAKE, FAKE, -1, 8, 8, 8, 1e-6, 1, F32) == -2
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 4, 8, 1e-6, 1, F32) == -2  # ld < width
+    assert rms(None, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32) == -1
+    assert rms(FAKE, FAKE, None, 4, 8, 8, 8, 1e-6, 1, BF16) == -1
+    assert rms(None, None, None, 0, 8, 8, 8, 1e-6, 1, F32) == 0  # nothing to do
+    assert rms(FAKE + 16, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32) == -5  # partial overlap
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 16, 1e-6, 1, F32) == -5  # in place, other stride
+
+
+def test_residual_validation():
+    lib = _lib.lib()
+    f = lambda *a: lib.qdc_residual_rmsnorm(*a, None)  # noqa: E731
+    A, B, C, D, W = FAKE, FAKE * 2, FAKE * 3, FAKE * 4, FAKE * 5
+    assert f(A, B, C, D, W, 4, 8, 1e-6, 9) == -3
+    assert f(A, B, C, None, W, 4, 8, 1e-6, F32) == -1
+    assert f(A, A, C, D, W, 4, 8, 1e-6, F32) == -5  # residual and out coincide
+    assert f(A, B, A + 4, D, W, 4, 8, 1e-6, F32) == -5  # residual overlaps x partially
+    assert f(A, B, C, D, W, 0, 8, 1e-6, F32) == 0
+
+
+def test_gated_validation():
+    lib = _lib.lib()
+    f = lambda *a: lib.qdc_gated_rmsnorm(*a, None)  # noqa: E731
+    A, X, Z, W = FAKE, FAKE * 2, FAKE * 3, FAKE * 4
+    assert f(A, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, 3) == -3
+    assert f(A, X, Z, W, 4, 2, 8, 8, 16, 16, 1e-6, F32) == -2  # token stride < heads*width
+    assert f(A, X, None, W, 4, 2, 8, 16, 16, 16, 1e-6, F32) == -1
+    assert f(Z, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, F32) == -5  # out on z
+    assert f(A, X, Z, W, 0, 2, 8, 16, 16, 16, 1e-6, F32) == 0
+
+
+def test_swiglu_validation():
+    lib = _lib.lib()
+    f = lambda *a: lib.qdc_swiglu(*a, None)  # noqa: E731
+    O_, G, U = FAKE, FAKE * 2, FAKE * 3
+    assert f(O_, G, U, 4, 8, 8, 8, 8, 5) == -3
+    assert f(O_, G, U, 4, 8, 4, 8, 8, F32) == -2
+    assert f(O_, None, U, 4, 8, 8, 8, 8, F32) == -1
+    assert f(G + 4, G, U, 4, 8, 8, 8, 8, F32) == -5
+    assert f(G, G, U, 4, 8, 8, 8, 16, F32) == -5  # in place with another stride
+    assert f(O_, G, U, 4, 0, 8, 8, 8, F32) == 0
+
+
+def test_gather_validation():
+    lib = _lib.lib()
+    f = lambda *a: lib.qdc_embedding_gather(*a, None, None)  # noqa: E731
+    O_, T, I = FAKE, FAKE * 2, FAKE * 3
+    assert f(O_, BF16, T, F32, I, 4, 16, 8) == -3  # f32 -> bf16 is not a copy
+    assert f(O_, F32, T, 9, I, 4, 16, 8) == -3
+    assert f(O_, F32, T, F32, None, 4, 16, 8) == -1
+    assert f(O_, F32, T, F32, I, -4, 16, 8) == -2
+    assert f(O_, F32, T, F32, I, 4, 0, 8) == -4
+    assert f(T + 64, F32, T, F32, I, 4, 16, 8) == -5  # output inside the table
+    assert f(O_, F32, T, F32, I, 0, 16, 8) == 0
+
+
+def test_qk_norm_rope_validation():
+    lib = _lib.lib()
+    Q, K, QI, KI, QN, KN, C, S = (FAKE * i for i in range(1, 9))
+
+    def f(tokens=8, heads=2, kv=1, hd=16, rd=8, seq=8, off=0, tl=8,
+          qs=(64, 32, 32, 16), ks=(16, 16, 16, 16), dtype=F32, q=Q, k=K, qi=QI, ki=KI, c=C):
+        return lib.qdc_qk_norm_rope(q, k, qi, ki, QN, KN, c, S, tokens, heads, kv, hd, rd, seq,
+                                    off, tl, *qs, *ks, 1e-6, dtype, None)
+    assert f(dtype=4) == -3
+    assert f(rd=7) == -2
+    assert f(rd=32) == -2  # rotary > head_dim
+    assert f(seq=0) == -2
+    assert f(tl=7) == -4  # position 7 is outside a 7-row table
+    assert f(off=1) == -4
+    assert f(c=None) == -1
+    assert f(qs=(64, 8, 32, 16)) == -2  # head stride < head_dim
+    assert f(q=KI) == -5  # q output on the k input
+    assert f(k=Q + 32) == -5  # the two outputs overlap
+    assert f(tokens=0) == 0
+
+
+@pytest.mark.timeout(300)
+def test_fastdiv_exhaustive(tmp_path):
+    """The multiply-high division used for row/token indexing, compiled for the
+    host from the same header, against integer division."""
+    src = tmp_path / "fastdiv_check.cpp"
+    src.write_text(r'''
+#include "qdc_common.hpp"
+#include <cstdio>
+#include <random>
+int main() {
+    std::mt19937_64 rng(1);
+    uint32_t divisors[4096]; int nd = 0;
+    for (uint32_t d = 1; d <= 2100; ++d) divisors[nd++] = d;
+    for (int k = 2; k <= 31; ++k) for (int e = -2; e <= 2; ++e) {
+        long long d = (1ll << k) + e; if (d >= 1 && d <= (1ll << 31)) divisors[nd++] = (uint32_t)d; }
+    const uint32_t extra[] = {448, 3584, 16384, 81920, 262144, 248320, 2147483647u};
+    for (uint32_t d : extra) divisors[nd++] = d;
+    long long checked = 0;
+    for (int i = 0; i < nd; ++i) {
+        const uint32_t d = divisors[i];
+        const qdc::FastDiv f = qdc::make_fastdiv(d);
+        auto one = [&](uint32_t n) {
+            if (n > 0x7fffffffu) return true;
+            ++checked;
+            return qdc::fastdiv(n, f) == n / d;
+        };
+        const uint32_t edge[] = {0u, 1u, d - 1, d, d + 1, 2 * d - 1, 2 * d, 0x7fffffffu,
+                                 0x7fffffffu - 1, (0x7fffffffu / d) * d, (0x7fffffffu / d) * d - 1};
+        for (uint32_t n : edge) if (!one(n)) { printf("FAIL d=%u n=%u\n", d, n); return 1; }
+        for (int r = 0; r < 20000; ++r) {
+            const uint32_t n = (uint32_t)(rng() & 0x7fffffffu);
+            if (!one(n)) { printf("FAIL d=%u n=%u\n", d, n); return 1; }
+        }
+    }
+    printf("ok %lld\n", checked);
+    return 0;
+}
+''')
+    exe = tmp_path / "fastdiv_check"
+    inc = os.path.join(ROOT, "qwendecisioncore.jl_amd", "csrc")
+    subprocess.run(["/opt/rocm/bin/hipcc", "-O2", "-std=c++17", f"-I{inc}",
+                    f"-I{os.path.join(ROOT, 'include')}", str(src), "-o", str(exe)],
+                   check=True, capture_output=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=240)
+    assert run.returncode == 0 and run.stdout.startswith("ok"), run.stdout

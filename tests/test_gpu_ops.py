@@ -1,0 +1,282 @@
+"""GPU parity of every fused row kernel against the CPU oracle, through the
+C ABI (qdc_amd.ops -> libqdc_hip.so).
+
+Bars: gather bit-exact; everything else normwise relative error (Julia
+isapprox semantics) <= 1e-5 in fp32 and <= 1e-2 in bf16, where bf16 runs use
+bf16-representable inputs and the oracle computes in fp32 on the same values.
+Shapes cover the benchmark configurations at full size, the reference's small
+and ragged cases, strided / packed layouts, in-place calls and the general
+(unaligned / odd-width) kernels.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import normwise
+from oracle import qdc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2}
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from qdc_amd import ops  # noqa: F401  (fails loudly if the library is missing)
+    yield
+    torch.cuda.synchronize()
+
+
+def host(shape, seed, scale=1.0, dtype=torch.float32):
+    """Seeded N(0, scale) fp32 values, made bf16-representable for bf16 runs."""
+    x = (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(scale))
+    return O.round_bf16(x) if dtype == torch.bfloat16 else x
+
+
+def dev(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV).to(dtype)
+
+
+def back(t):
+    return t.float().cpu().numpy()
+
+
+def report(name, got, exp, dtype):
+    err = normwise(got, exp)
+    print(f"{name}: normwise {err:.3e} maxabs {np.abs(got - exp).max() if got.size else 0:.3e}",
+          flush=True)
+    assert err <= TOL[dtype], (name, err)
+
+
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+# ------------------------------------------------------------------ RMSNorm --
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,width", [(8192, 1024), (81920, 256), (17, 7), (1, 1), (3, 1000),
+                                        (33, 2560), (5, 4096), (257, 128), (2, 8), (9, 64)])
+@pytest.mark.parametrize("centered", [True, False])
+def test_rmsnorm(dtype, rows, width, centered):
+    from qdc_amd import ops
+    x = host((rows, width), 1, 1.0, dtype)
+    w = host((width,), 2, 0.02, dtype)
+    got = back(ops.native_rms(dev(x, dtype), dev(w, dtype), 1e-6, centered=centered))
+    report(f"rms {rows}x{width} {dtype} c={centered}", got, O.rms(x, w, 1e-6, centered), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rmsnorm_strided_misaligned_inplace_empty(dtype):
+    from qdc_amd import ops
+    x = host((64, 1040), 3, 1.0, dtype)
+    w = host((1024,), 4, 0.02, dtype)
+    big = dev(x, dtype)
+    # rows of 1024 inside rows of 1040 (aligned stride) and shifted by one element
+    for off in (0, 1):
+        view = big[:, off:off + 1024]
+        got = back(ops.native_rms(view, dev(w, dtype), 1e-6))
+        report(f"rms strided off={off}", got, O.rms(x[:, off:off + 1024], w, 1e-6), dtype)
+    t = dev(x[:, :1024], dtype).contiguous()
+    ops.native_rms(t, dev(w, dtype), 1e-6, out=t)
+    report("rms in place", back(t), O.rms(x[:, :1024], w, 1e-6), dtype)
+    empty = torch.empty((0, 1024), dtype=dtype, device=DEV)
+    assert ops.native_rms(empty, dev(w, dtype), 1e-6).shape == (0, 1024)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,width", [(8192, 1024), (16384, 1024), (17, 7), (65, 256), (3, 3000)])
+def test_residual_rmsnorm(dtype, rows, width):
+    from qdc_amd import ops
+    x = host((rows, width), 5, 1.0, dtype)
+    m = host((rows, width), 6, 1.0, dtype)
+    w = host((width,), 7, 0.02, dtype)
+    res, out = ops.native_residual_rms(dev(x, dtype), dev(m, dtype), dev(w, dtype), 1e-6)
+    # the residual is x + mixed rounded once; the norm uses the unrounded fp32 sum
+    exp_res, exp_out = O.residual_rms(x, m, w, 1e-6)
+    if dtype == torch.bfloat16:
+        exp_res = O.round_bf16(exp_res)
+    report(f"residual {rows}x{width}", back(res), exp_res, dtype)
+    report(f"residual-norm {rows}x{width}", back(out), exp_out, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("width", [1024, 1000])
+def test_residual_rmsnorm_in_place(dtype, width):
+    from qdc_amd import ops
+    x = host((37, width), 8, 1.0, dtype)
+    m = host((37, width), 9, 1.0, dtype)
+    w = host((width,), 10, 0.02, dtype)
+    exp_res, exp_out = O.residual_rms(x, m, w, 1e-6)
+    if dtype == torch.bfloat16:
+        exp_res = O.round_bf16(exp_res)
+    xt, mt = dev(x, dtype), dev(m, dtype)
+    # residual over x, normalised output over mixed (the reference reuses buffers this way)
+    ops.native_residual_rms(xt, mt, dev(w, dtype), 1e-6, residual=xt, out=mt)
+    report("residual in place", back(xt), exp_res, dtype)
+    report("residual-norm in place", back(mt), exp_out, dtype)
+
+
+# ------------------------------------------------------- q/k norm + RoPE ----
+QK_CASES = [
+    # tokens, heads, kv, head_dim, rotary, seq_len, theta
+    (8192, 8, 2, 256, 64, 2048, 1e7),   # Qwen3.5-0.8B-like, 4 sequences of 2048
+    (128, 4, 1, 64, 16, 128, 1e7),      # 2-layer plumbing backbone
+    (65, 2, 1, 4, 4, 65, 1e4),          # reference fixture shape (general kernel)
+    (40, 3, 1, 64, 0, 40, 1e7),         # no rotation
+    (33, 2, 2, 128, 128, 11, 1e4),      # full rotary, sequences of 11
+    (19, 2, 1, 96, 24, 19, 1e6),        # 12-wide halves: general kernel
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", QK_CASES)
+def test_qk_norm_rope(dtype, case):
+    from qdc_amd import ops
+    T, H, KV, hd, rd, seq, theta = case
+    qgate = host((T, H, 2 * hd), 11, 1.0, dtype)   # interleaved q||gate projection
+    k = host((T, KV, hd), 12, 1.0, dtype)
+    qn = host((hd,), 13, 0.02, dtype)
+    kn = host((hd,), 14, 0.02, dtype)
+    tables = ops.rope_tables(seq, rd, theta, DEV)
+    qg = dev(qgate, dtype)
+    q_view = qg[:, :, :hd]
+    qo, ko = ops.prepare_heads(q_view, dev(k, dtype), dev(qn, dtype), dev(kn, dtype), tables, rd,
+                               1e-6, seq_len=seq)
+    cos, sin = O.rope_tables(seq, rd, theta)
+    report(f"q {case}", back(qo), O.qk_norm_rope(qgate[:, :, :hd], qn, cos, sin, rd, 1e-6, seq), dtype)
+    report(f"k {case}", back(ko), O.qk_norm_rope(k, kn, cos, sin, rd, 1e-6, seq), dtype)
+    # the gate half of the projection is untouched
+    assert torch.equal(qg[:, :, hd:], dev(qgate, dtype)[:, :, hd:])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_qk_norm_rope_offset_inplace_one_side(dtype):
+    from qdc_amd import ops
+    T, H, hd, rd = 48, 4, 256, 64
+    q = host((T, H, hd), 15, 2.0, dtype)
+    qn = host((hd,), 16, 0.02, dtype)
+    tables = ops.rope_tables(200, rd, 1e7, DEV)
+    cos, sin = O.rope_tables(200, rd, 1e7)
+    qt = dev(q, dtype)
+    # Q only, positions 100.., in place
+    ops.prepare_heads(qt, None, dev(qn, dtype), None, tables, rd, 1e-6, seq_len=T, pos_offset=100,
+                      q_out=qt)
+    report("q offset in place", back(qt), O.qk_norm_rope(q, qn, cos, sin, rd, 1e-6, T, 100), dtype)
+    with pytest.raises(ValueError):
+        ops.prepare_heads(qt, None, dev(qn, dtype), None, tables, rd, 1e-6, seq_len=T,
+                          pos_offset=160)
+
+
+# ----------------------------------------------------------- gated norm -----
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("tokens,heads,width", [(16384, 16, 128), (128, 4, 128), (17, 4, 128),
+                                                (9, 3, 100), (5, 2, 8)])
+def test_gated_rmsnorm(dtype, tokens, heads, width):
+    from qdc_amd import ops
+    x = host((tokens, heads, width), 17, 1.0, dtype)
+    z = host((tokens, heads, width), 18, 1.0, dtype)
+    w = host((width,), 19, 0.02, dtype)
+    got = back(ops.native_gated_rms(dev(x, dtype), dev(z, dtype), dev(w, dtype), 1e-6))
+    report(f"gated {tokens}x{heads}x{width}", got, O.gated_rms(x, z, w, 1e-6), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gated_rmsnorm_z_in_packed_projection(dtype):
+    """z read straight from the packed [qkv | z | a | b] projection."""
+    from qdc_amd import ops
+    T, H, W, qkv = 257, 16, 128, 6144
+    proj = host((T, qkv + H * W + 2 * H), 20, 1.0, dtype)
+    x = host((T, H, W), 21, 1.0, dtype)
+    w = host((W,), 22, 1.0, dtype)
+    pt = dev(proj, dtype)
+    z_view = pt[:, qkv:qkv + H * W].view(T, H, W)
+    xt = dev(x, dtype)
+    ops.native_gated_rms(xt, z_view, dev(w, dtype), 1e-6, out=xt)   # in place over x
+    exp = O.gated_rms(x, proj[:, qkv:qkv + H * W].reshape(T, H, W), w, 1e-6)
+    report("gated packed z, in place", back(xt), exp, dtype)
+
+
+# ---------------------------------------------------------------- SwiGLU ----
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("tokens,width", [(16384, 3584), (128, 768), (17, 16), (3, 1001), (1, 8)])
+def test_swiglu(dtype, tokens, width):
+    from qdc_amd import ops
+    g = host((tokens, width), 23, 1.0, dtype)
+    u = host((tokens, width), 24, 1.0, dtype)
+    got = back(ops.native_mlp_gate(dev(g, dtype), dev(u, dtype)))
+    report(f"swiglu {tokens}x{width}", got, O.swiglu(g, u), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_swiglu_packed_inplace_special(dtype):
+    from qdc_amd import ops
+    T, I = 300, 3584
+    packed = host((T, 2 * I), 25, 3.0, dtype)
+    special = np.array([0.0, -0.0, -100.0, 100.0, 1e-30, -1e-30, 80.0, -20.0, 88.0, -88.0, 1e-12,
+                        3.0, np.inf, -np.inf], np.float32)
+    packed[0, :special.size] = special
+    if dtype == torch.bfloat16:
+        packed = O.round_bf16(packed)
+    pt = dev(packed, dtype)
+    got = back(ops.native_mlp_gate(pt[:, :I], pt[:, I:]))
+    exp = O.swiglu(packed[:, :I], packed[:, I:])
+    finite = np.isfinite(exp)
+    report("swiglu packed", np.where(finite, got, 0), np.where(finite, exp, 0), dtype)
+    assert np.array_equal(np.isnan(got), np.isnan(exp)) and np.array_equal(
+        got[np.isinf(exp)], exp[np.isinf(exp)])
+    g = dev(packed[:, :I], dtype).contiguous()
+    ops.native_mlp_gate(g, dev(packed[:, I:], dtype).contiguous(), out=g)  # native_mlp_gate!
+    assert np.array_equal(back(g), got, equal_nan=True)
+
+
+# ---------------------------------------------------------------- gather ----
+@pytest.mark.parametrize("table_dtype,out_dtype", [(torch.bfloat16, torch.bfloat16),
+                                                   (torch.bfloat16, torch.float32),
+                                                   (torch.float32, torch.float32)])
+@pytest.mark.parametrize("vocab,hidden,n", [(248320, 1024, 16384), (4096, 256, 128), (64, 8, 65),
+                                            (100, 12, 33), (50, 1000, 7)])
+def test_gather_bit_exact(table_dtype, out_dtype, vocab, hidden, n):
+    from qdc_amd import ops
+    rng = np.random.default_rng(26)
+    if table_dtype == torch.bfloat16:
+        bits = rng.integers(0, 1 << 16, size=(vocab, hidden), dtype=np.uint16)
+        table = torch.from_numpy(bits.view(np.int16)).to(DEV).view(torch.bfloat16)
+        exp_bits = bits
+    else:
+        vals = rng.standard_normal((vocab, hidden), dtype=np.float32)
+        table = torch.from_numpy(vals).to(DEV)
+        exp_bits = vals.view(np.uint32)
+    ids = rng.integers(0, vocab, size=n)
+    ids[:3] = [0, vocab - 1, 0][:min(3, n)]
+    out = ops.native_gather(table, ids, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    exp = O.gather(exp_bits, ids)
+    if table_dtype == torch.bfloat16 and out_dtype == torch.float32:
+        exp = (exp.astype(np.uint32) << 16)
+        assert np.array_equal(got.view(torch.int32).numpy().view(np.uint32), exp)
+    elif table_dtype == torch.bfloat16:
+        assert np.array_equal(got.view(torch.int16).numpy().view(np.uint16), exp)
+    else:
+        assert np.array_equal(got.view(torch.int32).numpy().view(np.uint32), exp)
+
+
+def test_gather_checks_and_device_ids():
+    from qdc_amd import ops
+    table = torch.arange(64 * 8, dtype=torch.float32, device=DEV).view(64, 8)
+    with pytest.raises(ValueError):
+        ops.native_gather(table, [1, 64])
+    with pytest.raises(ValueError):
+        ops.native_gather(table, [-1])
+    assert ops.native_gather(table, []).shape == (0, 8)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ids = torch.tensor([3, 99, 5, -7], dtype=torch.int32, device=DEV)
+    out = ops.native_gather(table, ids, error_flag=flag)
+    torch.cuda.synchronize()
+    assert flag.item() == 1
+    exp = table.cpu().numpy()
+    got = out.cpu().numpy()
+    assert np.array_equal(got[0], exp[3]) and np.array_equal(got[2], exp[5])
+    assert not got[1].any() and not got[3].any()

@@ -1,0 +1,232 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
+
+Checks, per oracle function:
+  * the reference's own golden data: test/fixtures/native (5 PyTorch cases of
+    reference.json and 21 of cuda_reference.json) end to end at the reference's
+    tolerance (atol = rtol = 2e-5, test/backbone.jl:1-34) -- covers gather, all
+    RMSNorm variants, full-rotary RoPE, gated norm and SwiGLU together;
+  * an independent implementation (transformers' Qwen3.5 modules) for partial
+    RoPE (rotary 16 of 64 and 64 of 256, positions reset per sequence), the
+    norms, SwiGLU with special values and a 2-layer backbone;
+  * the bf16 known-answer tests of test/safetensors.jl:23-25;
+  * closed forms and invariants (exact scale invariance, identity rotations,
+    pair-norm preservation, silu(x) - silu(-x) = x, byte-equal gathers);
+  * planted mistakes: each mutant of the oracle must fail the fixture.
+"""
+import numpy as np
+import pytest
+
+from conftest import isapprox, normwise, ramp
+from oracle import forward
+from oracle import qdc_oracle as O
+
+
+def fixture_logits(fx, cases=None):
+    out = []
+    for name, ids, mask, expected in (cases or fx["cases"]):
+        got = np.stack([fx["readout"] @ forward.backbone_hidden(fx["weights"], fx["cfg"], ids[r],
+                                                                mask[r])[-1]
+                        for r in range(ids.shape[0])])
+        out.append((name, got, expected))
+    return out
+
+
+def test_fixture_end_to_end(native_fixture):
+    assert len(native_fixture["cases"]) == 26
+    for name, got, expected in fixture_logits(native_fixture):
+        assert isapprox(got, expected, 2e-5, 2e-5), (name, normwise(got, expected))
+
+
+def test_fixture_input_validation(native_fixture):
+    W, cfg = native_fixture["weights"], native_fixture["cfg"]
+    for ids, mask in (([1, 2], [1]), ([], []), ([1, 2], [1, 2, 0]), ([64], [1]), ([-1], [1]),
+                      ([1, 2], [1, 2])):
+        with pytest.raises(ValueError):
+            forward.backbone_hidden(W, cfg, ids, mask)
+
+
+MUTANTS = {
+    "rms weight not centred": ("rms", lambda x, w, eps, centered=True:
+                               _np_rms(x, w, eps, not centered)),
+    "rms eps outside sqrt": ("rms", lambda x, w, eps, centered=True:
+                             _np_rms(x, w, 0.0, centered) + 0 * eps),
+    "rope sin sign": ("qk_norm_rope", lambda x, w, c, s, rd, eps, seq_len=None, pos_offset=0:
+                      _orig["qk_norm_rope"](x, w, c, -s, rd, eps, seq_len, pos_offset)),
+    "rope pairs interleaved": ("qk_norm_rope", lambda x, w, c, s, rd, eps, seq_len=None,
+                               pos_offset=0: _np_rope_interleaved(x, w, c, s, rd, eps)),
+    "residual not added": ("residual_rms", lambda x, m, w, eps: (x + m, _np_rms(x, w, eps, True))),
+    "swiglu gate sigmoid only": ("swiglu", lambda g, u: (1 / (1 + np.exp(-g))).astype(np.float32) * u),
+    "gated norm centred": ("gated_rms", lambda x, z, w, eps: _orig["gated_rms"](x, z, w + 1, eps)),
+    "gated norm no silu": ("gated_rms", lambda x, z, w, eps: _np_rms(x, w, eps, False) * z),
+    "gather off by one": ("gather", lambda t, ids: _orig["gather"](t, (np.asarray(ids) + 1) % t.shape[0])),
+}
+_orig = {name: getattr(O, name) for name in ("rms", "qk_norm_rope", "residual_rms", "swiglu",
+                                             "gated_rms", "gather")}
+
+
+def _np_rms(x, w, eps, centered):
+    x = x.astype(np.float32)
+    s = 1 / np.sqrt((x * x).sum(-1, keepdims=True) / np.float32(x.shape[-1]) + np.float32(eps))
+    return ((x * s) * ((1 + w) if centered else w)).astype(np.float32)
+
+
+def _np_rope_interleaved(x, w, c, s, rd, eps):
+    y = _np_rms(x, w, eps, True)
+    T = x.shape[0]
+    for i in range(rd // 2):
+        a, b = y[..., 2 * i].copy(), y[..., 2 * i + 1].copy()
+        ci, si = c[:T, i][:, None], s[:T, i][:, None]
+        y[..., 2 * i], y[..., 2 * i + 1] = a * ci - b * si, b * ci + a * si
+    return y
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_fixture_catches_planted_mistakes(native_fixture, monkeypatch, mutant):
+    name, fn = MUTANTS[mutant]
+    monkeypatch.setattr(O, name, fn)
+    # two cases with masks, holes and 65 tokens are enough to expose each mutant
+    cases = [c for c in native_fixture["cases"] if c[0].startswith(("ref04", "cuda13"))]
+    bad = [n for n, got, exp in fixture_logits(native_fixture, cases)
+           if not isapprox(got, exp, 2e-5, 2e-5)]
+    assert bad, f"planted mistake '{mutant}' went unnoticed"
+
+
+def test_bf16_known_answers():
+    # test/safetensors.jl:23-25
+    assert O.f32_to_bf16(np.float32([1.0, -2.0, 0.0])).tolist() == [0x3F80, 0xC000, 0x0000]
+    # round to nearest, ties to even, on the 16 dropped bits
+    bits = np.array([0x3F808000, 0x3F818000, 0x3F808001, 0x3F807FFF, 0x7F7FFFFF], np.uint32)
+    assert O.f32_to_bf16(bits.view(np.float32)).tolist() == [0x3F80, 0x3F82, 0x3F81, 0x3F80, 0x7F80]
+    # widening is exact: every bf16 pattern round-trips
+    allbits = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    wide = O.bf16_to_f32(allbits)
+    assert np.array_equal(wide.view(np.uint32), allbits.astype(np.uint32) << 16)
+    finite = np.isfinite(wide)
+    assert np.array_equal(O.f32_to_bf16(wide[finite]), allbits[finite])
+
+
+def test_transformers_rms(transformers_golden):
+    for width in (7, 256, 1024):
+        got = O.rms(ramp(np.sin, (17, width)), ramp(np.cos, (width,), 0.1), 1e-6)
+        assert normwise(got, transformers_golden[f"rms/{width}"]) < 1e-6
+
+
+def test_transformers_gated(transformers_golden):
+    got = O.gated_rms(ramp(np.sin, (17, 4, 128)), ramp(np.cos, (17, 4, 128), 3.0),
+                      ramp(np.cos, (128,)), 1e-6)
+    assert normwise(got, transformers_golden["gated/out"]) < 1e-6
+
+
+@pytest.mark.parametrize("tag", ["hd64", "hd256"])
+def test_transformers_partial_rope(transformers_golden, tag):
+    hd, rot, heads, kv, seqs, seq = (int(v) for v in transformers_golden[f"rope/{tag}/meta"])
+    T = seqs * seq
+    cos, sin = O.rope_tables(seq, rot, 1e7)
+    q = O.qk_norm_rope(ramp(np.sin, (T, heads, hd), 2.0), ramp(np.cos, (hd,), 0.05), cos, sin, rot,
+                       1e-6, seq_len=seq)
+    k = O.qk_norm_rope(ramp(np.cos, (T, kv, hd), 2.0), ramp(np.sin, (hd,), 0.05), cos, sin, rot,
+                       1e-6, seq_len=seq)
+    assert normwise(q, transformers_golden[f"rope/{tag}/q"]) < 1e-6
+    assert normwise(k, transformers_golden[f"rope/{tag}/k"]) < 1e-6
+
+
+def test_transformers_swiglu(transformers_golden):
+    gate = transformers_golden["swiglu/gate"]
+    up = ramp(np.cos, (9, 64), 2.0)
+    got = O.swiglu(gate, up)
+    exp = transformers_golden["swiglu/out"]
+    assert normwise(got, exp) < 1e-6
+    # special values of the first row: 0, -0, -100, 100, +-1e-30, 80, -20, +-88, 1e-12, 3
+    np.testing.assert_allclose(got[0, :12], exp[0, :12], rtol=2e-6, atol=1e-37)
+
+
+def test_transformers_plumbing_backbone(transformers_golden):
+    import dataclasses
+    from qdc_amd.config import plumbing_config
+    from qdc_amd.weights import random_weights
+    vocab, T, seed = (int(v) for v in transformers_golden["model/meta"])
+    cfg = dataclasses.replace(plumbing_config(), vocab=vocab)
+    W = random_weights(cfg, seed=seed)
+    got = forward.backbone_hidden(W, cfg.as_dict(), transformers_golden["model/ids"],
+                                  np.ones(T, np.int8))
+    assert normwise(got, transformers_golden["model/hidden"]) < 2e-6
+
+
+def test_gather_bruteforce():
+    rng = np.random.default_rng(0)
+    for dtype in (np.float32, np.uint16):
+        table = rng.integers(0, 1 << 16, size=(37, 24)).astype(dtype)
+        ids = rng.integers(0, 37, size=101)
+        got = O.gather(table, ids)
+        assert got.tobytes() == b"".join(table[i].tobytes() for i in ids)
+    for bad in ([37], [-1], [0, 5, 99]):
+        with pytest.raises(ValueError):
+            O.gather(table, bad)
+    assert O.gather(table, []).shape == (0, 24)
+
+
+def test_rms_closed_forms():
+    # constant rows: s = 1/sqrt(c^2 + eps)
+    c = np.float32(0.75)
+    w = ramp(np.cos, (7,), 0.1)
+    got = O.rms(np.full((3, 7), c, np.float32), w, 1e-6)
+    exp = (c * (np.float32(1) / np.sqrt(c * c + np.float32(1e-6)))) * (np.float32(1) + w)
+    np.testing.assert_allclose(got, np.broadcast_to(exp, (3, 7)), rtol=2e-7)
+    # with eps = 0 scaling by a power of two is exact
+    x = ramp(np.sin, (5, 1024))
+    w = ramp(np.cos, (1024,))
+    assert np.array_equal(O.rms(x, w, 0.0), O.rms(x * np.float32(8), w, 0.0))
+    assert np.array_equal(O.rms(x, w, 0.0, centered=False), O.rms(x / np.float32(4), w, 0.0, False))
+    # widths 1 / 7 / 1024 and n = 0 / 1 / 17, as test/backbone.jl:387-413
+    for width in (1, 7, 1024):
+        for n in (0, 1, 17):
+            x = ramp(np.sin, (n, width))
+            w = ramp(np.cos, (width,))
+            np.testing.assert_allclose(O.rms(x, w, 1e-6), _np_rms(x, w, 1e-6, True), rtol=3e-6,
+                                       atol=1e-7)
+
+
+def test_rope_closed_forms():
+    T, H, hd, rd = 40, 3, 64, 16
+    cos, sin = O.rope_tables(T, rd, 1e7)
+    # freq_0 = 1: column 0 holds cos/sin of the position itself
+    np.testing.assert_array_equal(cos[:, 0], np.cos(np.arange(T, dtype=np.float64)).astype(np.float32))
+    np.testing.assert_array_equal(sin[:, 0], np.sin(np.arange(T, dtype=np.float64)).astype(np.float32))
+    assert np.allclose(cos * cos + sin * sin, 1, atol=1e-6)
+    assert np.array_equal(cos[0], np.ones(rd // 2, np.float32))
+    x = ramp(np.sin, (T, H, hd))
+    w = ramp(np.cos, (hd,), 0.1)
+    normed = O.rms(x, w, 1e-6)
+    # rotary 0 is the plain per-head norm (test/backbone.jl:359); position 0 is identity
+    np.testing.assert_array_equal(O.qk_norm_rope(x, w, cos[:, :0], sin[:, :0], 0, 1e-6), normed)
+    got = O.qk_norm_rope(x, w, cos, sin, rd, 1e-6)
+    np.testing.assert_array_equal(got[0], normed[0])
+    # dims >= rotary pass through, pair norms are preserved
+    np.testing.assert_array_equal(got[..., rd:], normed[..., rd:])
+    h = rd // 2
+    pair = lambda y: y[..., :h] ** 2 + y[..., h:rd] ** 2  # noqa: E731
+    np.testing.assert_allclose(pair(got), pair(normed), rtol=1e-5, atol=1e-7)
+    # against a float64 rotation by the fp32 angle freq_i * pos
+    freq = (np.float32(1) / np.float32(1e7) ** (np.arange(0, rd, 2, dtype=np.float32) / np.float32(rd)))
+    ang = (freq[None, :] * np.arange(T, dtype=np.float32)[:, None]).astype(np.float64)
+    a, b = normed[..., :h].astype(np.float64), normed[..., h:rd].astype(np.float64)
+    c64, s64 = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    exp = np.concatenate([a * c64 - b * s64, b * c64 + a * s64], -1)
+    assert normwise(got[..., :rd], exp) < 1e-6
+    # positions reset per sequence and the offset shifts them
+    two = O.qk_norm_rope(np.concatenate([x, x]), w, cos, sin, rd, 1e-6, seq_len=T)
+    np.testing.assert_array_equal(two[:T], two[T:])
+    cos2, sin2 = O.rope_tables(2 * T, rd, 1e7)
+    shifted = O.qk_norm_rope(x[5:], w, cos2, sin2, rd, 1e-6, seq_len=T, pos_offset=5)
+    np.testing.assert_array_equal(shifted, O.qk_norm_rope(x, w, cos2, sin2, rd, 1e-6)[5:])
+
+
+def test_swiglu_invariants():
+    g = ramp(np.sin, (4, 256), 6.0)
+    u = np.ones_like(g)
+    # silu(x) - silu(-x) = x
+    np.testing.assert_allclose(O.swiglu(g, u) - O.swiglu(-g, u), g, rtol=1e-6, atol=1e-6)
+    assert np.array_equal(O.swiglu(np.zeros((2, 8), np.float32), u[:2, :8]), np.zeros((2, 8)))
+    # silu(x)*u is linear in u
+    u2 = ramp(np.cos, (4, 256))
+    np.testing.assert_array_equal(O.swiglu(g, u2 * np.float32(2)), O.swiglu(g, u2) * np.float32(2))
