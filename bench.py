@@ -1,0 +1,346 @@
+"""Benchmark of the fused per-layer row kernels on one MI355X.
+
+A step is one launch of each fused kernel over its synthetic batch:
+
+  rmsnorm_f32        x [8192, 1024] fp32, zero-centred RMSNorm
+  rmsnorm_bf16       x [8192, 1024] bf16
+  headnorm_f32       per-head q/k rows [81920, 256] fp32 (8192 tokens x 10 heads)
+  headnorm_bf16      same in bf16
+  qk_norm_rope_bf16  Q [8192, 8, 256] + K [8192, 2, 256] bf16, rotary 64 of 256,
+                     theta 1e7, positions 0..2047 reset per sequence (4 x 2048)
+  gather_bf16        16384 ids (8 x 2048) from a [248320, 1024] bf16 table
+  swiglu_bf16        gate/up [16384, 3584] bf16 -> bf16
+  gated_rms_bf16     DeltaNet output x, z [16384, 16, 128] bf16
+  residual_rms_bf16  x, mixed [16384, 1024] bf16 -> residual, normalised
+
+Inputs are resident in HBM before timing.  Every kernel cycles through
+several input/output buffer sets totalling more than 512 MB, so the 256 MB
+last-level cache cannot serve repeated launches.  The K launches of each
+kernel are captured once in a HIP graph (no host launch overhead between the
+few-microsecond kernels) and replayed between HIP events recorded on the same
+stream; a kernel's average launch duration is its replay time / K.  value =
+total algorithmic bytes of the K steps / total time (GB/s).  Algorithmic bytes
+= inputs read once + outputs written once + parameter vectors (+ RoPE tables).
+
+The CPU baseline times the C oracle (a single-threaded restatement of the
+reference CPU path, fp32 arithmetic as in the reference) on a quarter of each
+kernel's rows, repeated to at least 10 s, on this machine's host cores.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "qwendecisioncore.jl_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "achieved HBM GB/s (% of peak) per fused kernel; backbone_hidden tokens/s"
+PEAK_GBS = 8000.0            # MI355X HBM3E
+ROTATE_BYTES = 640 << 20     # > 2x the 256 MB last-level cache
+PMC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+
+
+def _sets(set_bytes: int) -> int:
+    return max(2, math.ceil(ROTATE_BYTES / set_bytes))
+
+
+class Kernel:
+    """One fused kernel at its benchmark shape with rotating buffer sets."""
+
+    def __init__(self, name, symbol, algo_bytes, make_set, launch, shape, dtype):
+        self.name, self.symbol, self.algo_bytes = name, symbol, algo_bytes
+        self.shape, self.dtype = shape, dtype
+        self.launch = launch
+        self.sets = [make_set(i) for i in range(_sets(algo_bytes))]
+        self.graph = None
+        self.avg_ms = None
+
+    def run(self, i):
+        self.launch(self.sets[i % len(self.sets)])
+
+
+def build_kernels(dev):
+    import torch
+    from qdc_amd import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    bf, f32 = torch.bfloat16, torch.float32
+
+    def randn(shape, dtype, scale=1.0):
+        return (torch.randn(shape, generator=g, device=dev, dtype=f32) * scale).to(dtype)
+
+    kernels = []
+
+    def rms(name, rows, width, dtype):
+        es = 2 if dtype == bf else 4
+        w = randn((width,), dtype, 0.02)
+        kernels.append(Kernel(
+            name, "rms_rows_fast", 2 * rows * width * es + width * es,
+            lambda i: (randn((rows, width), dtype), torch.empty((rows, width), dtype=dtype, device=dev)),
+            lambda s: ops.native_rms(s[0], w, 1e-6, out=s[1]), [rows, width], str(dtype)[6:]))
+
+    rms("rmsnorm_f32", 8192, 1024, f32)
+    rms("rmsnorm_bf16", 8192, 1024, bf)
+    rms("headnorm_f32", 81920, 256, f32)
+    rms("headnorm_bf16", 81920, 256, bf)
+
+    T, H, KV, hd, rd, seq = 8192, 8, 2, 256, 64, 2048
+    qn, kn = randn((hd,), bf, 0.02), randn((hd,), bf, 0.02)
+    tables = ops.rope_tables(seq, rd, 1e7, dev)
+    kernels.append(Kernel(
+        "qk_norm_rope_bf16", "qk_norm_rope_fast",
+        2 * T * (H + KV) * hd * 2 + 2 * hd * 2 + 2 * seq * (rd // 2) * 4,
+        lambda i: (randn((T, H, hd), bf), randn((T, KV, hd), bf),
+                   torch.empty((T, H, hd), dtype=bf, device=dev),
+                   torch.empty((T, KV, hd), dtype=bf, device=dev)),
+        lambda s: ops.prepare_heads(s[0], s[1], qn, kn, tables, rd, 1e-6, seq_len=seq,
+                                    q_out=s[2], k_out=s[3]),
+        [T, H, KV, hd, rd, seq], "bfloat16"))
+
+    vocab, hidden, n = 248320, 1024, 16384
+    table = randn((vocab, hidden), bf, 0.02)
+    kernels.append(Kernel(
+        "gather_bf16", "gather_fast", 2 * n * hidden * 2 + n * 4,
+        lambda i: (torch.randint(0, vocab, (n,), generator=g, device=dev, dtype=torch.int32),
+                   torch.empty((n, hidden), dtype=bf, device=dev)),
+        lambda s: ops.native_gather(table, s[0], out=s[1]), [vocab, hidden, n], "bfloat16"))
+
+    Ti, I = 16384, 3584
+    kernels.append(Kernel(
+        "swiglu_bf16", "swiglu_fast", 3 * Ti * I * 2,
+        lambda i: (randn((Ti, I), bf), randn((Ti, I), bf), torch.empty((Ti, I), dtype=bf, device=dev)),
+        lambda s: ops.native_mlp_gate(s[0], s[1], out=s[2]), [Ti, I], "bfloat16"))
+
+    Tg, Hg, Wg = 16384, 16, 128
+    wg = randn((Wg,), bf, 1.0)
+    kernels.append(Kernel(
+        "gated_rms_bf16", "rms_rows_fast", 3 * Tg * Hg * Wg * 2 + Wg * 2,
+        lambda i: (randn((Tg, Hg, Wg), bf), randn((Tg, Hg, Wg), bf),
+                   torch.empty((Tg, Hg, Wg), dtype=bf, device=dev)),
+        lambda s: ops.native_gated_rms(s[0], s[1], wg, 1e-6, out=s[2]), [Tg, Hg, Wg], "bfloat16"))
+
+    Tr, Hr = 16384, 1024
+    wr = randn((Hr,), bf, 0.02)
+    kernels.append(Kernel(
+        "residual_rms_bf16", "rms_rows_fast", 4 * Tr * Hr * 2 + Hr * 2,
+        lambda i: (randn((Tr, Hr), bf), randn((Tr, Hr), bf),
+                   torch.empty((Tr, Hr), dtype=bf, device=dev), torch.empty((Tr, Hr), dtype=bf, device=dev)),
+        lambda s: ops.native_residual_rms(s[0], s[1], wr, 1e-6, residual=s[2], out=s[3]),
+        [Tr, Hr], "bfloat16"))
+    return kernels
+
+
+def capture(kernels, steps):
+    """One HIP graph per kernel holding `steps` launches over its rotating sets;
+    a replay must reproduce the eager result exactly."""
+    import torch
+    stream = torch.cuda.Stream()
+    for k in kernels:
+        torch.cuda.synchronize()
+        k.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(k.graph, stream=stream):
+            for i in range(steps):
+                k.run(i)
+    torch.cuda.synchronize()
+
+
+def check_replay(kernels, steps):
+    """Replay output == eager output for the last set each graph wrote."""
+    import torch
+    for k in kernels:
+        s = k.sets[(steps - 1) % len(k.sets)]
+        outs = [t for t in s if t.dtype != torch.int32][-2:]
+        k.graph.replay()
+        torch.cuda.synchronize()
+        replayed = [o.clone() for o in outs]
+        k.run(steps - 1)
+        torch.cuda.synchronize()
+        for a, b in zip(replayed, outs):
+            if not torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                               b.view(torch.int16) if b.dtype == torch.bfloat16 else b):
+                raise RuntimeError(f"graph replay of {k.name} differs from the eager launch")
+
+
+def time_gpu(kernels, steps):
+    import torch
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in kernels]
+    start.record(stream)
+    for k, (a, b) in zip(kernels, marks):
+        a.record(stream)
+        k.graph.replay()
+        b.record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    for k, (a, b) in zip(kernels, marks):
+        k.avg_ms = a.elapsed_time(b) / steps
+    return start.elapsed_time(end)
+
+
+CALIB_BYTES = 512 << 20
+
+
+def calibrate(dev):
+    """Plain device-to-device copies of CALIB_BYTES each (torch's copy kernel):
+    the reference point that scales FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+    src = [torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev) for _ in range(2)]
+    dst = [torch.empty_like(s) for s in src]
+    for i in range(4):
+        dst[i % 2].copy_(src[i % 2])
+    torch.cuda.synchronize()
+    print(f"calibration: 4 copies of {CALIB_BYTES} bytes", file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(min_seconds=10.0):
+    """The C oracle (single thread, fp32 as the reference CPU path) on a quarter
+    of each kernel's rows; GB/s over the same algorithmic bytes (bf16 kernels
+    counted at their bf16 sizes, which favours the CPU)."""
+    import numpy as np
+    from oracle import qdc_oracle as O
+
+    rng = np.random.default_rng(0)
+
+    def rnd(*shape, scale=1.0):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+
+    jobs = []
+    for name, rows, width, es in (("rmsnorm_f32", 2048, 1024, 4), ("rmsnorm_bf16", 2048, 1024, 2),
+                                  ("headnorm_f32", 20480, 256, 4), ("headnorm_bf16", 20480, 256, 2)):
+        x, w = rnd(rows, width), rnd(width, scale=0.02)
+        jobs.append((name, 2 * rows * width * es + width * es, lambda x=x, w=w: O.rms(x, w, 1e-6)))
+    T, H, KV, hd, rd = 2048, 8, 2, 256, 64
+    q, k, qn = rnd(T, H, hd), rnd(T, KV, hd), rnd(hd, scale=0.02)
+    cos, sin = O.rope_tables(2048, rd, 1e7)
+    jobs.append(("qk_norm_rope_bf16", 2 * T * (H + KV) * hd * 2 + 2 * hd * 2 + 2 * 2048 * 32 * 4,
+                 lambda: (O.qk_norm_rope(q, qn, cos, sin, rd, 1e-6),
+                          O.qk_norm_rope(k, qn, cos, sin, rd, 1e-6))))
+    table = rng.integers(0, 1 << 16, size=(248320, 1024), dtype=np.uint16)
+    ids = rng.integers(0, 248320, size=4096)
+    jobs.append(("gather_bf16", 2 * 4096 * 1024 * 2 + 4096 * 4, lambda: O.gather(table, ids)))
+    gt, ut = rnd(4096, 3584), rnd(4096, 3584)
+    jobs.append(("swiglu_bf16", 3 * 4096 * 3584 * 2, lambda: O.swiglu(gt, ut)))
+    xg, zg, wg = rnd(4096, 16, 128), rnd(4096, 16, 128), rnd(128)
+    jobs.append(("gated_rms_bf16", 3 * 4096 * 16 * 128 * 2 + 256, lambda: O.gated_rms(xg, zg, wg, 1e-6)))
+    xr, mr, wr = rnd(4096, 1024), rnd(4096, 1024), rnd(1024, scale=0.02)
+    jobs.append(("residual_rms_bf16", 4 * 4096 * 1024 * 2 + 2048,
+                 lambda: O.residual_rms(xr, mr, wr, 1e-6)))
+    per, total_bytes, total_s, reps = {}, 0, 0.0, 0
+    while total_s < min_seconds or reps == 0:
+        for name, nbytes, fn in jobs:
+            t0 = time.perf_counter()
+            fn()
+            dt = time.perf_counter() - t0
+            b, s = per.get(name, (0, 0.0))
+            per[name] = (b + nbytes, s + dt)
+            total_bytes += nbytes
+            total_s += dt
+        reps += 1
+    return {
+        "value": round(total_bytes / total_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": (f"C oracle, 1 thread, fp32 arithmetic, on 1/4 of each kernel's rows "
+                   f"(same kernel mix), {reps} passes in {total_s:.1f} s on '{cpu_model()}' "
+                   f"({os.cpu_count()} logical CPUs visible)"),
+        "per_kernel_gbs": {k: round(b / s / 1e9, 3) for k, (b, s) in per.items()},
+    }
+
+
+def load_traffic(symbol):
+    try:
+        with open(PMC_FILE) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = data.get("kernels", {}).get(symbol)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma-separated kernel names (profiling runs)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run 4 plain 512 MiB device copies (scales the PMC byte counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the row kernels need no exchange; see the sharding notes)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.calibrate:
+        calibrate(dev)
+    kernels = build_kernels(dev)
+    if args.only:
+        keep = set(args.only.split(","))
+        kernels = [k for k in kernels if k.name in keep]
+    for i in range(args.warmup):
+        for k in kernels:
+            k.run(i)
+    capture(kernels, args.steps)
+    check_replay(kernels, args.steps)
+    for k in kernels:  # one untimed replay
+        k.graph.replay()
+    total_ms = time_gpu(kernels, args.steps)
+    step_bytes = sum(k.algo_bytes for k in kernels)
+    value = step_bytes * args.steps / (total_ms / 1e3) / 1e9
+    per = {k.name: {"shape": k.shape, "dtype": k.dtype, "bytes": k.algo_bytes,
+                    "us": round(k.avg_ms * 1e3, 3),
+                    "gbs": round(k.algo_bytes / (k.avg_ms / 1e3) / 1e9, 1),
+                    "pct_peak": round(100 * k.algo_bytes / (k.avg_ms / 1e3) / 1e9 / PEAK_GBS, 1)}
+           for k in kernels}
+    dom = max(kernels, key=lambda k: k.avg_ms)
+    achieved = dom.algo_bytes / (dom.avg_ms / 1e3) / 1e9
+    traffic = load_traffic(dom.name)
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "fused row kernels of one Qwen3.5-0.8B-like layer set: "
+                               + ", ".join(k.name for k in kernels),
+                   "storage": "bf16 and fp32 as named per kernel", "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": dom.name, "achieved": round(achieved, 1),
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
+                     "traffic": traffic, "algorithmic_bytes": dom.algo_bytes},
+        "kernels": per,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
