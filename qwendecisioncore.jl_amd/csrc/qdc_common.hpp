@@ -48,35 +48,67 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // ------------------------------------------------------ 16-byte chunk I/O --
-// `p` must be 16-byte aligned.  Values land in / come from v[0..kVec).
-__device__ __forceinline__ void load_chunk(const float *p, float (&v)[4]) {
-    const f32x4 r = *reinterpret_cast<const f32x4 *>(p);
-    v[0] = r.x; v[1] = r.y; v[2] = r.z; v[3] = r.w;
+// A chunk is loaded as raw 16 bytes (one global_load_dwordx4) and unpacked to
+// fp32 only where it is used; `p` must be 16-byte aligned.
+__device__ __forceinline__ u32x4 load_raw(const void *p) {
+    return *reinterpret_cast<const u32x4 *>(p);
 }
-__device__ __forceinline__ void load_chunk(const bf16_t *p, float (&v)[8]) {
-    const u32x4 r = *reinterpret_cast<const u32x4 *>(p);
+__device__ __forceinline__ void store_raw(void *p, u32x4 r) { *reinterpret_cast<u32x4 *>(p) = r; }
+// Streamed data read exactly once per launch: a nontemporal load, so it does
+// not displace reused lines (weights, RoPE tables) in the caches.
+__device__ __forceinline__ u32x4 load_stream(const void *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+}
+
+__device__ __forceinline__ void unpack(u32x4 r, float (&v)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(r[i]);
+}
+__device__ __forceinline__ void unpack(u32x4 r, float (&v)[8]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         v[2 * i] = __uint_as_float(r[i] << 16);
         v[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
     }
 }
-__device__ __forceinline__ void store_chunk(float *p, const float (&v)[4]) {
-    f32x4 r = {v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4 *>(p) = r;
+__device__ __forceinline__ u32x4 pack(const float (&v)[4]) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = __float_as_uint(v[i]);
+    return r;
 }
-__device__ __forceinline__ void store_chunk(bf16_t *p, const float (&v)[8]) {
+__device__ __forceinline__ u32x4 pack(const float (&v)[8]) {
     u32x4 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
-    *reinterpret_cast<u32x4 *>(p) = r;
+    return r;
 }
 
+__device__ __forceinline__ void load_chunk(const float *p, float (&v)[4]) { unpack(load_raw(p), v); }
+__device__ __forceinline__ void load_chunk(const bf16_t *p, float (&v)[8]) { unpack(load_raw(p), v); }
+__device__ __forceinline__ void store_chunk(float *p, const float (&v)[4]) { store_raw(p, pack(v)); }
+__device__ __forceinline__ void store_chunk(bf16_t *p, const float (&v)[8]) { store_raw(p, pack(v)); }
+
 // ------------------------------------------------------------- reductions --
-// Sum over aligned groups of N lanes (N a power of two <= 64) of a wavefront.
+// Sum over aligned groups of N lanes (N a power of two <= 64) of a wavefront;
+// every lane of a group ends with the bit-identical sum (each step adds a pair
+// of partial sums that the partner lane adds in the other order, and fp32
+// addition is commutative).  Steps inside a 16-lane row use DPP lane swizzles
+// (quad permutes, then the half-row and row mirrors, which pair each lane with
+// one in the other quad / half); the 16- and 32-lane steps cross rows and use
+// the LDS crossbar permute.
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
 template <int N> __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int offset = N / 2; offset >= 1; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "group of 1..64 lanes");
+    if constexpr (N >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (N >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (N >= 8) v += dpp<0x141>(v);  // row_half_mirror: lane 7-i of 8
+    if constexpr (N >= 16) v += dpp<0x140>(v); // row_mirror: lane 15-i of 16
+    if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
+    if constexpr (N >= 64) v += __shfl_xor(v, 32, kWave);
     return v;
 }
 

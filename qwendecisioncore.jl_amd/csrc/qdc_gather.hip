@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kBlock) void gather_fast(TO *__restrict__ out,
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int64_t c = base + u * kWave + lane;
-            if (c < chunks) r[u] = src[c];
+            if (c < chunks) r[u] = load_stream(src + c);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {

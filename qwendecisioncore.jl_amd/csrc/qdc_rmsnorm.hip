@@ -31,8 +31,7 @@ struct RowMap {
 template <typename T, int LPR, int CPL, Mode M, bool CENTERED>
 __global__ __launch_bounds__(kBlock) void rms_rows_fast(
     T *out, T *res_out, const T *x, const T *mixed, const T *__restrict__ z,
-    const T *__restrict__ w,
-    int64_t rows, RowMap map, float width, float eps) {
+    const T *__restrict__ w, int64_t rows, RowMap map, float width, float eps) {
     constexpr int V = Elem<T>::kVec;
     constexpr int RPB = kBlock / LPR;  // rows per workgroup
     const int lane = threadIdx.x % LPR;
@@ -48,25 +47,40 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
         oo = (int64_t)t * map.o_tok + (int64_t)h * map.o_head;
     }
 
+    // Issue every load of the row (x, mixed, gate, weights) before the first
+    // dependent instruction so their latencies overlap.
+    u32x4 xr[CPL], mr[M == Mode::kResidual ? CPL : 1], zr[M == Mode::kGated ? CPL : 1], wr[CPL];
+    if (active) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) xr[c] = load_stream(x + xo + (c * LPR + lane) * V);
+        if constexpr (M == Mode::kResidual) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) mr[c] = load_stream(mixed + xo + (c * LPR + lane) * V);
+        }
+        if constexpr (M == Mode::kGated) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) zr[c] = load_stream(z + zo + (c * LPR + lane) * V);
+        }
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) wr[c] = load_raw(w + (c * LPR + lane) * V);
+    }
+
     float v[CPL][V];
     float ss = 0.0f;
     if (active) {
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) load_chunk(x + xo + (c * LPR + lane) * V, v[c]);
-        if constexpr (M == Mode::kResidual) {
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) {
+        for (int c = 0; c < CPL; ++c) {
+            unpack(xr[c], v[c]);
+            if constexpr (M == Mode::kResidual) {
                 float m[V];
-                load_chunk(mixed + xo + (c * LPR + lane) * V, m);
+                unpack(mr[c], m);
 #pragma unroll
                 for (int j = 0; j < V; ++j) v[c][j] = v[c][j] + m[j];
                 store_chunk(res_out + oo + (c * LPR + lane) * V, v[c]);
             }
-        }
-#pragma unroll
-        for (int c = 0; c < CPL; ++c)
 #pragma unroll
             for (int j = 0; j < V; ++j) ss += v[c][j] * v[c][j];
+        }
     }
     ss = group_sum<LPR>(ss);
     if (!active) return;
@@ -74,12 +88,11 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
 
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-        const int e = (c * LPR + lane) * V;
         float wv[V], o[V];
-        load_chunk(w + e, wv);
+        unpack(wr[c], wv);
         if constexpr (M == Mode::kGated) {
             float g[V];
-            load_chunk(z + zo + e, g);
+            unpack(zr[c], g);
 #pragma unroll
             for (int j = 0; j < V; ++j) o[j] = ((v[c][j] * s) * wv[j]) * silu(g[j]);
         } else {
@@ -87,7 +100,7 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
             for (int j = 0; j < V; ++j)
                 o[j] = (v[c][j] * s) * (CENTERED ? (1.0f + wv[j]) : wv[j]);
         }
-        store_chunk(out + oo + e, o);
+        store_chunk(out + oo + (c * LPR + lane) * V, o);
     }
 }
 
@@ -141,8 +154,10 @@ int32_t launch_fast(T *out, T *res, const T *x, const T *mixed, const T *z, cons
     return launch_status();
 }
 
-// Fast-path shapes: C = 1..64 (powers of two) with one chunk per lane, or
-// C = 64*CPL for the listed CPL.  kNoFastPath when no instantiation matches.
+// Fast-path shapes by C = chunks per row: a lane holds 2 chunks (32 bytes in
+// flight) for rows of up to 64 chunks and 4 chunks (64 bytes) for 128- and
+// 256-chunk rows, which measured fastest on MI355X; wider rows use all 64
+// lanes with C/64 chunks each.  kNoFastPath when no instantiation matches.
 template <typename T, Mode M, bool C>
 int32_t dispatch_fast(T *out, T *res, const T *x, const T *mixed, const T *z, const T *w,
                       int64_t rows, const RowMap &map, int64_t width, float eps,
@@ -154,13 +169,13 @@ int32_t dispatch_fast(T *out, T *res, const T *x, const T *mixed, const T *z, co
                                               stream);
     switch (chunks) {
         QDC_FAST(1, 1)
-        QDC_FAST(2, 1)
-        QDC_FAST(4, 1)
-        QDC_FAST(8, 1)
-        QDC_FAST(16, 1)
-        QDC_FAST(32, 1)
-        QDC_FAST(64, 1)
-        QDC_FAST(64, 2)
+        QDC_FAST(1, 2)
+        QDC_FAST(2, 2)
+        QDC_FAST(4, 2)
+        QDC_FAST(8, 2)
+        QDC_FAST(16, 2)
+        QDC_FAST(32, 2)
+        QDC_FAST(32, 4)
         QDC_FAST(64, 3)
         QDC_FAST(64, 4)
         QDC_FAST(64, 5)

@@ -53,28 +53,45 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
     const int group_base = (threadIdx.x % kWave) - lane;  // first lane of this row group
     const int64_t row = block * RPB + threadIdx.x / LPR;
     const bool active = row < sd.rows;
+    const int hc = a.half / V;  // chunks per half of the rotary block
+    const bool rotary = lane < 2 * hc;
 
+    // Every load first: the row, its norm weights and (rotary lanes) the
+    // cos/sin of its position, so the latencies overlap.
     uint32_t t = 0, h = 0;
-    float v[V] = {};
-    float ss = 0.0f;
+    u32x4 xr = {0u, 0u, 0u, 0u};
+    u32x4 cr[V / 4], sr[V / 4];
     if (active) {
         t = fastdiv((uint32_t)row, sd.heads);
         h = (uint32_t)row - t * sd.heads.d;
-        load_chunk(sd.in + (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head + lane * V, v);
+        xr = load_stream(sd.in + (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head + lane * V);
+        if (rotary) {
+            const uint32_t tq = fastdiv(t, a.seq_len);
+            const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
+            const int64_t i0 = pos * a.half + (lane < hc ? lane : lane - hc) * V;
 #pragma unroll
-        for (int j = 0; j < V; ++j) ss += v[j] * v[j];
+            for (int q = 0; q < V / 4; ++q) {
+                cr[q] = load_raw(a.cos + i0 + 4 * q);
+                sr[q] = load_raw(a.sin + i0 + 4 * q);
+            }
+        }
     }
+    const u32x4 wr = load_raw(sd.w + lane * V);
+
+    float v[V];
+    unpack(xr, v);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) ss += v[j] * v[j];
     ss = group_sum<LPR>(ss);
     const float s = rms_scale(ss, (float)a.dim, a.eps);
     float wv[V];
-    load_chunk(sd.w + lane * V, wv);
+    unpack(wr, wv);
 #pragma unroll
     for (int j = 0; j < V; ++j) v[j] = (v[j] * s) * (1.0f + wv[j]);
 
     // Partner chunk of the rotation, fetched from the owning lane.  Every lane
     // takes part in the permute (inactive rows included) so it stays uniform.
-    const int hc = a.half / V;  // chunks per half of the rotary block
-    const bool rotary = lane < 2 * hc;
     const int src = rotary ? (lane < hc ? lane + hc : lane - hc) : lane;
     float p[V];
 #pragma unroll
@@ -82,23 +99,14 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
     if (!active) return;
 
     if (rotary) {
-        const uint32_t tq = fastdiv(t, a.seq_len);
-        const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
-        const int i0 = (lane < hc ? lane : lane - hc) * V;
-        const float *cp = a.cos + pos * a.half + i0;
-        const float *sp = a.sin + pos * a.half + i0;
         float c[V], sn[V];
 #pragma unroll
-        for (int j = 0; j < V; j += 4) {
-            float c4[4], s4[4];
-            load_chunk(cp + j, c4);
-            load_chunk(sp + j, s4);
+        for (int q = 0; q < V / 4; ++q)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                c[j + q] = c4[q];
-                sn[j + q] = s4[q];
+            for (int e = 0; e < 4; ++e) {
+                c[4 * q + e] = __uint_as_float(cr[q][e]);
+                sn[4 * q + e] = __uint_as_float(sr[q][e]);
             }
-        }
         if (lane < hc) {
 #pragma unroll
             for (int j = 0; j < V; ++j) v[j] = v[j] * c[j] - p[j] * sn[j];

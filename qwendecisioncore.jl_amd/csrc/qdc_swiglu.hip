@@ -13,7 +13,7 @@
 namespace qdc {
 namespace {
 
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void swiglu_fast(T *out, const T *gate, const T *up,
@@ -31,8 +31,8 @@ __global__ __launch_bounds__(kBlock) void swiglu_fast(T *out, const T *gate, con
         if (idx < total_chunks) {
             const uint32_t t = fastdiv(idx, per_row);
             const int64_t col = (int64_t)(idx - t * per_row.d) * V;
-            load_chunk(gate + (int64_t)t * ld_gate + col, g[k]);
-            load_chunk(up + (int64_t)t * ld_up + col, u[k]);
+            unpack(load_stream(gate + (int64_t)t * ld_gate + col), g[k]);
+            unpack(load_stream(up + (int64_t)t * ld_up + col), u[k]);
             oo[k] = (int64_t)t * ld_out + col;
         }
     }
