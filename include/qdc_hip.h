@@ -6,9 +6,10 @@
  *  - Tensors are device pointers to row-major data; "[rows, width]" here is the
  *    reference's column-major (width, rows) Julia matrix in the same memory.
  *    Strides ("tok", "head", "ld") are in elements, not bytes.
- *  - dtype selects the element type of every activation and weight argument of
- *    the call (QDC_F32 or QDC_BF16).  Arithmetic is fp32; bf16 results are
- *    rounded to nearest even.  RoPE tables are always fp32.
+ *  - dtype arguments (QDC_F32 or QDC_BF16) select the element types of the
+ *    call's tensors; the RMSNorm entry points take one per tensor role so an
+ *    fp32 residual stream can feed bf16 activations.  Arithmetic is fp32; bf16
+ *    results are rounded to nearest even.  RoPE tables are always fp32.
  *  - The library never allocates or frees memory, keeps no pointer after
  *    return, has no mutable global state and never synchronises: work is
  *    enqueued on `stream` (0 = the null stream of the current device) and the
@@ -76,23 +77,31 @@ int32_t qdc_check_ids(const int64_t *ids, int64_t n_ids, int64_t vocab);
  * src/backbone.jl:200-204; CPU cpu_rms! src/backbone_cpu.jl:333-350).  Serves
  * the input, post-attention and final norms, per-head q/k rows without RoPE
  * (rows = tokens*heads, width = head_dim) and, with centered = 0, the plain
- * DeltaNet output norm.  Row r reads x + r*ld_x and writes out + r*ld_out;
- * out may equal x.
+ * DeltaNet output norm.  Row r reads x + r*ld_x and writes out + r*ld_out.
+ * x_dtype is the type of x; out_dtype that of out and weight.  Supported:
+ * f32->f32, bf16->bf16 and f32->bf16 (an fp32 residual stream feeding bf16
+ * GEMMs).  out may equal x when the type and stride agree.
  */
 int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows, int64_t width,
-                    int64_t ld_x, int64_t ld_out, float eps, int32_t centered, int32_t dtype,
-                    hipStream_t stream);
+                    int64_t ld_x, int64_t ld_out, float eps, int32_t centered, int32_t x_dtype,
+                    int32_t out_dtype, hipStream_t stream);
 
 /*
- * residual = x + mixed; out = zero-centred RMSNorm(residual) with weight.
- * Replaces native_residual_rms (ext/amdgpu_workspace.jl:157-166; generic
- * src/backbone.jl:347-350; CPU src/backbone_cpu.jl:321-328) in one pass.
- * Contiguous rows of `width`.  residual may equal x or mixed; out may equal
- * x or mixed; out and residual must differ.
+ * residual = x + mixed; out = zero-centred RMSNorm(residual) with weight, in
+ * one pass over contiguous rows of `width`.  Replaces native_residual_rms
+ * (ext/amdgpu_workspace.jl:157-166; generic src/backbone.jl:347-350; CPU
+ * src/backbone_cpu.jl:321-328) and, called with the next layer's input-norm
+ * weight, the residual add of native_layer (src/backbone.jl:358-366) fused
+ * with that next norm.  residual_dtype types x and residual, mixed_dtype
+ * mixed, out_dtype out and weight.  Supported: all bf16, or an f32 residual
+ * stream with an f32 or bf16 addend and an f32 or bf16 output.  The sum is formed and
+ * normalised in fp32.  residual may equal x (or mixed of the same type); out
+ * may equal x or mixed of the same type; out and residual must differ.
  */
 int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x, const void *mixed,
                              const void *weight, int64_t rows, int64_t width, float eps,
-                             int32_t dtype, hipStream_t stream);
+                             int32_t residual_dtype, int32_t mixed_dtype, int32_t out_dtype,
+                             hipStream_t stream);
 
 /*
  * Per-head zero-centred RMSNorm fused with half-split partial RoPE, for the Q

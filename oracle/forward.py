@@ -8,6 +8,14 @@ Weights are a dict of float32 numpy arrays keyed by the checkpoint names with
 the ``language_model.`` prefix removed (``layers.0.mlp.gate_proj.weight`` ...),
 laid out as stored (PyTorch ``[out, in]``), which is the reference's Julia
 ``(in, out)`` matrix in the same memory.
+
+``bf16=True`` runs the same algorithm with bf16 storage (RNE,
+``src/safetensors.jl:37-42``) of the activations a bf16 device pipeline keeps in
+bf16: the normalised GEMM inputs, the outputs of the input-side projections
+(q||gate, k, v, qkv, z, a, b, gate, up), the normed+rotated q/k, the merged
+attention output, the DeltaNet recurrence and gated-norm outputs and the SwiGLU
+output.  The residual stream and the outputs of the residual-side projections
+(o_proj, out_proj, down_proj) stay fp32.  Arithmetic stays fp32 throughout.
 """
 from __future__ import annotations
 
@@ -71,17 +79,24 @@ def _linear(x, w):
     return (x @ w.T).astype(F32)
 
 
-def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, tables):
+def _store(x, bf16):
+    """Storage rounding of an activation: bf16 RNE when ``bf16``, else fp32."""
+    return ops.round_bf16(x) if bf16 else np.asarray(x, F32)
+
+
+def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, tables,
+                   bf16: bool = False):
     """``full_attention`` (``src/backbone.jl:224-262``) on ``x [T, hidden]``."""
     T = x.shape[0]
     hd, H, KV = cfg["head_dim"], cfg["heads"], cfg["kv_heads"]
-    qgate = _linear(x, W[p + "self_attn.q_proj.weight"]).reshape(T, H, 2 * hd)
+    qgate = _store(_linear(x, W[p + "self_attn.q_proj.weight"]), bf16).reshape(T, H, 2 * hd)
     cos, sin = tables
-    q = ops.qk_norm_rope(qgate[:, :, :hd], W[p + "self_attn.q_norm.weight"], cos, sin,
-                         cfg["rotary_dim"], cfg["eps"])
-    kp = _linear(x, W[p + "self_attn.k_proj.weight"]).reshape(T, KV, hd)
-    k = ops.qk_norm_rope(kp, W[p + "self_attn.k_norm.weight"], cos, sin, cfg["rotary_dim"], cfg["eps"])
-    v = _linear(x, W[p + "self_attn.v_proj.weight"]).reshape(T, KV, hd)
+    q = _store(ops.qk_norm_rope(qgate[:, :, :hd], W[p + "self_attn.q_norm.weight"], cos, sin,
+                                cfg["rotary_dim"], cfg["eps"]), bf16)
+    kp = _store(_linear(x, W[p + "self_attn.k_proj.weight"]), bf16).reshape(T, KV, hd)
+    k = _store(ops.qk_norm_rope(kp, W[p + "self_attn.k_norm.weight"], cos, sin, cfg["rotary_dim"],
+                                cfg["eps"]), bf16)
+    v = _store(_linear(x, W[p + "self_attn.v_proj.weight"]), bf16).reshape(T, KV, hd)
     # scores_mask[i (key), j (query)] (src/backbone.jl:237-242)
     keys = np.arange(T)[:, None]
     queries = np.arange(T)[None, :]
@@ -98,7 +113,7 @@ def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, 
         values = (probs.T @ v[:, kv, :]).astype(F32)  # [query, hd]
         gate = _sigmoid(qgate[:, h, hd:])
         out[:, h * hd:(h + 1) * hd] = values * gate
-    return _linear(out, W[p + "self_attn.o_proj.weight"])
+    return _linear(_store(out, bf16), W[p + "self_attn.o_proj.weight"])
 
 
 def causal_depthwise(x: np.ndarray, w: np.ndarray) -> np.ndarray:
@@ -114,7 +129,8 @@ def causal_depthwise(x: np.ndarray, w: np.ndarray) -> np.ndarray:
     return _silu(out)
 
 
-def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict):
+def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
+                    bf16: bool = False):
     """Gated DeltaNet, recurrent form of the CPU default path.
 
     ``cpu_delta_prepare`` (``src/backbone_cpu.jl:465-499``) and
@@ -124,7 +140,7 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict)
     T = x.shape[0]
     kd, kh, vd, vh = cfg["key_dim"], cfg["key_heads"], cfg["value_dim"], cfg["value_heads"]
     masked = (x * mask.astype(F32)[:, None]).astype(F32)
-    qkv = _linear(masked, W[p + "linear_attn.in_proj_qkv.weight"])
+    qkv = _store(_linear(masked, W[p + "linear_attn.in_proj_qkv.weight"]), bf16)
     conv = W[p + "linear_attn.conv1d.weight"]
     conv = conv.reshape(conv.shape[0], conv.shape[-1])
     mixed = causal_depthwise(qkv, conv)
@@ -134,11 +150,11 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict)
     v = mixed[:, 2 * kw:].reshape(T, vh, vd)
     q = (q / (np.sqrt((q * q).sum(-1, keepdims=True) + F32(1e-6)) * np.sqrt(F32(kd)))).astype(F32)
     k = (k / (np.sqrt((k * k).sum(-1, keepdims=True) + F32(1e-6)) * F32(1))).astype(F32)
-    z = _linear(masked, W[p + "linear_attn.in_proj_z.weight"]).reshape(T, vh, vd)
-    beta = _sigmoid(_linear(masked, W[p + "linear_attn.in_proj_b.weight"]))
+    z = _store(_linear(masked, W[p + "linear_attn.in_proj_z.weight"]), bf16).reshape(T, vh, vd)
+    beta = _sigmoid(_store(_linear(masked, W[p + "linear_attn.in_proj_b.weight"]), bf16))
     a_decay = (F32(-1) * np.exp(W[p + "linear_attn.A_log"].astype(F32))).astype(F32)
-    decay = (a_decay * _softplus(_linear(masked, W[p + "linear_attn.in_proj_a.weight"])
-                                 + W[p + "linear_attn.dt_bias"])).astype(F32)
+    decay = (a_decay * _softplus(_store(_linear(masked, W[p + "linear_attn.in_proj_a.weight"]),
+                                        bf16) + W[p + "linear_attn.dt_bias"])).astype(F32)
     groups = vh // kh
     kidx = np.arange(vh) // groups
     state = np.zeros((vh, vd, kd), F32)
@@ -151,7 +167,8 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict)
         proj = (beta[t][:, None] * (v[t] - factor[:, None] * proj)).astype(F32)
         state = (factor[:, None, None] * state + proj[:, :, None] * kt[:, None, :]).astype(F32)
         result[t] = np.einsum("hvk,hk->hv", state, qt)
-    out = ops.gated_rms(result, z, W[p + "linear_attn.norm.weight"], cfg["eps"])
+    out = _store(ops.gated_rms(_store(result, bf16), z, W[p + "linear_attn.norm.weight"],
+                               cfg["eps"]), bf16)
     return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
 
 
@@ -169,8 +186,12 @@ def check_sequence(ids, mask, vocab):
         raise ValueError("Mask values must be zero or one.")
 
 
-def backbone_hidden(W: dict, cfg: dict, ids, mask) -> np.ndarray:
-    """``backbone_hidden`` (``src/backbone.jl:433-460``) -> ``[T, hidden]`` fp32."""
+def backbone_hidden(W: dict, cfg: dict, ids, mask, bf16: bool = False) -> np.ndarray:
+    """``backbone_hidden`` (``src/backbone.jl:433-460``) -> ``[T, hidden]`` fp32.
+
+    The residual add of each layer is computed together with the next RMSNorm
+    (the final norm after the last layer); ``bf16`` selects bf16 storage of
+    the activations listed in the module docstring."""
     embed = W["embed_tokens.weight"]
     check_sequence(ids, mask, embed.shape[0])
     ids = np.asarray(ids, dtype=np.int32).reshape(-1)
@@ -180,17 +201,24 @@ def backbone_hidden(W: dict, cfg: dict, ids, mask) -> np.ndarray:
     tables = ops.rope_tables(T, cfg["rotary_dim"], cfg["rope_theta"]) if cfg["rotary_dim"] else (
         np.zeros((T, 0), F32), np.zeros((T, 0), F32))
     eps = cfg["eps"]
-    for i, kind in enumerate(cfg["layer_types"]):
+    kinds = cfg["layer_types"]
+    normed = _store(ops.rms(h, W["layers.0.input_layernorm.weight"], eps), bf16)
+    for i, kind in enumerate(kinds):
         p = f"layers.{i}."
-        normed = ops.rms(h, W[p + "input_layernorm.weight"], eps)
         if kind == "full_attention":
-            mixed = full_attention(W, p, normed, mask, cfg, tables)
+            mixed = full_attention(W, p, normed, mask, cfg, tables, bf16)
         elif kind == "linear_attention":
-            mixed = delta_attention(W, p, normed, mask, cfg)
+            mixed = delta_attention(W, p, normed, mask, cfg, bf16)
         else:
             raise ValueError(f"Unsupported layer type {kind}.")
         residual, normed = ops.residual_rms(h, mixed, W[p + "post_attention_layernorm.weight"], eps)
-        gate = _linear(normed, W[p + "mlp.gate_proj.weight"])
-        up = _linear(normed, W[p + "mlp.up_proj.weight"])
-        h = (residual + _linear(ops.swiglu(gate, up), W[p + "mlp.down_proj.weight"])).astype(F32)
-    return ops.rms(h, W["norm.weight"], eps)
+        normed = _store(normed, bf16)
+        gate = _store(_linear(normed, W[p + "mlp.gate_proj.weight"]), bf16)
+        up = _store(_linear(normed, W[p + "mlp.up_proj.weight"]), bf16)
+        down = _linear(_store(ops.swiglu(gate, up), bf16), W[p + "mlp.down_proj.weight"])
+        nxt = W[f"layers.{i + 1}.input_layernorm.weight"] if i + 1 < len(kinds) else W["norm.weight"]
+        # native_residual_add! (src/backbone.jl:358-361), then the next RMSNorm
+        h, normed = ops.residual_rms(residual, down, nxt, eps)
+        if i + 1 < len(kinds):
+            normed = _store(normed, bf16)
+    return normed

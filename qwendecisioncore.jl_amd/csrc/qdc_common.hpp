@@ -89,6 +89,59 @@ __device__ __forceinline__ void load_chunk(const bf16_t *p, float (&v)[8]) { unp
 __device__ __forceinline__ void store_chunk(float *p, const float (&v)[4]) { store_raw(p, pack(v)); }
 __device__ __forceinline__ void store_chunk(bf16_t *p, const float (&v)[8]) { store_raw(p, pack(v)); }
 
+// ----------------------------------------------- V-element fragments ---
+// V consecutive elements of type T (V*sizeof(T) bytes, a multiple of 16) held
+// as raw 16-byte vectors; lets one kernel mix fp32 and bf16 tensors at the
+// same element granularity (8 bf16 = 1 load, 8 fp32 = 2 loads).
+template <typename T, int V> struct Frag {
+    static constexpr int kN = V * (int)sizeof(T) / 16;
+    static_assert(kN >= 1 && kN * 16 == V * (int)sizeof(T), "fragment must be whole 16-byte chunks");
+    u32x4 r[kN];
+};
+
+template <typename T, int V> __device__ __forceinline__ Frag<T, V> load_frag(const T *p) {
+    Frag<T, V> f;
+#pragma unroll
+    for (int i = 0; i < Frag<T, V>::kN; ++i) f.r[i] = load_raw(p + i * (16 / (int)sizeof(T)));
+    return f;
+}
+template <typename T, int V> __device__ __forceinline__ Frag<T, V> stream_frag(const T *p) {
+    Frag<T, V> f;
+#pragma unroll
+    for (int i = 0; i < Frag<T, V>::kN; ++i) f.r[i] = load_stream(p + i * (16 / (int)sizeof(T)));
+    return f;
+}
+template <int V> __device__ __forceinline__ void unpack(const Frag<float, V> &f, float (&v)[V]) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = __uint_as_float(f.r[i / 4][i % 4]);
+}
+template <int V> __device__ __forceinline__ void unpack(const Frag<bf16_t, V> &f, float (&v)[V]) {
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i) {
+        const uint32_t b = f.r[i / 4][i % 4];
+        v[2 * i] = __uint_as_float(b << 16);
+        v[2 * i + 1] = __uint_as_float(b & 0xffff0000u);
+    }
+}
+template <int V> __device__ __forceinline__ void store_frag(float *p, const float (&v)[V]) {
+#pragma unroll
+    for (int i = 0; i < V / 4; ++i) {
+        u32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = __float_as_uint(v[4 * i + e]);
+        store_raw(p + 4 * i, r);
+    }
+}
+template <int V> __device__ __forceinline__ void store_frag(bf16_t *p, const float (&v)[V]) {
+#pragma unroll
+    for (int i = 0; i < V / 8; ++i) {
+        u32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = pack_bf16x2(v[8 * i + 2 * e], v[8 * i + 2 * e + 1]);
+        store_raw(p + 8 * i, r);
+    }
+}
+
 // ------------------------------------------------------------- reductions --
 // Sum over aligned groups of N lanes (N a power of two <= 64) of a wavefront;
 // every lane of a group ends with the bit-identical sum (each step adds a pair

@@ -3,16 +3,26 @@
 //   qdc_residual_rmsnorm residual = x + mixed, then zero-centred RMSNorm
 //   qdc_gated_rmsnorm    DeltaNet output norm fused with silu(z)
 //
-// Fast path: a row of W elements is split into C = W*sizeof(T)/16 chunks of
-// 16 bytes.  A group of LPR = min(C, 64) lanes owns a row; lane l holds chunks
-// l, l+LPR, ... (CPL = C/LPR chunks, so every load instruction of the group is
-// one contiguous LPR*16-byte segment).  The row stays in registers: HBM sees
-// each input byte read once and each output byte written once.  The sum of
-// squares is reduced across the group with xor-shuffles; 64/LPR rows share a
+// Types: TX is the row input (and the residual stream: x and the residual
+// output), TM the `mixed` addend, TO the normalised output and the weight.
+// The supported mixes keep the residual stream in fp32 while the activations
+// fed to the GEMMs are bf16.
+//
+// Fast path: a row is split into G = width/V groups of V elements (V = 4 when
+// every tensor is fp32, else 8, so a group of any tensor is whole 16-byte
+// chunks).  A set of LPR lanes owns a row; lane l holds groups l, l+LPR, ...
+// (CPL groups), so each load instruction of the set covers one contiguous
+// segment.  All loads of a row (x, mixed, gate, weights) are issued before the
+// first dependent instruction; streamed inputs use nontemporal loads.  The row
+// stays in registers: HBM sees each input byte read once and each output byte
+// written once.  The sum of squares is reduced across the LPR lanes (DPP inside
+// 16-lane rows, LDS-crossbar permutes across them); 64/LPR rows share a
 // wavefront, 4 wavefronts a workgroup.
 //
 // General path (any width, stride or alignment): one wavefront per row, scalar
 // strided accesses, two passes over the row (the second from cache).
+#include <initializer_list>
+
 #include "qdc_common.hpp"
 
 namespace qdc {
@@ -23,16 +33,20 @@ enum class Mode { kPlain, kResidual, kGated };
 // Row addressing: row r = (t, h) with t = r / heads, h = r % heads.
 struct RowMap {
     FastDiv heads;
-    int64_t x_tok, x_head;  // input (and residual-input `mixed` shares x's map)
+    int64_t x_tok, x_head;  // input (the residual-mode addend shares x's map)
     int64_t z_tok, z_head;  // gate input (gated mode)
     int64_t o_tok, o_head;  // output (and residual output)
 };
 
-template <typename T, int LPR, int CPL, Mode M, bool CENTERED>
+template <typename TX, typename TM, typename TO> constexpr int group_elems() {
+    return (sizeof(TX) == 4 && sizeof(TM) == 4 && sizeof(TO) == 4) ? 4 : 8;
+}
+
+template <typename TX, typename TM, typename TO, int LPR, int CPL, Mode M, bool CENTERED>
 __global__ __launch_bounds__(kBlock) void rms_rows_fast(
-    T *out, T *res_out, const T *x, const T *mixed, const T *__restrict__ z,
-    const T *__restrict__ w, int64_t rows, RowMap map, float width, float eps) {
-    constexpr int V = Elem<T>::kVec;
+    TO *out, TX *res_out, const TX *x, const TM *mixed, const TO *__restrict__ z,
+    const TO *__restrict__ w, int64_t rows, RowMap map, float width, float eps) {
+    constexpr int V = group_elems<TX, TM, TO>();
     constexpr int RPB = kBlock / LPR;  // rows per workgroup
     const int lane = threadIdx.x % LPR;
     const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
@@ -47,22 +61,25 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
         oo = (int64_t)t * map.o_tok + (int64_t)h * map.o_head;
     }
 
-    // Issue every load of the row (x, mixed, gate, weights) before the first
-    // dependent instruction so their latencies overlap.
-    u32x4 xr[CPL], mr[M == Mode::kResidual ? CPL : 1], zr[M == Mode::kGated ? CPL : 1], wr[CPL];
+    // Issue every load of the row before the first dependent instruction.
+    Frag<TX, V> xr[CPL];
+    Frag<TM, V> mr[M == Mode::kResidual ? CPL : 1];
+    Frag<TO, V> zr[M == Mode::kGated ? CPL : 1];
+    Frag<TO, V> wr[CPL];
     if (active) {
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) xr[c] = load_stream(x + xo + (c * LPR + lane) * V);
+        for (int c = 0; c < CPL; ++c) xr[c] = stream_frag<TX, V>(x + xo + (c * LPR + lane) * V);
         if constexpr (M == Mode::kResidual) {
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) mr[c] = load_stream(mixed + xo + (c * LPR + lane) * V);
+            for (int c = 0; c < CPL; ++c)
+                mr[c] = stream_frag<TM, V>(mixed + xo + (c * LPR + lane) * V);
         }
         if constexpr (M == Mode::kGated) {
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) zr[c] = load_stream(z + zo + (c * LPR + lane) * V);
+            for (int c = 0; c < CPL; ++c) zr[c] = stream_frag<TO, V>(z + zo + (c * LPR + lane) * V);
         }
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) wr[c] = load_raw(w + (c * LPR + lane) * V);
+        for (int c = 0; c < CPL; ++c) wr[c] = load_frag<TO, V>(w + (c * LPR + lane) * V);
     }
 
     float v[CPL][V];
@@ -76,7 +93,7 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
                 unpack(mr[c], m);
 #pragma unroll
                 for (int j = 0; j < V; ++j) v[c][j] = v[c][j] + m[j];
-                store_chunk(res_out + oo + (c * LPR + lane) * V, v[c]);
+                store_frag(res_out + oo + (c * LPR + lane) * V, v[c]);
             }
 #pragma unroll
             for (int j = 0; j < V; ++j) ss += v[c][j] * v[c][j];
@@ -100,30 +117,29 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
             for (int j = 0; j < V; ++j)
                 o[j] = (v[c][j] * s) * (CENTERED ? (1.0f + wv[j]) : wv[j]);
         }
-        store_chunk(out + oo + (c * LPR + lane) * V, o);
+        store_frag(out + oo + (c * LPR + lane) * V, o);
     }
 }
 
 // One wavefront per row, any width/stride/alignment.
-template <typename T, Mode M, bool CENTERED>
+template <typename TX, typename TM, typename TO, Mode M, bool CENTERED>
 __global__ __launch_bounds__(kBlock) void rms_rows_general(
-    T *out, T *res_out, const T *x, const T *mixed, const T *__restrict__ z,
-    const T *__restrict__ w,
-    int64_t rows, RowMap map, int64_t width, float eps) {
+    TO *out, TX *res_out, const TX *x, const TM *mixed, const TO *__restrict__ z,
+    const TO *__restrict__ w, int64_t rows, RowMap map, int64_t width, float eps) {
     const int lane = threadIdx.x % kWave;
     const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
     if (row >= rows) return;  // uniform per wavefront
     const uint32_t t = fastdiv((uint32_t)row, map.heads);
     const uint32_t h = (uint32_t)row - t * map.heads.d;
-    const T *xr = x + (int64_t)t * map.x_tok + (int64_t)h * map.x_head;
-    const T *zr = z + (int64_t)t * map.z_tok + (int64_t)h * map.z_head;
+    const int64_t xo = (int64_t)t * map.x_tok + (int64_t)h * map.x_head;
+    const int64_t zo = (int64_t)t * map.z_tok + (int64_t)h * map.z_head;
     const int64_t oo = (int64_t)t * map.o_tok + (int64_t)h * map.o_head;
     float ss = 0.0f;
     for (int64_t i = lane; i < width; i += kWave) {
-        float v = to_f32(xr[i]);
+        float v = to_f32(x[xo + i]);
         if constexpr (M == Mode::kResidual) {
-            v = v + to_f32(mixed[(xr - x) + i]);
-            res_out[oo + i] = from_f32<T>(v);
+            v = v + to_f32(mixed[xo + i]);
+            res_out[oo + i] = from_f32<TX>(v);
         }
         ss += v * v;
     }
@@ -132,42 +148,49 @@ __global__ __launch_bounds__(kBlock) void rms_rows_general(
     for (int64_t i = lane; i < width; i += kWave) {
         // the residual may overwrite x or mixed in place: read back what this
         // lane stored in the first pass
-        const float v = M == Mode::kResidual ? to_f32(res_out[oo + i]) : to_f32(xr[i]);
+        const float v = M == Mode::kResidual ? to_f32(res_out[oo + i]) : to_f32(x[xo + i]);
         const float wv = to_f32(w[i]);
         float o;
         if constexpr (M == Mode::kGated) {
-            o = ((v * s) * wv) * silu(to_f32(zr[i]));
+            o = ((v * s) * wv) * silu(to_f32(z[zo + i]));
         } else {
             o = (v * s) * (CENTERED ? (1.0f + wv) : wv);
         }
-        out[oo + i] = from_f32<T>(o);
+        out[oo + i] = from_f32<TO>(o);
     }
 }
 
-template <typename T, int LPR, int CPL, Mode M, bool C>
-int32_t launch_fast(T *out, T *res, const T *x, const T *mixed, const T *z, const T *w,
-                    int64_t rows, const RowMap &map, int64_t width, float eps,
-                    hipStream_t stream) {
-    const int64_t blocks = ceil_div(rows, kBlock / LPR);
-    hipLaunchKernelGGL((rms_rows_fast<T, LPR, CPL, M, C>), dim3((uint32_t)blocks), dim3(kBlock), 0,
-                       stream, out, res, x, mixed, z, w, rows, map, (float)width, eps);
+struct Args {
+    void *out, *res;
+    const void *x, *mixed, *z, *w;
+    int64_t rows, width;
+    RowMap map;
+    float eps;
+    bool fast;
+};
+
+template <typename TX, typename TM, typename TO, int LPR, int CPL, Mode M, bool C>
+int32_t launch_fast(const Args &a, hipStream_t stream) {
+    const int64_t blocks = ceil_div(a.rows, kBlock / LPR);
+    hipLaunchKernelGGL((rms_rows_fast<TX, TM, TO, LPR, CPL, M, C>), dim3((uint32_t)blocks),
+                       dim3(kBlock), 0, stream, (TO *)a.out, (TX *)a.res, (const TX *)a.x,
+                       (const TM *)a.mixed, (const TO *)a.z, (const TO *)a.w, a.rows, a.map,
+                       (float)a.width, a.eps);
     return launch_status();
 }
 
-// Fast-path shapes by C = chunks per row: a lane holds 2 chunks (32 bytes in
-// flight) for rows of up to 64 chunks and 4 chunks (64 bytes) for 128- and
-// 256-chunk rows, which measured fastest on MI355X; wider rows use all 64
-// lanes with C/64 chunks each.  kNoFastPath when no instantiation matches.
-template <typename T, Mode M, bool C>
-int32_t dispatch_fast(T *out, T *res, const T *x, const T *mixed, const T *z, const T *w,
-                      int64_t rows, const RowMap &map, int64_t width, float eps,
-                      hipStream_t stream) {
-    const int64_t chunks = width / Elem<T>::kVec;
-#define QDC_FAST(LPR, CPL)                                                                    \
-    case LPR * CPL:                                                                           \
-        return launch_fast<T, LPR, CPL, M, C>(out, res, x, mixed, z, w, rows, map, width, eps, \
-                                              stream);
-    switch (chunks) {
+// Fast-path shapes by G = groups per row: a lane holds 2 groups for rows of up
+// to 64 groups and 4 groups for 128- and 256-group rows (the splits that
+// measured fastest on MI355X); wider rows use all 64 lanes with G/64 groups
+// each.  kNoFastPath when no instantiation matches.
+template <typename TX, typename TM, typename TO, Mode M, bool C>
+int32_t dispatch_fast(const Args &a, hipStream_t stream) {
+    constexpr int V = group_elems<TX, TM, TO>();
+    if (a.width % V) return kNoFastPath;
+#define QDC_FAST(LPR, CPL) \
+    case LPR * CPL:        \
+        return launch_fast<TX, TM, TO, LPR, CPL, M, C>(a, stream);
+    switch (a.width / V) {
         QDC_FAST(1, 1)
         QDC_FAST(1, 2)
         QDC_FAST(2, 2)
@@ -191,35 +214,27 @@ int32_t dispatch_fast(T *out, T *res, const T *x, const T *mixed, const T *z, co
 #undef QDC_FAST
 }
 
-template <typename T, Mode M, bool C>
-int32_t run(T *out, T *res, const T *x, const T *mixed, const T *z, const T *w, int64_t rows,
-            const RowMap &map, int64_t width, float eps, bool fast, hipStream_t stream) {
-    if (fast && width % Elem<T>::kVec == 0) {
-        const int32_t rc = dispatch_fast<T, M, C>(out, res, x, mixed, z, w, rows, map, width, eps,
-                                                  stream);
+template <typename TX, typename TM, typename TO, Mode M, bool C>
+int32_t run(const Args &a, hipStream_t stream) {
+    if (a.fast) {
+        const int32_t rc = dispatch_fast<TX, TM, TO, M, C>(a, stream);
         if (rc != kNoFastPath) return rc;
     }
-    const int64_t blocks = ceil_div(rows, kBlock / kWave);
-    hipLaunchKernelGGL((rms_rows_general<T, M, C>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
-                       out, res, x, mixed, z, w, rows, map, width, eps);
+    const int64_t blocks = ceil_div(a.rows, kBlock / kWave);
+    hipLaunchKernelGGL((rms_rows_general<TX, TM, TO, M, C>), dim3((uint32_t)blocks), dim3(kBlock),
+                       0, stream, (TO *)a.out, (TX *)a.res, (const TX *)a.x, (const TM *)a.mixed,
+                       (const TO *)a.z, (const TO *)a.w, a.rows, a.map, a.width, a.eps);
     return launch_status();
-}
-
-template <Mode M, bool C>
-int32_t run_dtype(int32_t dtype, void *out, void *res, const void *x, const void *mixed,
-                  const void *z, const void *w, int64_t rows, const RowMap &map, int64_t width,
-                  float eps, bool fast, hipStream_t stream) {
-    if (dtype == QDC_BF16)
-        return run<bf16_t, M, C>((bf16_t *)out, (bf16_t *)res, (const bf16_t *)x,
-                                 (const bf16_t *)mixed, (const bf16_t *)z, (const bf16_t *)w, rows,
-                                 map, width, eps, fast, stream);
-    return run<float, M, C>((float *)out, (float *)res, (const float *)x, (const float *)mixed,
-                            (const float *)z, (const float *)w, rows, map, width, eps, fast,
-                            stream);
 }
 
 // Rows are addressed with 32-bit row indices in the kernels.
 constexpr int64_t kMaxRows = (int64_t)1 << 31;
+
+bool all16(std::initializer_list<const void *> ptrs) {
+    for (const void *p : ptrs)
+        if (!aligned16(p)) return false;
+    return true;
+}
 
 }  // namespace
 }  // namespace qdc
@@ -228,46 +243,69 @@ using namespace qdc;
 
 extern "C" int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows,
                                int64_t width, int64_t ld_x, int64_t ld_out, float eps,
-                               int32_t centered, int32_t dtype, hipStream_t stream) {
-    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
+                               int32_t centered, int32_t x_dtype, int32_t out_dtype,
+                               hipStream_t stream) {
+    if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return QDC_ERR_DTYPE;
+    if (x_dtype == QDC_BF16 && out_dtype == QDC_F32) return QDC_ERR_DTYPE;
     if (rows < 0 || width < 0 || rows >= kMaxRows) return QDC_ERR_SHAPE;
     if (rows == 0 || width == 0) return QDC_OK;
     if (!out || !x || !weight) return QDC_ERR_NULL;
     if (ld_x < width || ld_out < width) return QDC_ERR_SHAPE;
-    const int64_t es = elem_size(dtype);
-    if (out != x && overlaps(out, ((rows - 1) * ld_out + width) * es, x,
-                             ((rows - 1) * ld_x + width) * es))
+    const int64_t ex = elem_size(x_dtype), eo = elem_size(out_dtype);
+    const int64_t span_x = ((rows - 1) * ld_x + width) * ex;
+    const int64_t span_o = ((rows - 1) * ld_out + width) * eo;
+    // in place: the same buffer, element type and stride
+    if (out == x ? (ld_out != ld_x || ex != eo) : overlaps(out, span_o, x, span_x))
         return QDC_ERR_ALIAS;
-    if (out == x && ld_out != ld_x) return QDC_ERR_ALIAS;
-    RowMap map{make_fastdiv(1), ld_x, 0, 0, 0, ld_out, 0};
-    const bool fast = aligned16(out) && aligned16(x) && aligned16(weight) &&
-                      (ld_x * es) % 16 == 0 && (ld_out * es) % 16 == 0;
-    if (centered)
-        return run_dtype<Mode::kPlain, true>(dtype, out, nullptr, x, nullptr, nullptr, weight, rows,
-                                             map, width, eps, fast, stream);
-    return run_dtype<Mode::kPlain, false>(dtype, out, nullptr, x, nullptr, nullptr, weight, rows,
-                                          map, width, eps, fast, stream);
+    const Args a{out, nullptr, x, nullptr, nullptr, weight, rows, width,
+                 RowMap{make_fastdiv(1), ld_x, 0, 0, 0, ld_out, 0}, eps,
+                 all16({out, x, weight}) && (ld_x * ex) % 16 == 0 && (ld_out * eo) % 16 == 0};
+    if (centered) {
+        if (x_dtype == QDC_BF16) return run<bf16_t, bf16_t, bf16_t, Mode::kPlain, true>(a, stream);
+        if (out_dtype == QDC_BF16) return run<float, float, bf16_t, Mode::kPlain, true>(a, stream);
+        return run<float, float, float, Mode::kPlain, true>(a, stream);
+    }
+    if (x_dtype == QDC_BF16) return run<bf16_t, bf16_t, bf16_t, Mode::kPlain, false>(a, stream);
+    if (out_dtype == QDC_BF16) return run<float, float, bf16_t, Mode::kPlain, false>(a, stream);
+    return run<float, float, float, Mode::kPlain, false>(a, stream);
 }
 
 extern "C" int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x,
                                         const void *mixed, const void *weight, int64_t rows,
-                                        int64_t width, float eps, int32_t dtype,
+                                        int64_t width, float eps, int32_t residual_dtype,
+                                        int32_t mixed_dtype, int32_t out_dtype,
                                         hipStream_t stream) {
-    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
+    if (!valid_dtype(residual_dtype) || !valid_dtype(mixed_dtype) || !valid_dtype(out_dtype))
+        return QDC_ERR_DTYPE;
+    const bool all_f32 =
+        residual_dtype == QDC_F32 && mixed_dtype == QDC_F32 && out_dtype == QDC_F32;
+    const bool all_bf16 =
+        residual_dtype == QDC_BF16 && mixed_dtype == QDC_BF16 && out_dtype == QDC_BF16;
+    // an fp32 residual stream may take a bf16 or fp32 addend and write either output
+    const bool f32_stream = residual_dtype == QDC_F32;
+    if (!all_bf16 && !f32_stream) return QDC_ERR_DTYPE;
     if (rows < 0 || width < 0 || rows >= kMaxRows) return QDC_ERR_SHAPE;
     if (rows == 0 || width == 0) return QDC_OK;
     if (!residual || !out || !x || !mixed || !weight) return QDC_ERR_NULL;
-    const int64_t bytes = rows * width * elem_size(dtype);
-    if (overlaps(residual, bytes, out, bytes)) return QDC_ERR_ALIAS;
-    for (const void *in : {x, mixed}) {
-        if (residual != in && overlaps(residual, bytes, in, bytes)) return QDC_ERR_ALIAS;
-        if (out != in && overlaps(out, bytes, in, bytes)) return QDC_ERR_ALIAS;
-    }
-    RowMap map{make_fastdiv(1), width, 0, 0, 0, width, 0};
-    const bool fast = aligned16(residual) && aligned16(out) && aligned16(x) && aligned16(mixed) &&
-                      aligned16(weight) && (width * elem_size(dtype)) % 16 == 0;
-    return run_dtype<Mode::kResidual, true>(dtype, out, residual, x, mixed, nullptr, weight, rows,
-                                            map, width, eps, fast, stream);
+    const int64_t br = rows * width * elem_size(residual_dtype);
+    const int64_t bm = rows * width * elem_size(mixed_dtype);
+    const int64_t bo = rows * width * elem_size(out_dtype);
+    // in place means the same buffer in the same element type
+    if (overlaps(residual, br, out, bo)) return QDC_ERR_ALIAS;
+    if (residual != x && overlaps(residual, br, x, br)) return QDC_ERR_ALIAS;
+    if (residual == mixed ? residual_dtype != mixed_dtype : overlaps(residual, br, mixed, bm))
+        return QDC_ERR_ALIAS;
+    if (out == x ? out_dtype != residual_dtype : overlaps(out, bo, x, br)) return QDC_ERR_ALIAS;
+    if (out == mixed ? out_dtype != mixed_dtype : overlaps(out, bo, mixed, bm))
+        return QDC_ERR_ALIAS;
+    const Args a{out, residual, x, mixed, nullptr, weight, rows, width,
+                 RowMap{make_fastdiv(1), width, 0, 0, 0, width, 0}, eps,
+                 all16({residual, out, x, mixed, weight})};
+    if (all_f32) return run<float, float, float, Mode::kResidual, true>(a, stream);
+    if (all_bf16) return run<bf16_t, bf16_t, bf16_t, Mode::kResidual, true>(a, stream);
+    if (mixed_dtype == QDC_F32) return run<float, float, bf16_t, Mode::kResidual, true>(a, stream);
+    if (out_dtype == QDC_BF16) return run<float, bf16_t, bf16_t, Mode::kResidual, true>(a, stream);
+    return run<float, bf16_t, float, Mode::kResidual, true>(a, stream);
 }
 
 extern "C" int32_t qdc_gated_rmsnorm(void *out, const void *x, const void *z, const void *weight,
@@ -286,11 +324,14 @@ extern "C" int32_t qdc_gated_rmsnorm(void *out, const void *x, const void *z, co
     if (out != x && overlaps(out, span_o, x, ((tokens - 1) * x_tok + heads * width) * es))
         return QDC_ERR_ALIAS;
     if (out == x && out_tok != x_tok) return QDC_ERR_ALIAS;
-    if (overlaps(out, span_o, z, ((tokens - 1) * z_tok + heads * width) * es)) return QDC_ERR_ALIAS;
-    RowMap map{make_fastdiv((uint32_t)heads), x_tok, width, z_tok, width, out_tok, width};
-    const bool fast = aligned16(out) && aligned16(x) && aligned16(z) && aligned16(weight) &&
-                      (width * es) % 16 == 0 && (x_tok * es) % 16 == 0 &&
-                      (z_tok * es) % 16 == 0 && (out_tok * es) % 16 == 0;
-    return run_dtype<Mode::kGated, false>(dtype, out, nullptr, x, nullptr, z, weight,
-                                          tokens * heads, map, width, eps, fast, stream);
+    if (overlaps(out, span_o, z, ((tokens - 1) * z_tok + heads * width) * es))
+        return QDC_ERR_ALIAS;
+    const Args a{out, nullptr, x, nullptr, z, weight, tokens * heads, width,
+                 RowMap{make_fastdiv((uint32_t)heads), x_tok, width, z_tok, width, out_tok, width},
+                 eps,
+                 all16({out, x, z, weight}) && (width * es) % 16 == 0 &&
+                     (x_tok * es) % 16 == 0 && (z_tok * es) % 16 == 0 &&
+                     (out_tok * es) % 16 == 0};
+    if (dtype == QDC_BF16) return run<bf16_t, bf16_t, bf16_t, Mode::kGated, false>(a, stream);
+    return run<float, float, float, Mode::kGated, false>(a, stream);
 }

@@ -29,8 +29,9 @@ SIGNATURES = {
     "qdc_status_string": (ctypes.c_char_p, [_i32]),
     "qdc_embedding_gather": (_i32, [_vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _vp]),
     "qdc_check_ids": (_i32, [_vp, _i64, _i64]),
-    "qdc_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _vp]),
-    "qdc_residual_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
+    "qdc_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _vp]),
+    "qdc_residual_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _i32,
+                                    _vp]),
     "qdc_qk_norm_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 16
                          + [_f32, _i32, _vp]),
     "qdc_rope_tables": (_i32, [_vp, _vp, _i64, _i64, _f32]),

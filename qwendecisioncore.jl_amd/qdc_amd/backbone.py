@@ -1,0 +1,286 @@
+"""``backbone_hidden`` on MI355X with the fused row kernels.
+
+Mirrors the reference's public entry points and their validation:
+
+* :class:`QwenBackbone` -- ``QwenBackbone(dir; device=:amdgpu)`` (``src/backbone.jl:74-192``):
+  weights uploaded once, projection weights stored transposed and packed
+  (``[q; k; v]``, ``[qkv; z; a; b]``, ``[gate; up]``) the way the reference's AMDGPU
+  extension packs them (``ext/amdgpu_mlp.jl:15-52``).
+* :func:`backbone_hidden` / :func:`backbone_last_hidden` (``src/backbone.jl:433-501``):
+  one sequence per call, ids checked on the host (``check_sequence`` :413-422).
+* :func:`batch_backbone_hidden`: the optional batched hook (``src/backbone.jl:66-70``),
+  here returning every position of every row.
+
+Per layer (``native_layer``, ``src/backbone.jl:363-388``) the fused kernels do
+the row work: the layer's input RMSNorm is fused with the previous layer's MLP
+residual add (``qdc_residual_rmsnorm``; the last one with the final norm),
+post-attention residual + RMSNorm, q/k norm + partial RoPE read straight out of
+the packed projection, the DeltaNet gated RMSNorm reading z inside the packed
+projection, and SwiGLU reading the packed gate||up GEMM output.  GEMMs, the
+attention softmax/merge and the DeltaNet convolution/recurrence are the
+"existing path" and run as PyTorch-ROCm ops (hipBLASLt GEMMs); attention
+scores are computed in fp32.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .config import BackboneConfig, load_config
+from .weights import read_checkpoint
+
+FLOATMAX = float(np.finfo(np.float32).max)
+
+
+class QwenBackbone:
+    """A Qwen3.5 hybrid backbone resident on one GPU."""
+
+    def __init__(self, cfg: BackboneConfig, weights: dict, device="cuda:0",
+                 dtype: torch.dtype = torch.float32):
+        """``dtype`` is the storage type of weights and GEMM activations; the
+        residual stream and the returned hidden states are fp32 either way."""
+        if dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("dtype must be float32 or bfloat16")
+        self.cfg, self.dtype = cfg, dtype
+        self.device = torch.device(device)
+        self._tables = {}
+
+        def dev(x, dt=None):
+            t = x if isinstance(x, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(x))
+            return t.to(self.device).to(dt or dtype).contiguous()
+
+        def lin(*names):  # packed, transposed [in, out] for y = x @ W
+            return torch.cat([dev(weights[n]) for n in names], 0).t().contiguous()
+
+        self.embedding = dev(weights["embed_tokens.weight"])
+        # the last residual add is fused with the final norm, which writes fp32
+        self.final_norm = dev(weights["norm.weight"], torch.float32)
+        self.layers = []
+        for i, kind in enumerate(cfg.layer_types):
+            p = f"layers.{i}."
+            layer = {
+                "kind": kind,
+                "input_norm": dev(weights[p + "input_layernorm.weight"]),
+                "post_norm": dev(weights[p + "post_attention_layernorm.weight"]),
+                "gate_up": lin(p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"),
+                "down": lin(p + "mlp.down_proj.weight"),
+            }
+            if kind == "full_attention":
+                a = p + "self_attn."
+                layer.update(qkv=lin(a + "q_proj.weight", a + "k_proj.weight", a + "v_proj.weight"),
+                             out=lin(a + "o_proj.weight"), q_norm=dev(weights[a + "q_norm.weight"]),
+                             k_norm=dev(weights[a + "k_norm.weight"]))
+            elif kind == "linear_attention":
+                a = p + "linear_attn."
+                conv = weights[a + "conv1d.weight"]
+                conv = conv if isinstance(conv, torch.Tensor) else torch.from_numpy(np.asarray(conv))
+                a_log = weights[a + "A_log"]
+                a_log = a_log if isinstance(a_log, torch.Tensor) else torch.from_numpy(np.asarray(a_log))
+                layer.update(
+                    proj=lin(a + "in_proj_qkv.weight", a + "in_proj_z.weight",
+                             a + "in_proj_a.weight", a + "in_proj_b.weight"),
+                    conv=dev(conv.reshape(conv.shape[0], 1, conv.shape[-1]), torch.float32),
+                    # fixed decay multiplier, computed once in fp32 (src/backbone.jl:160-162)
+                    a_decay=(-1.0 * torch.exp(a_log.to(torch.float32))).to(self.device),
+                    dt_bias=dev(weights[a + "dt_bias"], torch.float32),
+                    norm=dev(weights[a + "norm.weight"]),
+                    out=lin(a + "out_proj.weight"))
+            else:
+                raise ValueError(f"Unsupported layer type {kind}.")
+            self.layers.append(layer)
+
+    @classmethod
+    def from_weights(cls, weights: dict, cfg: BackboneConfig, device="cuda:0",
+                     dtype: torch.dtype = torch.float32) -> "QwenBackbone":
+        return cls(cfg, weights, device, dtype)
+
+    @classmethod
+    def from_directory(cls, directory: str, device="cuda:0",
+                       dtype: torch.dtype = torch.float32) -> "QwenBackbone":
+        """A local safetensors checkpoint directory (no network access)."""
+        cfg = load_config(directory)
+        weights = read_checkpoint(directory)
+        cfg = BackboneConfig(**{**cfg.as_dict(), "vocab": weights["embed_tokens.weight"].shape[0],
+                                "intermediate": weights["layers.0.mlp.gate_proj.weight"].shape[0],
+                                "layer_types": cfg.layer_types})
+        return cls(cfg, weights, device, dtype)
+
+    def _mm32(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        """A GEMM whose result feeds the fp32 residual stream: fp32 output even
+        from bf16 operands (hipBLASLt accumulates in fp32 either way)."""
+        if a.dtype == torch.float32:
+            return a @ b
+        return torch.mm(a, b, out_dtype=torch.float32)
+
+    @property
+    def vocab(self) -> int:
+        return self.embedding.shape[0]
+
+    def rope_tables(self, seq_len: int):
+        key = seq_len
+        if key not in self._tables:
+            self._tables[key] = ops.rope_tables(seq_len, self.cfg.rotary_dim, self.cfg.rope_theta,
+                                                self.device)
+        return self._tables[key]
+
+    # ------------------------------------------------------------ forward --
+    @torch.no_grad()
+    def forward(self, ids: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """Final-normalised hidden states ``[B*S, hidden]`` (device, fp32)
+        for device ids ``[B, S]`` (int32) and mask ``[B, S]`` (0/1)."""
+        B, S = ids.shape
+        cfg = self.cfg
+        # residual stream h in fp32 (a bf16 table widens exactly while gathered)
+        h = ops.native_gather(self.embedding, ids.reshape(-1).contiguous(), out_dtype=torch.float32)
+        normed = ops.native_rms(h, self.layers[0]["input_norm"], cfg.eps)
+        maskf = mask.to(torch.float32)
+        for i, layer in enumerate(self.layers):
+            if layer["kind"] == "full_attention":
+                mixed = self._full_attention(layer, normed, maskf, B, S)
+            else:
+                mixed = self._delta_attention(layer, normed, maskf, B, S)
+            residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps)
+            gate_up = normed @ layer["gate_up"]
+            inter = gate_up.shape[1] // 2
+            act = ops.native_mlp_gate(gate_up[:, :inter], gate_up[:, inter:])
+            down = self._mm32(act, layer["down"])
+            nxt = self.layers[i + 1]["input_norm"] if i + 1 < len(self.layers) else self.final_norm
+            # residual add of the MLP fused with the next RMSNorm
+            h, normed = ops.native_residual_rms(residual, down, nxt, cfg.eps)
+        return normed
+
+    def _full_attention(self, layer, x, maskf, B, S):
+        """``full_attention`` (``src/backbone.jl:224-262``)."""
+        cfg = self.cfg
+        hd, H, KV = cfg.head_dim, cfg.heads, cfg.kv_heads
+        T = B * S
+        proj = x @ layer["qkv"]                              # [T, 2*hd*H + 2*hd*KV]
+        qgate = proj[:, :2 * hd * H].view(T, H, 2 * hd)
+        k_in = proj[:, 2 * hd * H:2 * hd * H + hd * KV].view(T, KV, hd)
+        v = proj[:, 2 * hd * H + hd * KV:].view(T, KV, hd)
+        q, k = ops.prepare_heads(qgate[:, :, :hd], k_in, layer["q_norm"], layer["k_norm"],
+                                 self.rope_tables(S) if cfg.rotary_dim else None, cfg.rotary_dim,
+                                 cfg.eps, seq_len=S)
+        groups = H // KV
+        qf = q.float().view(B, S, H, hd).permute(0, 2, 1, 3).contiguous()
+        kf = k.float().view(B, S, KV, hd).permute(0, 2, 1, 3).repeat_interleave(groups, 1)
+        vf = v.float().view(B, S, KV, hd).permute(0, 2, 1, 3).repeat_interleave(groups, 1)
+        scores = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) / math.sqrt(hd)
+        # key i is visible to query j when i <= j and mask[i] == 1 (src/backbone.jl:237-242)
+        keys = torch.arange(S, device=x.device)
+        allowed = (keys[None, :] <= keys[:, None])[None] & (maskf[:, None, :] == 1)
+        scores = scores + torch.where(allowed, 0.0, -FLOATMAX)[:, None]
+        probs = torch.softmax(scores, dim=-1)
+        values = torch.matmul(probs, vf.contiguous())        # [B, H, S, hd]
+        gate = torch.sigmoid(qgate[:, :, hd:].float())       # [T, H, hd]
+        merged = values.permute(0, 2, 1, 3).reshape(T, H, hd) * gate
+        return self._mm32(merged.reshape(T, H * hd).to(self.dtype), layer["out"])
+
+    def _delta_attention(self, layer, x, maskf, B, S):
+        """Gated DeltaNet (``src/backbone.jl:284-345``; recurrent form
+        ``src/backbone_cpu.jl:680-759``)."""
+        cfg = self.cfg
+        kd, kh, vd, vh = cfg.key_dim, cfg.key_heads, cfg.value_dim, cfg.value_heads
+        T = B * S
+        kw, vw = kd * kh, vd * vh
+        cq = 2 * kw + vw
+        masked = x * maskf.reshape(T, 1).to(x.dtype)
+        proj = masked @ layer["proj"]                        # [T, cq + vw + 2*vh]
+        conv_in = proj[:, :cq].float().view(B, S, cq).transpose(1, 2)
+        K = layer["conv"].shape[-1]
+        mixed = F.silu(F.conv1d(conv_in, layer["conv"], padding=K - 1, groups=cq)[..., :S])
+        mixed = mixed.transpose(1, 2)                        # [B, S, cq] fp32
+        q = mixed[..., :kw].reshape(B, S, kh, kd)
+        k = mixed[..., kw:2 * kw].reshape(B, S, kh, kd)
+        v = mixed[..., 2 * kw:].reshape(B, S, vh, vd)
+        q = q / (torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6) * math.sqrt(kd))
+        k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+        a_in = proj[:, cq + vw:cq + vw + vh].float().view(B, S, vh)
+        b_in = proj[:, cq + vw + vh:].float().view(B, S, vh)
+        beta = torch.sigmoid(b_in)
+        decay = layer["a_decay"] * F.softplus(a_in + layer["dt_bias"])
+        groups = vh // kh
+        kx = k.repeat_interleave(groups, 2)                  # [B, S, vh, kd]
+        qx = q.repeat_interleave(groups, 2)
+        result = delta_recurrence(qx, kx, v, beta, decay)   # [B, S, vh, vd] fp32
+        z = proj[:, cq:cq + vw].view(T, vh, vd)
+        out = ops.native_gated_rms(result.reshape(T, vh, vd).to(self.dtype), z, layer["norm"],
+                                   cfg.eps)
+        return self._mm32(out.view(T, vw), layer["out"])
+
+
+def delta_recurrence(q, k, v, beta, decay):
+    """Gated delta rule, token by token (``cpu_delta_recurrent_step!``,
+    ``src/backbone_cpu.jl:681-705``): with f = exp(decay),
+    u = beta*(v - f*S k); S = f*S + u k^T; out = S q.  Shapes [B, S, H, d]."""
+    B, S, H, kd = k.shape
+    vd = v.shape[-1]
+    state = torch.zeros(B, H, vd, kd, dtype=torch.float32, device=k.device)
+    out = torch.empty(B, S, H, vd, dtype=torch.float32, device=k.device)
+    factors = torch.exp(decay)
+    for t in range(S):
+        f = factors[:, t, :, None]                           # [B, H, 1]
+        kt, qt = k[:, t], q[:, t]                            # [B, H, kd]
+        pred = torch.matmul(state, kt[..., None])[..., 0]    # [B, H, vd]
+        u = beta[:, t, :, None] * (v[:, t] - f * pred)
+        state = f[..., None] * state + u[..., None] * kt[:, :, None, :]
+        out[:, t] = torch.matmul(state, qt[..., None])[..., 0]
+    return out
+
+
+# ---------------------------------------------------------------- API -------
+def check_sequence(model: QwenBackbone, ids, mask) -> None:
+    """``check_sequence`` (``src/backbone.jl:413-422``), ValueError for ArgumentError."""
+    ids = np.asarray(ids)
+    mask = np.asarray(mask)
+    if ids.size != mask.size:
+        raise ValueError("Input IDs and mask must have identical lengths.")
+    if ids.size == 0:
+        raise ValueError("Inputs must not be empty.")
+    ops.check_ids(ids, model.vocab)
+    if not np.isin(mask, (0, 1)).all():
+        raise ValueError("Mask values must be zero or one.")
+
+
+def _device_inputs(model, ids, mask):
+    ids = np.asarray(ids, dtype=np.int64)
+    mask = np.asarray(mask, dtype=np.int64)
+    if ids.ndim == 2:
+        if ids.shape[0] != 1 or mask.shape[0] != 1:
+            raise ValueError("Pass one sequence per call; batching is not implemented yet.")
+        ids, mask = ids[0], mask[0]
+    check_sequence(model, ids, mask)
+    d_ids = torch.from_numpy(ids.astype(np.int32)).to(model.device).view(1, -1)
+    d_mask = torch.from_numpy(mask.astype(np.int32)).to(model.device).view(1, -1)
+    return d_ids, d_mask
+
+
+def backbone_hidden(model: QwenBackbone, ids, mask, positions=None) -> np.ndarray:
+    """Final-normalised hidden states ``[len(ids), hidden]`` (fp32, host) of one
+    sequence; ``positions`` (1-based) selects rows as the reference does."""
+    d_ids, d_mask = _device_inputs(model, ids, mask)
+    states = model.forward(d_ids, d_mask).float().cpu().numpy()
+    if positions is None:
+        return states
+    positions = np.asarray(positions, dtype=np.int64)
+    if positions.size and (positions.min() < 1 or positions.max() > states.shape[0]):
+        raise ValueError("Position is outside the sequence.")
+    return states[positions - 1]
+
+
+def backbone_last_hidden(model: QwenBackbone, ids, mask) -> np.ndarray:
+    """Final-normalised hidden state of the last position (``src/backbone.jl:470-490``)."""
+    return backbone_hidden(model, ids, mask)[-1]
+
+
+def batch_backbone_hidden(model: QwenBackbone, ids: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """Every position of ``B`` equal-length sequences at once: device int32 ids
+    ``[B, S]`` and 0/1 mask ``[B, S]`` -> ``[B, S, hidden]`` on the device.  RoPE
+    positions restart at 0 for every row.  Ids are not re-checked here: device
+    ids outside the vocabulary gather zero rows (see ``ops.native_gather``)."""
+    B, S = ids.shape
+    return model.forward(ids.to(torch.int32).contiguous(), mask).view(B, S, -1)

@@ -118,28 +118,38 @@ def native_gather(embedding: torch.Tensor, ids, out: torch.Tensor | None = None,
 # ------------------------------------------------------------------ norms ---
 def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool = True,
                out: torch.Tensor | None = None) -> torch.Tensor:
-    """RMSNorm over the last axis: ``(x*s)*(1+w)`` (centred) or ``(x*s)*w``."""
+    """RMSNorm over the last axis: ``(x*s)*(1+w)`` (centred) or ``(x*s)*w``.
+
+    The output takes the weight's dtype, so an fp32 ``x`` with a bf16 weight
+    gives a bf16 result (an fp32 residual stream feeding bf16 GEMMs)."""
     _device(x, weight)
-    code = _dtype_code(x, weight)
+    if x.dtype not in _DTYPES or weight.dtype not in _DTYPES:
+        raise ValueError("x and weight must be float32 or bfloat16")
     rows, width, ld_x = _rows_view(x)
     if weight.numel() != width or not weight.is_contiguous():
         raise ValueError("weight must be a contiguous vector of the row width")
     if out is None:
-        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    if out.shape != x.shape:
-        raise ValueError("out must have the shape of x")
-    orows, _, ld_out = _rows_view(out)
+        out = torch.empty(x.shape, dtype=weight.dtype, device=x.device)
+    if out.shape != x.shape or out.dtype != weight.dtype:
+        raise ValueError("out must have the shape of x and the dtype of weight")
+    _, _, ld_out = _rows_view(out)
     check(lib().qdc_rmsnorm(out.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, width, ld_x,
-                            ld_out, eps, int(bool(centered)), code, _stream(x)), "native_rms")
+                            ld_out, eps, int(bool(centered)), _DTYPES[x.dtype],
+                            _DTYPES[weight.dtype], _stream(x)), "native_rms")
     return out
 
 
 def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tensor, eps: float,
                         residual: torch.Tensor | None = None,
                         out: torch.Tensor | None = None):
-    """``residual = x + mixed``; returns ``(residual, rms(residual))`` in one pass."""
+    """``residual = x + mixed``; returns ``(residual, rms(residual))`` in one pass.
+
+    ``residual`` has x's dtype, the normalised output the weight's dtype;
+    ``mixed`` may be bf16 while x is fp32 (fp32 residual stream)."""
     _device(x, mixed, weight)
-    code = _dtype_code(x, mixed, weight)
+    for t in (x, mixed, weight):
+        if t.dtype not in _DTYPES:
+            raise ValueError("tensors must be float32 or bfloat16")
     if x.shape != mixed.shape or not x.is_contiguous() or not mixed.is_contiguous():
         raise ValueError("x and mixed must be contiguous tensors of one shape")
     width = x.shape[-1]
@@ -147,13 +157,15 @@ def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tens
     if weight.numel() != width:
         raise ValueError("weight must be a vector of the row width")
     residual = torch.empty_like(x) if residual is None else residual
-    out = torch.empty_like(x) if out is None else out
-    for t in (residual, out):
-        if t.shape != x.shape or not t.is_contiguous() or t.dtype != x.dtype:
-            raise ValueError("residual/out must be contiguous tensors like x")
+    out = torch.empty(x.shape, dtype=weight.dtype, device=x.device) if out is None else out
+    if residual.shape != x.shape or not residual.is_contiguous() or residual.dtype != x.dtype:
+        raise ValueError("residual must be a contiguous tensor like x")
+    if out.shape != x.shape or not out.is_contiguous() or out.dtype != weight.dtype:
+        raise ValueError("out must be contiguous, shaped like x, of the weight's dtype")
     check(lib().qdc_residual_rmsnorm(residual.data_ptr(), out.data_ptr(), x.data_ptr(),
-                                     mixed.data_ptr(), weight.data_ptr(), rows, width, eps, code,
-                                     _stream(x)), "native_residual_rms")
+                                     mixed.data_ptr(), weight.data_ptr(), rows, width, eps,
+                                     _DTYPES[x.dtype], _DTYPES[mixed.dtype],
+                                     _DTYPES[weight.dtype], _stream(x)), "native_residual_rms")
     return residual, out
 
 

@@ -69,25 +69,30 @@ def test_check_ids():
 def test_rmsnorm_validation():
     lib = _lib.lib()
     rms = lambda *a: lib.qdc_rmsnorm(*a, None)  # noqa: E731
-    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, 7) == -3
-    assert rms(FAKE, FAKE, FAKE, -1, 8, 8, 8, 1e-6, 1, F32) == -2
-    assert rms(FAKE, FAKE, FAKE, 4, 8, 4, 8, 1e-6, 1, F32) == -2  # ld < width
-    assert rms(None, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32) == -1
-    assert rms(FAKE, FAKE, None, 4, 8, 8, 8, 1e-6, 1, BF16) == -1
-    assert rms(None, None, None, 0, 8, 8, 8, 1e-6, 1, F32) == 0  # nothing to do
-    assert rms(FAKE + 16, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32) == -5  # partial overlap
-    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 16, 1e-6, 1, F32) == -5  # in place, other stride
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, 7, F32) == -3
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, BF16, F32) == -3  # bf16 -> f32 not offered
+    assert rms(FAKE, FAKE, FAKE, -1, 8, 8, 8, 1e-6, 1, F32, F32) == -2
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 4, 8, 1e-6, 1, F32, F32) == -2  # ld < width
+    assert rms(None, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32, F32) == -1
+    assert rms(FAKE, FAKE, None, 4, 8, 8, 8, 1e-6, 1, BF16, BF16) == -1
+    assert rms(None, None, None, 0, 8, 8, 8, 1e-6, 1, F32, F32) == 0  # nothing to do
+    assert rms(FAKE + 16, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32, F32) == -5  # partial overlap
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 16, 1e-6, 1, F32, F32) == -5  # in place, other stride
+    assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32, BF16) == -5  # in place, other type
 
 
 def test_residual_validation():
     lib = _lib.lib()
     f = lambda *a: lib.qdc_residual_rmsnorm(*a, None)  # noqa: E731
     A, B, C, D, W = FAKE, FAKE * 2, FAKE * 3, FAKE * 4, FAKE * 5
-    assert f(A, B, C, D, W, 4, 8, 1e-6, 9) == -3
-    assert f(A, B, C, None, W, 4, 8, 1e-6, F32) == -1
-    assert f(A, A, C, D, W, 4, 8, 1e-6, F32) == -5  # residual and out coincide
-    assert f(A, B, A + 4, D, W, 4, 8, 1e-6, F32) == -5  # residual overlaps x partially
-    assert f(A, B, C, D, W, 0, 8, 1e-6, F32) == 0
+    assert f(A, B, C, D, W, 4, 8, 1e-6, 9, F32, F32) == -3
+    assert f(A, B, C, D, W, 4, 8, 1e-6, BF16, F32, F32) == -3  # bf16 stream, f32 addend
+    assert f(A, B, C, D, W, 4, 8, 1e-6, BF16, BF16, F32) == -3  # bf16 stream, f32 output
+    assert f(A, B, C, None, W, 4, 8, 1e-6, F32, F32, F32) == -1
+    assert f(A, A, C, D, W, 4, 8, 1e-6, F32, F32, F32) == -5  # residual and out coincide
+    assert f(A, B, A + 4, D, W, 4, 8, 1e-6, F32, F32, F32) == -5  # residual overlaps x partially
+    assert f(A, B, C, B, W, 4, 8, 1e-6, F32, BF16, F32) == -5  # out on mixed of another type
+    assert f(A, B, C, D, W, 0, 8, 1e-6, F32, F32, F32) == 0
 
 
 def test_gated_validation():

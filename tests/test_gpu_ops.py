@@ -280,3 +280,35 @@ def test_gather_checks_and_device_ids():
     got = out.cpu().numpy()
     assert np.array_equal(got[0], exp[3]) and np.array_equal(got[2], exp[5])
     assert not got[1].any() and not got[3].any()
+
+
+# ------------------------------------------- fp32 residual stream mixes ------
+@pytest.mark.parametrize("rows,width", [(16384, 1024), (33, 256), (5, 1000)])
+def test_rmsnorm_fp32_to_bf16(rows, width):
+    """fp32 rows normalised into a bf16 output with a bf16 weight."""
+    from qdc_amd import ops
+    x = host((rows, width), 27, 1.0)
+    w = host((width,), 28, 0.02, torch.bfloat16)
+    got = ops.native_rms(dev(x, torch.float32), dev(w, torch.bfloat16), 1e-6)
+    assert got.dtype == torch.bfloat16
+    report(f"rms f32->bf16 {rows}x{width}", back(got), O.rms(x, w, 1e-6), torch.bfloat16)
+
+
+@pytest.mark.parametrize("mixed_dtype,out_dtype", [(torch.bfloat16, torch.bfloat16),
+                                                    (torch.bfloat16, torch.float32),
+                                                    (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("rows,width", [(16384, 1024), (65, 256), (3, 3000)])
+def test_residual_rmsnorm_fp32_stream(mixed_dtype, out_dtype, rows, width):
+    """fp32 residual stream + bf16 or fp32 addend -> fp32 residual, normalised
+    output in the weight's dtype (bf16 for the next GEMM, fp32 for the final norm)."""
+    from qdc_amd import ops
+    x = host((rows, width), 29, 1.0)
+    m = host((rows, width), 30, 1.0, mixed_dtype)
+    w = host((width,), 31, 0.02, out_dtype)
+    res, out = ops.native_residual_rms(dev(x, torch.float32), dev(m, mixed_dtype),
+                                       dev(w, out_dtype), 1e-6)
+    assert res.dtype == torch.float32 and out.dtype == out_dtype
+    exp_res, exp_out = O.residual_rms(x, m, w, 1e-6)
+    # x + mixed is one fp32 addition of the same values: bit-exact
+    assert np.array_equal(back(res), exp_res)
+    report(f"residual f32+bf16 -> {out_dtype} {rows}x{width}", back(out), exp_out, out_dtype)

@@ -48,8 +48,8 @@ def test_fixture_input_validation(native_fixture):
 MUTANTS = {
     "rms weight not centred": ("rms", lambda x, w, eps, centered=True:
                                _np_rms(x, w, eps, not centered)),
-    "rms eps outside sqrt": ("rms", lambda x, w, eps, centered=True:
-                             _np_rms(x, w, 0.0, centered) + 0 * eps),
+    "residual rms eps dropped": ("residual_rms", lambda x, m, w, eps:
+                                 (x + m, _np_rms(x + m, w, 0.0, True))),
     "rope sin sign": ("qk_norm_rope", lambda x, w, c, s, rd, eps, seq_len=None, pos_offset=0:
                       _orig["qk_norm_rope"](x, w, c, -s, rd, eps, seq_len, pos_offset)),
     "rope pairs interleaved": ("qk_norm_rope", lambda x, w, c, s, rd, eps, seq_len=None,
