@@ -167,6 +167,23 @@ int32_t qdc_swiglu(void *out, const void *gate, const void *up, int64_t tokens, 
                    int64_t ld_gate, int64_t ld_up, int64_t ld_out, int32_t dtype,
                    hipStream_t stream);
 
+/*
+ * Gated delta rule recurrence of the DeltaNet layers -- the "existing path"
+ * recurrence (delta_recurrent_kernel!, ext/amdgpu_delta.jl:37-81; CPU
+ * cpu_delta_recurrent_step! src/backbone_cpu.jl:681-705), not one of the fused
+ * row kernels; provided so backbone_hidden runs at speed.  Per sequence b and
+ * value head h (key head h / (heads / key_heads)), state S[value_dim, key_dim]
+ * from zero, for t = 0..seq-1:  f = exp(decay);  u = beta*(v - f*S k);
+ * S = f*S + u k^T;  out = S q.  Contiguous fp32 inputs q, k [batch, seq,
+ * key_heads, key_dim] (q already L2-normalised and scaled), v [batch, seq,
+ * heads, value_dim], beta and decay [batch, seq, heads]; out [batch, seq,
+ * heads, value_dim] in out_dtype.  key_dim 1..256.
+ */
+int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, const float *k,
+                       const float *v, const float *beta, const float *decay, int64_t batch,
+                       int64_t seq, int64_t heads, int64_t key_heads, int64_t key_dim,
+                       int64_t value_dim, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

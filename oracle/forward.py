@@ -155,21 +155,32 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
     a_decay = (F32(-1) * np.exp(W[p + "linear_attn.A_log"].astype(F32))).astype(F32)
     decay = (a_decay * _softplus(_store(_linear(masked, W[p + "linear_attn.in_proj_a.weight"]),
                                         bf16) + W[p + "linear_attn.dt_bias"])).astype(F32)
-    groups = vh // kh
-    kidx = np.arange(vh) // groups
-    state = np.zeros((vh, vd, kd), F32)
-    result = np.empty((T, vh, vd), F32)
+    result = delta_recurrence(q, k, v, beta, decay)
+    out = _store(ops.gated_rms(_store(result, bf16), z, W[p + "linear_attn.norm.weight"],
+                               cfg["eps"]), bf16)
+    return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
+
+
+def delta_recurrence(q, k, v, beta, decay):
+    """Gated delta rule, token by token, for one sequence:
+    ``cpu_delta_recurrent_step!`` (``src/backbone_cpu.jl:681-705``) inside
+    ``cpu_delta_recurrent_heads!`` (:710-759).  q, k ``[T, KH, kd]``, v
+    ``[T, H, vd]``, beta and decay ``[T, H]`` -> ``[T, H, vd]`` fp32; value
+    head h reads key head ``h // (H // KH)`` (``cld(head, groups)``, 1-based)."""
+    T, H, vd = v.shape
+    kh, kd = k.shape[1], k.shape[2]
+    kidx = np.arange(H) // (H // kh)
+    state = np.zeros((H, vd, kd), F32)
+    result = np.empty((T, H, vd), F32)
     for t in range(T):
-        factor = np.exp(decay[t]).astype(F32)                     # [vh]
-        kt = k[t, kidx]                                            # [vh, kd]
+        factor = np.exp(decay[t]).astype(F32)                     # [H]
+        kt = k[t, kidx]                                            # [H, kd]
         qt = q[t, kidx]
         proj = np.einsum("hvk,hk->hv", state, kt).astype(F32)
         proj = (beta[t][:, None] * (v[t] - factor[:, None] * proj)).astype(F32)
         state = (factor[:, None, None] * state + proj[:, :, None] * kt[:, None, :]).astype(F32)
         result[t] = np.einsum("hvk,hk->hv", state, qt)
-    out = _store(ops.gated_rms(_store(result, bf16), z, W[p + "linear_attn.norm.weight"],
-                               cfg["eps"]), bf16)
-    return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
+    return result
 
 
 def check_sequence(ids, mask, vocab):

@@ -38,6 +38,8 @@ SIGNATURES = {
     "qdc_gated_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                  _i32, _vp]),
     "qdc_swiglu": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _vp]),
+    "qdc_delta_scan": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                              _i64, _vp]),
 }
 
 _lib = None

@@ -203,33 +203,12 @@ class QwenBackbone:
         b_in = proj[:, cq + vw + vh:].float().view(B, S, vh)
         beta = torch.sigmoid(b_in)
         decay = layer["a_decay"] * F.softplus(a_in + layer["dt_bias"])
-        groups = vh // kh
-        kx = k.repeat_interleave(groups, 2)                  # [B, S, vh, kd]
-        qx = q.repeat_interleave(groups, 2)
-        result = delta_recurrence(qx, kx, v, beta, decay)   # [B, S, vh, vd] fp32
+        # recurrence straight into the model dtype the gated norm reads
+        result = ops.delta_scan(q.contiguous(), k.contiguous(), v.contiguous(),
+                                beta.contiguous(), decay.contiguous(), self.dtype)
         z = proj[:, cq:cq + vw].view(T, vh, vd)
-        out = ops.native_gated_rms(result.reshape(T, vh, vd).to(self.dtype), z, layer["norm"],
-                                   cfg.eps)
+        out = ops.native_gated_rms(result.view(T, vh, vd), z, layer["norm"], cfg.eps)
         return self._mm32(out.view(T, vw), layer["out"])
-
-
-def delta_recurrence(q, k, v, beta, decay):
-    """Gated delta rule, token by token (``cpu_delta_recurrent_step!``,
-    ``src/backbone_cpu.jl:681-705``): with f = exp(decay),
-    u = beta*(v - f*S k); S = f*S + u k^T; out = S q.  Shapes [B, S, H, d]."""
-    B, S, H, kd = k.shape
-    vd = v.shape[-1]
-    state = torch.zeros(B, H, vd, kd, dtype=torch.float32, device=k.device)
-    out = torch.empty(B, S, H, vd, dtype=torch.float32, device=k.device)
-    factors = torch.exp(decay)
-    for t in range(S):
-        f = factors[:, t, :, None]                           # [B, H, 1]
-        kt, qt = k[:, t], q[:, t]                            # [B, H, kd]
-        pred = torch.matmul(state, kt[..., None])[..., 0]    # [B, H, vd]
-        u = beta[:, t, :, None] * (v[:, t] - f * pred)
-        state = f[..., None] * state + u[..., None] * kt[:, :, None, :]
-        out[:, t] = torch.matmul(state, qt[..., None])[..., 0]
-    return out
 
 
 # ---------------------------------------------------------------- API -------

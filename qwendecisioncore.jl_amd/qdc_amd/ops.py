@@ -277,6 +277,27 @@ def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
     return out
 
 
+def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+               decay: torch.Tensor, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Gated delta rule recurrence (the DeltaNet "existing path", not a fused
+    row op): contiguous fp32 q, k ``[B, S, KH, kd]``, v ``[B, S, H, vd]``, beta and
+    decay ``[B, S, H]`` -> ``[B, S, H, vd]`` in ``out_dtype``."""
+    _device(q, k, v, beta, decay)
+    for t in (q, k, v, beta, decay):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("delta_scan inputs must be contiguous float32 tensors")
+    B, S, KH, kd = k.shape
+    H, vd = v.shape[2], v.shape[3]
+    if q.shape != k.shape or v.shape[:2] != (B, S) or beta.shape != (B, S, H) or \
+            decay.shape != (B, S, H):
+        raise ValueError("inconsistent delta_scan shapes")
+    out = torch.empty((B, S, H, vd), dtype=out_dtype, device=q.device)
+    check(lib().qdc_delta_scan(out.data_ptr(), _DTYPES[out_dtype], q.data_ptr(), k.data_ptr(),
+                               v.data_ptr(), beta.data_ptr(), decay.data_ptr(), B, S, H, KH, kd,
+                               vd, _stream(q)), "delta_scan")
+    return out
+
+
 def check_ids(ids: Sequence[int], vocab: int) -> None:
     """Host id check of ``check_sequence`` (``src/backbone.jl:417-418``)."""
     host = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))

@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 10, names
+    assert len(names) == 11, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -150,6 +150,17 @@ def test_qk_norm_rope_validation():
     assert f(q=KI) == -5  # q output on the k input
     assert f(k=Q + 32) == -5  # the two outputs overlap
     assert f(tokens=0) == 0
+
+
+def test_delta_scan_validation():
+    lib = _lib.lib()
+    f = lambda *a: lib.qdc_delta_scan(*a, None)  # noqa: E731
+    P = FAKE
+    assert f(P, 7, P, P, P, P, P, 1, 4, 2, 1, 128, 128) == -3
+    assert f(P, F32, P, P, P, P, P, 1, 4, 3, 2, 128, 128) == -2  # heads not a multiple
+    assert f(P, F32, P, P, P, P, P, 1, 4, 2, 1, 320, 128) == -2  # key_dim above 256
+    assert f(P, F32, P, None, P, P, P, 1, 4, 2, 1, 128, 128) == -1
+    assert f(None, F32, None, None, None, None, None, 0, 4, 2, 1, 128, 128) == 0
 
 
 @pytest.mark.timeout(300)

@@ -312,3 +312,26 @@ def test_residual_rmsnorm_fp32_stream(mixed_dtype, out_dtype, rows, width):
     # x + mixed is one fp32 addition of the same values: bit-exact
     assert np.array_equal(back(res), exp_res)
     report(f"residual f32+bf16 -> {out_dtype} {rows}x{width}", back(out), exp_out, out_dtype)
+
+
+# ------------------------------------------------ DeltaNet recurrence --------
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,S,KH,H,kd,vd", [(2, 37, 2, 4, 128, 128), (1, 5, 1, 2, 64, 20),
+                                            (3, 64, 16, 16, 128, 128), (1, 9, 1, 1, 256, 8),
+                                            (2, 65, 1, 2, 2, 2), (1, 17, 2, 6, 96, 33)])
+def test_delta_scan(out_dtype, B, S, KH, H, kd, vd):
+    from oracle import forward
+    from qdc_amd import ops
+    rng = np.random.default_rng(32)
+    q = rng.standard_normal((B, S, KH, kd), dtype=np.float32)
+    k = rng.standard_normal((B, S, KH, kd), dtype=np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True) * np.float32(np.sqrt(kd))
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((B, S, H, vd), dtype=np.float32)
+    beta = rng.random((B, S, H), dtype=np.float32)
+    decay = -rng.random((B, S, H), dtype=np.float32) * np.float32(2)
+    got = back(ops.delta_scan(*(dev(a, torch.float32) for a in (q, k, v, beta, decay)),
+                              out_dtype=out_dtype))
+    exp = np.stack([forward.delta_recurrence(q[b], k[b], v[b], beta[b], decay[b])
+                    for b in range(B)])
+    report(f"delta scan {B}x{S} kh{KH} h{H} kd{kd} vd{vd}", got, exp, out_dtype)
