@@ -206,6 +206,116 @@ def calibrate(dev):
     print(f"calibration: 4 copies of {CALIB_BYTES} bytes", file=sys.stderr, flush=True)
 
 
+E2E_BATCH, E2E_SEQ = 8, 2048
+
+
+def fused_sequence(cfg, dev, tokens):
+    """The fused row-kernel launches of one bf16 forward at `tokens` tokens
+    (gather, input norm, 2 residual norms per layer, SwiGLU per layer, q/k
+    norm + RoPE per full-attention layer, gated norm per DeltaNet layer) on
+    buffers of the forward's shapes and strides."""
+    import torch
+    from qdc_amd import ops
+    bf, f32 = torch.bfloat16, torch.float32
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    rn = lambda shape, dt: torch.randn(shape, generator=g, device=dev).to(dt)  # noqa: E731
+    H = cfg.hidden
+    table = rn((cfg.vocab, H), bf)
+    ids = torch.randint(0, cfg.vocab, (tokens,), generator=g, device=dev, dtype=torch.int32)
+    w = rn((H,), bf)
+    h, mixed = rn((tokens, H), f32), rn((tokens, H), f32)
+    res, normed = torch.empty_like(h), torch.empty((tokens, H), dtype=bf, device=dev)
+    gu = rn((tokens, 2 * cfg.intermediate), bf)
+    act = torch.empty((tokens, cfg.intermediate), dtype=bf, device=dev)
+    hd, nh, kv = cfg.head_dim, cfg.heads, cfg.kv_heads
+    qkv = rn((tokens, 2 * hd * nh + 2 * hd * kv), bf)
+    qn = rn((hd,), bf)
+    q_out = torch.empty((tokens, nh, hd), dtype=bf, device=dev)
+    k_out = torch.empty((tokens, kv, hd), dtype=bf, device=dev)
+    tables = ops.rope_tables(E2E_SEQ, cfg.rotary_dim, cfg.rope_theta, dev)
+    vw = cfg.value_dim * cfg.value_heads
+    cq = 2 * cfg.key_dim * cfg.key_heads + vw
+    proj = rn((tokens, cq + vw + 2 * cfg.value_heads), bf)
+    dx = rn((tokens, cfg.value_heads, cfg.value_dim), bf)
+    gated = torch.empty_like(dx)
+    wv = rn((cfg.value_dim,), bf)
+    I = cfg.intermediate
+
+    def run():
+        ops.native_gather(table, ids, out=h, out_dtype=f32)
+        ops.native_rms(h, w, 1e-6, out=normed)
+        for kind in cfg.layer_types:
+            if kind == "full_attention":
+                ops.prepare_heads(qkv[:, :2 * hd * nh].view(tokens, nh, 2 * hd)[:, :, :hd],
+                                  qkv[:, 2 * hd * nh:2 * hd * nh + hd * kv].view(tokens, kv, hd),
+                                  qn, qn, tables, cfg.rotary_dim, 1e-6, seq_len=E2E_SEQ,
+                                  q_out=q_out, k_out=k_out)
+            else:
+                ops.native_gated_rms(dx, proj[:, cq:cq + vw].view(tokens, cfg.value_heads,
+                                                                  cfg.value_dim), wv, 1e-6,
+                                     out=gated)
+            ops.native_residual_rms(h, mixed, w, 1e-6, residual=res, out=normed)
+            ops.native_mlp_gate(gu[:, :I], gu[:, I:], out=act)
+            ops.native_residual_rms(res, mixed, w, 1e-6, residual=h, out=normed)
+    return run
+
+
+def e2e_benchmark(dev, steps=3, warmup=1):
+    """backbone_hidden of the random-init Qwen3.5-0.8B-like backbone (24 layers,
+    bf16 weights/activations, fp32 residual stream) on 8 sequences of 2048."""
+    import torch
+    from qdc_amd import backbone
+    from qdc_amd.config import qwen35_08b_config
+    from qdc_amd.weights import random_device_weights
+    cfg = qwen35_08b_config()
+    weights = random_device_weights(cfg, seed=0, device=dev, dtype=torch.bfloat16)
+    model = backbone.QwenBackbone.from_weights(weights, cfg, dev, torch.bfloat16)
+    del weights
+    torch.cuda.empty_cache()
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    ids = torch.randint(0, cfg.vocab, (E2E_BATCH, E2E_SEQ), generator=g, device=dev,
+                        dtype=torch.int32)
+    mask = torch.ones((E2E_BATCH, E2E_SEQ), dtype=torch.int32, device=dev)
+    for _ in range(warmup):
+        out = model.forward(ids, mask)
+    torch.cuda.synchronize()
+    if not torch.isfinite(out).all():
+        raise RuntimeError("non-finite backbone output")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        model.forward(ids, mask)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del model
+    torch.cuda.empty_cache()
+    # fused kernels of one forward, replayed from a graph on buffers of the same shapes
+    run = fused_sequence(cfg, dev, E2E_BATCH * E2E_SEQ)
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
+        run()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    fused_ms = a.elapsed_time(b)
+    return {"workload": "random-init Qwen3.5-0.8B-like backbone, 24 layers (18 DeltaNet + 6 full), "
+                        "hidden 1024, vocab 248320, bf16 weights and activations, fp32 residual",
+            "batch": E2E_BATCH, "seq_len": E2E_SEQ, "ms_per_forward": round(ms, 3),
+            "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (ms / 1e3), 1),
+            "fused_kernels_ms": round(fused_ms, 3),
+            "fused_kernel_time_share": round(fused_ms / ms, 4),
+            "steps": steps, "warmup": warmup}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -287,6 +397,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma-separated kernel names (profiling runs)")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end backbone run")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 4 plain 512 MiB device copies (scales the PMC byte counters)")
     args = ap.parse_args()
@@ -337,6 +448,11 @@ def main():
                      "traffic": traffic, "algorithmic_bytes": dom.algo_bytes},
         "kernels": per,
     }
+    if not args.no_e2e:
+        for k in kernels:  # release the kernel benchmark's buffers first
+            k.sets, k.graph = None, None
+        torch.cuda.empty_cache()
+        line["backbone"] = e2e_benchmark(dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -75,6 +75,20 @@ def random_weights(cfg: BackboneConfig, seed: int = 0, std: float = 0.02) -> dic
     return out
 
 
+def random_device_weights(cfg: BackboneConfig, seed: int = 0, device="cuda:0", dtype=None,
+                          std: float = 0.02) -> dict:
+    """Every tensor ~ N(0, std), generated on the device with a seeded torch
+    generator (fast at full model size; values differ from :func:`random_weights`)."""
+    import torch
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    out = {}
+    for name, shape in all_shapes(cfg).items():
+        t = torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std
+        out[name] = t.to(dtype) if dtype is not None else t
+    return out
+
+
 def read_checkpoint(directory: str) -> dict:
     """Load every ``language_model.*`` tensor of a local safetensors checkpoint
     (single file or sharded index) widened to fp32 (``src/safetensors.jl:28-30``)."""
