@@ -9,84 +9,98 @@
 //     f = exp(decay[t]);  u = beta[t] * (v[t] - f * S k[t]);
 //     S = f * S + u k[t]^T;  out[t] = S q[t]
 //
-// Mapping: one wavefront per (b, h, group of R value rows).  Lane l holds the
-// key components l, l+64, ... of each of its R state rows in registers; the
-// two dot products per row and token are reduced across the wavefront (DPP
-// inside 16-lane rows, permutes across them).  The next token's k, q, v, beta
-// and decay are loaded while the current token is computed.
+// Mapping: a wavefront is 4 groups of 16 lanes; each group owns R consecutive
+// value rows of one (b, h) and splits the key dimension across its lanes (lane
+// i holds key components i*KPL .. i*KPL+KPL-1, loaded as 16-byte chunks), so
+// both dot products per row and token reduce over 16 lanes with 4 DPP steps and
+// no cross-row traffic.  The state (R x KPL values per lane) stays in
+// registers; the next token's k, q, v, beta and decay are loaded while the
+// current token is computed.
 #include "qdc_common.hpp"
 
 namespace qdc {
 namespace {
 
-constexpr int kRows = 8;  // value rows per wavefront
+constexpr int kGroup = 16;        // lanes per key split
+constexpr int kGroups = kWave / kGroup;
+constexpr int kRowsPerGroup = 2;  // value rows per 16-lane group
+
+template <int KPL> __device__ __forceinline__ void load_keys(const float *p, bool full, int valid,
+                                                             float (&out)[KPL]) {
+    if (KPL % 4 == 0 && full) {
+#pragma unroll
+        for (int i = 0; i < KPL; i += 4) {
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(p + i);
+            out[i] = c.x; out[i + 1] = c.y; out[i + 2] = c.z; out[i + 3] = c.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) out[i] = i < valid ? p[i] : 0.0f;
+    }
+}
 
 template <int KPL, typename TO>
 __global__ __launch_bounds__(kWave) void delta_scan(
     TO *__restrict__ out, const float *__restrict__ q, const float *__restrict__ k,
     const float *__restrict__ v, const float *__restrict__ beta, const float *__restrict__ decay,
-    int S, int H, int KH, int KD, int vd, int groups) {
-    // lanes past key_dim hold zero key/query components and so add nothing
-    const int lane = threadIdx.x;
-    const int r0 = blockIdx.x * kRows;
+    int S, int H, int KH, int KD, int vd, int groups, bool vec) {
+    constexpr int R = kRowsPerGroup;
+    const int lane = threadIdx.x % kGroup;
+    const int grp = threadIdx.x / kGroup;
+    const int r0 = (blockIdx.x * kGroups + grp) * R;  // first value row of this group
     const int h = blockIdx.y, b = blockIdx.z;
     const int g = h / groups;
-    // element strides of the [B, S, heads, dim] inputs
+    // this lane's key components [j0, j0 + valid); lanes past key_dim hold zeros
+    const int j0 = lane * KPL;
+    const int valid = max(0, min(KPL, KD - j0));
+    // 16-byte key loads need 16-byte aligned q/k and key_dim % 4 == 0 (checked on the host)
+    const bool full = vec && valid == KPL;
     const int64_t k_tok = (int64_t)KH * KD, v_tok = (int64_t)H * vd, s_tok = H;
-    const float *kp = k + (int64_t)b * S * k_tok + (int64_t)g * KD + lane;
-    const float *qp = q + (int64_t)b * S * k_tok + (int64_t)g * KD + lane;
-    const float *vp = v + (int64_t)b * S * v_tok + (int64_t)h * vd + r0;
+    const float *kp = k + (int64_t)b * S * k_tok + (int64_t)g * KD + min(j0, KD - 1);
+    const float *qp = q + (int64_t)b * S * k_tok + (int64_t)g * KD + min(j0, KD - 1);
+    const float *vp = v + (int64_t)b * S * v_tok + (int64_t)h * vd;
     const float *bp = beta + (int64_t)b * S * s_tok + h;
     const float *dp = decay + (int64_t)b * S * s_tok + h;
-    TO *op = out + (int64_t)b * S * v_tok + (int64_t)h * vd + r0;
-    const int rows = min(kRows, vd - r0);
+    TO *op = out + (int64_t)b * S * v_tok + (int64_t)h * vd;
 
-    float st[kRows][KPL];
+    float st[R][KPL];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int i = 0; i < KPL; ++i) st[r][i] = 0.0f;
 
-    // token-t operands, prefetched one token ahead
-    float kn[KPL], qn[KPL], vn[kRows], bn = 0.0f, dn = 0.0f;
+    float kn[KPL], qn[KPL], vn[R], bn = 0.0f, dn = 0.0f;
     auto fetch = [&](int t) {
+        load_keys<KPL>(kp + (int64_t)t * k_tok, full, valid, kn);
+        load_keys<KPL>(qp + (int64_t)t * k_tok, full, valid, qn);
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) {
-            const bool in = lane + i * kWave < KD;
-            kn[i] = in ? kp[(int64_t)t * k_tok + i * kWave] : 0.0f;
-            qn[i] = in ? qp[(int64_t)t * k_tok + i * kWave] : 0.0f;
-        }
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) vn[r] = r < rows ? vp[(int64_t)t * v_tok + r] : 0.0f;
+        for (int r = 0; r < R; ++r) vn[r] = r0 + r < vd ? vp[(int64_t)t * v_tok + r0 + r] : 0.0f;
         bn = bp[(int64_t)t * s_tok];
         dn = dp[(int64_t)t * s_tok];
     };
     if (S > 0) fetch(0);
     for (int t = 0; t < S; ++t) {
-        float kt[KPL], qt[KPL], vt[kRows];
+        float kt[KPL], qt[KPL], vt[R];
 #pragma unroll
         for (int i = 0; i < KPL; ++i) {
             kt[i] = kn[i];
             qt[i] = qn[i];
         }
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) vt[r] = vn[r];
+        for (int r = 0; r < R; ++r) vt[r] = vn[r];
         const float bt = bn, f = __expf(dn);
         if (t + 1 < S) fetch(t + 1);
 
-        float pred[kRows];
+        float pred[R], o[R];
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) {
+        for (int r = 0; r < R; ++r) {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < KPL; ++i) s += st[r][i] * kt[i];
-            pred[r] = s;
+            pred[r] = group_sum<kGroup>(s);
         }
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) pred[r] = group_sum<kWave>(pred[r]);
-        float o[kRows];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
+        for (int r = 0; r < R; ++r) {
             const float u = bt * (vt[r] - f * pred[r]);
             float s = 0.0f;
 #pragma unroll
@@ -94,15 +108,13 @@ __global__ __launch_bounds__(kWave) void delta_scan(
                 st[r][i] = f * st[r][i] + u * kt[i];
                 s += st[r][i] * qt[i];
             }
-            o[r] = s;
+            o[r] = group_sum<kGroup>(s);
         }
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) o[r] = group_sum<kWave>(o[r]);
-        // lane r stores row r: one coalesced store of the wavefront's rows
+        // lane r of the group stores row r0 + r
         float mine = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) mine = lane == r ? o[r] : mine;
-        if (lane < rows) op[(int64_t)t * v_tok + lane] = from_f32<TO>(mine);
+        for (int r = 0; r < R; ++r) mine = lane == r ? o[r] : mine;
+        if (lane < R && r0 + lane < vd) op[(int64_t)t * v_tok + r0 + lane] = from_f32<TO>(mine);
     }
 }
 
@@ -125,21 +137,29 @@ extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, 
         value_dim >= ((int64_t)1 << 24))
         return QDC_ERR_SHAPE;
     if (!out || !q || !k || !v || !beta || !decay) return QDC_ERR_NULL;
-    const dim3 grid((uint32_t)ceil_div(value_dim, kRows), (uint32_t)heads, (uint32_t)batch);
+    const int rows_per_block = kGroups * kRowsPerGroup;
+    const dim3 grid((uint32_t)ceil_div(value_dim, rows_per_block), (uint32_t)heads,
+                    (uint32_t)batch);
     const int groups = (int)(heads / key_heads);
     const int S = (int)seq, H = (int)heads, KH = (int)key_heads, KD = (int)key_dim;
     const int vd = (int)value_dim;
 #define QDC_SCAN(KPL, TO)                                                                       \
     hipLaunchKernelGGL((delta_scan<KPL, TO>), grid, dim3(kWave), 0, stream, (TO *)out, q, k, v,  \
-                       beta, decay, S, H, KH, KD, vd, groups);                                   \
+                       beta, decay, S, H, KH, KD, vd, groups, vec);                              \
     return launch_status();
+    const int64_t kpl = ceil_div(key_dim, kGroup);
+    const bool vec = aligned16(q) && aligned16(k) && key_dim % 4 == 0;
     if (out_dtype == QDC_BF16) {
-        if (key_dim <= 64) { QDC_SCAN(1, bf16_t) }
-        if (key_dim <= 128) { QDC_SCAN(2, bf16_t) }
-        QDC_SCAN(4, bf16_t)
+        if (kpl <= 1) { QDC_SCAN(1, bf16_t) }
+        if (kpl <= 2) { QDC_SCAN(2, bf16_t) }
+        if (kpl <= 4) { QDC_SCAN(4, bf16_t) }
+        if (kpl <= 8) { QDC_SCAN(8, bf16_t) }
+        QDC_SCAN(16, bf16_t)
     }
-    if (key_dim <= 64) { QDC_SCAN(1, float) }
-    if (key_dim <= 128) { QDC_SCAN(2, float) }
-    QDC_SCAN(4, float)
+    if (kpl <= 1) { QDC_SCAN(1, float) }
+    if (kpl <= 2) { QDC_SCAN(2, float) }
+    if (kpl <= 4) { QDC_SCAN(4, float) }
+    if (kpl <= 8) { QDC_SCAN(8, float) }
+    QDC_SCAN(16, float)
 #undef QDC_SCAN
 }
