@@ -184,6 +184,25 @@ int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, const float
                        int64_t seq, int64_t heads, int64_t key_heads, int64_t key_dim,
                        int64_t value_dim, hipStream_t stream);
 
+/*
+ * DeltaNet prologue in one pass over the packed projection rows
+ * [q | k | v | z | a | b] (widths kh*kd, kh*kd, vh*vd, vh*vd, vh, vh; row
+ * stride ld elements, proj_dtype): causal depthwise convolution of the qkv
+ * block with `taps` taps per sequence of seq_len tokens (conv fp32
+ * [channels, taps], tap 0 on the oldest row), SiLU, then per key head
+ * q / (sqrt(sum(q^2) + 1e-6) * sqrt(kd)) and k / sqrt(sum(k^2) + 1e-6); v
+ * passes through; beta = sigmoid(b), decay = a_decay * softplus(a + dt_bias).
+ * Outputs fp32, contiguous: q, k [tokens, kh*kd], v [tokens, vh*vd], beta and
+ * decay [tokens, vh].  Replaces causal_depthwise_kernel!, qk_normalize_kernel!
+ * and the beta/decay broadcasts (ext/amdgpu_delta.jl:1-33, 83-113, 154-159;
+ * generic src/backbone.jl:264-296; CPU src/backbone_cpu.jl:411-427, 501-533).
+ */
+int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta, float *decay,
+                           const void *proj, int32_t proj_dtype, int64_t ld, const float *conv,
+                           int64_t taps, const float *a_decay, const float *dt_bias,
+                           int64_t tokens, int64_t seq_len, int64_t key_heads, int64_t key_dim,
+                           int64_t value_heads, int64_t value_dim, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -143,22 +143,36 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
     qkv = _store(_linear(masked, W[p + "linear_attn.in_proj_qkv.weight"]), bf16)
     conv = W[p + "linear_attn.conv1d.weight"]
     conv = conv.reshape(conv.shape[0], conv.shape[-1])
+    z = _store(_linear(masked, W[p + "linear_attn.in_proj_z.weight"]), bf16).reshape(T, vh, vd)
+    b_raw = _store(_linear(masked, W[p + "linear_attn.in_proj_b.weight"]), bf16)
+    a_raw = _store(_linear(masked, W[p + "linear_attn.in_proj_a.weight"]), bf16)
+    a_decay = (F32(-1) * np.exp(W[p + "linear_attn.A_log"].astype(F32))).astype(F32)
+    q, k, v, beta, decay = delta_prologue(qkv, conv, a_raw, b_raw, a_decay,
+                                          W[p + "linear_attn.dt_bias"], kh, kd, vh, vd)
+    result = delta_recurrence(q, k, v, beta, decay)
+    out = _store(ops.gated_rms(_store(result, bf16), z, W[p + "linear_attn.norm.weight"],
+                               cfg["eps"]), bf16)
+    return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
+
+
+def delta_prologue(qkv, conv, a_raw, b_raw, a_decay, dt_bias, kh, kd, vh, vd):
+    """Causal conv + SiLU of the qkv projection, q/k L2 normalisation and the
+    gates, for one sequence (``cpu_delta_prepare``, ``src/backbone_cpu.jl:465-499``;
+    generic ``src/backbone.jl:286-296``; ``cpu_normalize_delta_heads!`` :411-427
+    with its scale-then-multiply form).  Returns q, k ``[T, kh, kd]``, v
+    ``[T, vh, vd]``, beta, decay ``[T, vh]``, all fp32."""
+    T = qkv.shape[0]
     mixed = causal_depthwise(qkv, conv)
     kw = kd * kh
     q = mixed[:, :kw].reshape(T, kh, kd)
     k = mixed[:, kw:2 * kw].reshape(T, kh, kd)
     v = mixed[:, 2 * kw:].reshape(T, vh, vd)
-    q = (q / (np.sqrt((q * q).sum(-1, keepdims=True) + F32(1e-6)) * np.sqrt(F32(kd)))).astype(F32)
-    k = (k / (np.sqrt((k * k).sum(-1, keepdims=True) + F32(1e-6)) * F32(1))).astype(F32)
-    z = _store(_linear(masked, W[p + "linear_attn.in_proj_z.weight"]), bf16).reshape(T, vh, vd)
-    beta = _sigmoid(_store(_linear(masked, W[p + "linear_attn.in_proj_b.weight"]), bf16))
-    a_decay = (F32(-1) * np.exp(W[p + "linear_attn.A_log"].astype(F32))).astype(F32)
-    decay = (a_decay * _softplus(_store(_linear(masked, W[p + "linear_attn.in_proj_a.weight"]),
-                                        bf16) + W[p + "linear_attn.dt_bias"])).astype(F32)
-    result = delta_recurrence(q, k, v, beta, decay)
-    out = _store(ops.gated_rms(_store(result, bf16), z, W[p + "linear_attn.norm.weight"],
-                               cfg["eps"]), bf16)
-    return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
+    q = (q * (F32(1) / (np.sqrt((q * q).sum(-1, keepdims=True) + F32(1e-6))
+                        * np.sqrt(F32(kd))))).astype(F32)
+    k = (k * (F32(1) / np.sqrt((k * k).sum(-1, keepdims=True) + F32(1e-6)))).astype(F32)
+    beta = _sigmoid(b_raw)
+    decay = (a_decay * _softplus(a_raw + dt_bias)).astype(F32)
+    return q, k, np.ascontiguousarray(v), beta, decay
 
 
 def delta_recurrence(q, k, v, beta, decay):

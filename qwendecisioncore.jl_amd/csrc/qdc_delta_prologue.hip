@@ -1,0 +1,278 @@
+// qdc_delta_prologue.hip -- the DeltaNet prologue row work in one pass over the
+// packed projection [qkv | z | a | b] (one row per token; the launch grid keeps
+// blocks x work-items per dimension below 2^32, so tokens < 2^26):
+//   mixed  = silu(causal depthwise conv of the qkv block, K taps, per sequence)
+//   q      = mixed_q / (sqrt(sum(mixed_q^2) + 1e-6) * sqrt(key_dim))   per key head
+//   k      = mixed_k /  sqrt(sum(mixed_k^2) + 1e-6)                     per key head
+//   v      = mixed_v
+//   beta   = sigmoid(b);  decay = a_decay * softplus(a + dt_bias)       per value head
+// Reference: causal_depthwise src/backbone.jl:264-276 (CPU four-tap form
+// src/backbone_cpu.jl:787-809, same tap order), cpu_normalize_delta_heads!
+// src/backbone_cpu.jl:411-427, cpu_delta_prepare src/backbone_cpu.jl:501-533,
+// gates src/backbone.jl:293-296; AMDGPU causal_depthwise_kernel! /
+// qk_normalize_kernel! and the beta/decay broadcasts, ext/amdgpu_delta.jl:1-33, 83-113, 154-159.
+//
+// Fast path: a thread owns 8 consecutive channels (one 16-byte bf16 chunk of the
+// projection row) for a tile of kTile consecutive tokens and slides a K-tap
+// window down the tile, so each projection row is read once from HBM (plus a
+// K-1 row halo per tile from L2).  The kd/8 lanes of a key head are an aligned
+// lane group, so the L2 norm reduces inside the group (DPP).  Outputs are fp32
+// (the recurrence reads fp32).  One extra row of blocks computes the gates.
+#include <cmath>
+
+#include "qdc_common.hpp"
+
+namespace qdc {
+namespace {
+
+constexpr int kTile = 16;   // tokens per thread
+constexpr int kTaps = 4;    // fast-path convolution width (the Qwen3.5 default)
+
+struct Prologue {
+    const void *proj;
+    int64_t ld;             // elements between token rows of proj
+    int64_t a_off, b_off;   // columns of the a and b blocks
+    const float *conv;      // [channels, taps]
+    const float *a_decay, *dt_bias;
+    float *q, *k, *v, *beta, *decay;
+    int64_t tokens;
+    FastDiv seq;            // sequence length (positions reset per sequence)
+    int kh, kd, vh, vd, taps;
+    int chunks;             // qkv channels / 8
+    int qk_chunks;          // 2*kh*kd / 8
+    float sqrt_kd;
+};
+
+__device__ __forceinline__ float sigmoid_f(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+__device__ __forceinline__ float softplus_f(float x) {
+    return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+
+template <typename T> __device__ __forceinline__ void load8(const T *p, float (&v)[8]);
+template <> __device__ __forceinline__ void load8<bf16_t>(const bf16_t *p, float (&v)[8]) {
+    unpack(load_raw(p), v);
+}
+template <> __device__ __forceinline__ void load8<float>(const float *p, float (&v)[8]) {
+    float a[4], b[4];
+    unpack(load_raw(p), a);
+    unpack(load_raw(p + 4), b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = a[i];
+        v[4 + i] = b[i];
+    }
+}
+
+template <typename T, int LPH>
+__global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
+    const int64_t t0 = (int64_t)blockIdx.x * kTile;
+    if (blockIdx.y == gridDim.y - 1) {  // gates row of the grid
+        for (int i = threadIdx.x; i < kTile * a.vh; i += kBlock) {
+            const int64_t t = t0 + i / a.vh;
+            const int h = i % a.vh;
+            if (t >= a.tokens) continue;
+            const T *row = reinterpret_cast<const T *>(a.proj) + t * a.ld;
+            const float bv = to_f32(row[a.b_off + h]);
+            const float av = to_f32(row[a.a_off + h]);
+            a.beta[t * a.vh + h] = sigmoid_f(bv);
+            a.decay[t * a.vh + h] = a.a_decay[h] * softplus_f(av + a.dt_bias[h]);
+        }
+        return;
+    }
+    const int ci = blockIdx.y * kBlock + threadIdx.x;  // chunk of 8 channels
+    const bool live = ci < a.chunks;
+    const int c0 = (live ? ci : 0) * 8;
+    const bool is_q = ci < a.qk_chunks / 2, is_k = !is_q && ci < a.qk_chunks;
+    const T *base = reinterpret_cast<const T *>(a.proj) + c0;
+
+    float w[8][kTaps];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int j = 0; j < kTaps; ++j) w[c][j] = live ? a.conv[(c0 + c) * kTaps + j] : 0.0f;
+
+    // win[j] holds input row t - (kTaps-1) + j; rows before the tile are the halo
+    float win[kTaps][8];
+#pragma unroll
+    for (int j = 0; j < kTaps; ++j)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) win[j][c] = 0.0f;
+#pragma unroll
+    for (int j = 1; j < kTaps; ++j) {
+        const int64_t t = t0 - kTaps + j;  // becomes slot j-1 after the first slide
+        if (live && t >= 0 && t < a.tokens) load8<T>(base + t * a.ld, win[j]);
+    }
+
+    for (int tt = 0; tt < kTile; ++tt) {
+        const int64_t t = t0 + tt;
+        const bool tok = t < a.tokens;
+        // slide the window and bring in row t
+#pragma unroll
+        for (int j = 0; j < kTaps - 1; ++j)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) win[j][c] = win[j + 1][c];
+        if (live && tok) load8<T>(base + t * a.ld, win[kTaps - 1]);
+        // taps reaching before the start of this token's sequence read zeros
+        const uint32_t s = tok ? (uint32_t)t - fastdiv((uint32_t)t, a.seq) * a.seq.d : 0u;
+        float m[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kTaps; ++j)
+                if (s >= (uint32_t)(kTaps - 1 - j)) acc = acc + win[j][c] * w[c][j];
+            m[c] = silu(acc);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) ss += m[c] * m[c];
+        ss = group_sum<LPH>(ss);  // whole aligned head groups: q/k rows only use it
+        if (!live || !tok) continue;
+        float *dst;
+        if (is_q || is_k) {
+            const float scale = is_q ? 1.0f / (__builtin_sqrtf(ss + 1e-6f) * a.sqrt_kd)
+                                     : 1.0f / __builtin_sqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) m[c] = m[c] * scale;
+            const int64_t kw = (int64_t)a.kh * a.kd;
+            dst = is_q ? a.q + t * kw + c0 : a.k + t * kw + (c0 - kw);
+        } else {
+            const int64_t vw = (int64_t)a.vh * a.vd;
+            dst = a.v + t * vw + (c0 - 2 * (int64_t)a.kh * a.kd);
+        }
+        store_frag<8>(dst, m);
+    }
+}
+
+// One wavefront per (token, segment); segments: q heads, k heads, the v block, the gates.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void delta_prologue_general(Prologue a) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t t = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    if (t >= a.tokens) return;  // uniform per wavefront
+    const int seg = blockIdx.y;
+    const T *proj = reinterpret_cast<const T *>(a.proj);
+    const uint32_t s = (uint32_t)t - fastdiv((uint32_t)t, a.seq) * a.seq.d;
+    const int64_t kw = (int64_t)a.kh * a.kd, vw = (int64_t)a.vh * a.vd;
+    auto conv_silu = [&](int64_t c) {
+        float acc = 0.0f;
+        for (int j = 0; j < a.taps; ++j) {
+            const int lag = a.taps - 1 - j;
+            if ((int64_t)s >= lag) acc = acc + to_f32(proj[(t - lag) * a.ld + c]) * a.conv[c * a.taps + j];
+        }
+        return silu(acc);
+    };
+    if (seg < 2 * a.kh) {  // a q or k head
+        const bool is_q = seg < a.kh;
+        const int64_t c0 = (int64_t)seg * a.kd;
+        float *dst = is_q ? a.q + t * kw + c0 : a.k + t * kw + (c0 - kw);
+        float ss = 0.0f;
+        for (int i = lane; i < a.kd; i += kWave) {
+            const float m = conv_silu(c0 + i);
+            dst[i] = m;
+            ss += m * m;
+        }
+        ss = group_sum<kWave>(ss);
+        const float scale = is_q ? 1.0f / (__builtin_sqrtf(ss + 1e-6f) * a.sqrt_kd)
+                                 : 1.0f / __builtin_sqrtf(ss + 1e-6f);
+        for (int i = lane; i < a.kd; i += kWave) dst[i] = dst[i] * scale;
+    } else if (seg == 2 * a.kh) {  // the v block
+        for (int64_t i = lane; i < vw; i += kWave) a.v[t * vw + i] = conv_silu(2 * kw + i);
+    } else {  // gates
+        for (int h = lane; h < a.vh; h += kWave) {
+            a.beta[t * a.vh + h] = sigmoid_f(to_f32(proj[t * a.ld + a.b_off + h]));
+            a.decay[t * a.vh + h] =
+                a.a_decay[h] * softplus_f(to_f32(proj[t * a.ld + a.a_off + h]) + a.dt_bias[h]);
+        }
+    }
+}
+
+template <typename T>
+int32_t launch(const Prologue &p, bool fast, hipStream_t stream) {
+    const int lph = p.kd / 8;
+    if (fast && p.kd % 8 == 0 && p.vd % 8 == 0 && p.taps == kTaps && lph <= kWave &&
+        (lph & (lph - 1)) == 0) {
+        // x: token tiles; y: channel blocks plus one for the gates
+        const dim3 grid((uint32_t)ceil_div(p.tokens, kTile), (uint32_t)ceil_div(p.chunks, kBlock) + 1);
+#define QDC_PRO(L)                                                                               \
+    case L:                                                                                      \
+        hipLaunchKernelGGL((delta_prologue_fast<T, L>), grid, dim3(kBlock), 0, stream, p);     \
+        return launch_status();
+        switch (lph) {
+            QDC_PRO(1)
+            QDC_PRO(2)
+            QDC_PRO(4)
+            QDC_PRO(8)
+            QDC_PRO(16)
+            QDC_PRO(32)
+            QDC_PRO(64)
+            default:
+                break;
+        }
+#undef QDC_PRO
+    }
+    const dim3 grid((uint32_t)ceil_div(p.tokens, kBlock / kWave), (uint32_t)(2 * p.kh + 2));
+    hipLaunchKernelGGL((delta_prologue_general<T>), grid, dim3(kBlock), 0, stream, p);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace qdc
+
+using namespace qdc;
+
+extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta, float *decay,
+                                      const void *proj, int32_t proj_dtype, int64_t ld,
+                                      const float *conv, int64_t taps, const float *a_decay,
+                                      const float *dt_bias, int64_t tokens, int64_t seq_len,
+                                      int64_t key_heads, int64_t key_dim, int64_t value_heads,
+                                      int64_t value_dim, hipStream_t stream) {
+    if (!valid_dtype(proj_dtype)) return QDC_ERR_DTYPE;
+    if (tokens < 0 || seq_len <= 0 || key_heads <= 0 || key_dim <= 0 || value_heads <= 0 ||
+        value_dim <= 0 || taps <= 0 || taps > 64)
+        return QDC_ERR_SHAPE;
+    const int64_t kw = key_heads * key_dim, vw = value_heads * value_dim;
+    const int64_t cq = 2 * kw + vw;
+    if (ld < cq + vw + 2 * value_heads) return QDC_ERR_SHAPE;
+    if (tokens == 0) return QDC_OK;
+    if (tokens >= ((int64_t)1 << 26) || seq_len >= ((int64_t)1 << 31) || cq >= ((int64_t)1 << 28) ||
+        key_heads > 32000)
+        return QDC_ERR_SHAPE;
+    if (!q || !k || !v || !beta || !decay || !proj || !conv || !a_decay || !dt_bias)
+        return QDC_ERR_NULL;
+    const int64_t es = elem_size(proj_dtype);
+    const int64_t span_in = ((tokens - 1) * ld + ld) * es;
+    for (const void *o : {(const void *)q, (const void *)k, (const void *)v})
+        if (overlaps(o, tokens * (o == (const void *)v ? vw : kw) * 4, proj, span_in))
+            return QDC_ERR_ALIAS;
+    Prologue p{};
+    p.proj = proj;
+    p.ld = ld;
+    p.a_off = cq + vw;
+    p.b_off = cq + vw + value_heads;
+    p.conv = conv;
+    p.a_decay = a_decay;
+    p.dt_bias = dt_bias;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.beta = beta;
+    p.decay = decay;
+    p.tokens = tokens;
+    p.seq = make_fastdiv((uint32_t)seq_len);
+    p.kh = (int)key_heads;
+    p.kd = (int)key_dim;
+    p.vh = (int)value_heads;
+    p.vd = (int)value_dim;
+    p.taps = (int)taps;
+    p.chunks = (int)(cq / 8);
+    p.qk_chunks = (int)(2 * kw / 8);
+    // sqrt(Float32(key_dim)) of src/backbone.jl:313 / src/backbone_cpu.jl:516
+    p.sqrt_kd = std::sqrt((float)key_dim);
+    const bool fast = aligned16(proj) && (ld * es) % 16 == 0 && aligned16(q) && aligned16(k) &&
+                      aligned16(v) && cq % 8 == 0;
+    if (proj_dtype == QDC_BF16) return launch<bf16_t>(p, fast, stream);
+    return launch<float>(p, fast, stream);
+}

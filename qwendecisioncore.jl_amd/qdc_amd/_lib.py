@@ -40,6 +40,8 @@ SIGNATURES = {
     "qdc_swiglu": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _vp]),
     "qdc_delta_scan": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                               _i64, _vp]),
+    "qdc_delta_prologue": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _vp,
+                                  _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
 }
 
 _lib = None

@@ -83,9 +83,9 @@ class QwenBackbone:
                 layer.update(
                     proj=lin(a + "in_proj_qkv.weight", a + "in_proj_z.weight",
                              a + "in_proj_a.weight", a + "in_proj_b.weight"),
-                    conv=dev(conv.reshape(conv.shape[0], 1, conv.shape[-1]), torch.float32),
+                    conv=dev(conv.reshape(conv.shape[0], conv.shape[-1]), torch.float32),
                     # fixed decay multiplier, computed once in fp32 (src/backbone.jl:160-162)
-                    a_decay=(-1.0 * torch.exp(a_log.to(torch.float32))).to(self.device),
+                    a_decay=(-1.0 * torch.exp(a_log.to(torch.float32))).to(self.device).contiguous(),
                     dt_bias=dev(weights[a + "dt_bias"], torch.float32),
                     norm=dev(weights[a + "norm.weight"]),
                     out=lin(a + "out_proj.weight"))
@@ -190,22 +190,13 @@ class QwenBackbone:
         cq = 2 * kw + vw
         masked = x * maskf.reshape(T, 1).to(x.dtype)
         proj = masked @ layer["proj"]                        # [T, cq + vw + 2*vh]
-        conv_in = proj[:, :cq].float().view(B, S, cq).transpose(1, 2)
-        K = layer["conv"].shape[-1]
-        mixed = F.silu(F.conv1d(conv_in, layer["conv"], padding=K - 1, groups=cq)[..., :S])
-        mixed = mixed.transpose(1, 2)                        # [B, S, cq] fp32
-        q = mixed[..., :kw].reshape(B, S, kh, kd)
-        k = mixed[..., kw:2 * kw].reshape(B, S, kh, kd)
-        v = mixed[..., 2 * kw:].reshape(B, S, vh, vd)
-        q = q / (torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6) * math.sqrt(kd))
-        k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
-        a_in = proj[:, cq + vw:cq + vw + vh].float().view(B, S, vh)
-        b_in = proj[:, cq + vw + vh:].float().view(B, S, vh)
-        beta = torch.sigmoid(b_in)
-        decay = layer["a_decay"] * F.softplus(a_in + layer["dt_bias"])
+        # conv + SiLU, q/k L2 norm and the beta/decay gates in one pass
+        q, k, v, beta, decay = ops.delta_prologue(proj, layer["conv"], layer["a_decay"],
+                                                  layer["dt_bias"], S, kh, kd, vh, vd)
+        q, k = q.view(B, S, kh, kd), k.view(B, S, kh, kd)
+        v, beta, decay = v.view(B, S, vh, vd), beta.view(B, S, vh), decay.view(B, S, vh)
         # recurrence straight into the model dtype the gated norm reads
-        result = ops.delta_scan(q.contiguous(), k.contiguous(), v.contiguous(),
-                                beta.contiguous(), decay.contiguous(), self.dtype)
+        result = ops.delta_scan(q, k, v, beta, decay, self.dtype)
         z = proj[:, cq:cq + vw].view(T, vh, vd)
         out = ops.native_gated_rms(result.view(T, vh, vd), z, layer["norm"], cfg.eps)
         return self._mm32(out.view(T, vw), layer["out"])

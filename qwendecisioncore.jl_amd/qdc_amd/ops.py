@@ -298,6 +298,36 @@ def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Te
     return out
 
 
+def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor,
+                   dt_bias: torch.Tensor, seq_len: int, key_heads: int, key_dim: int,
+                   value_heads: int, value_dim: int):
+    """DeltaNet prologue on the packed projection ``[T, q|k|v|z|a|b]`` (rows
+    contiguous): causal conv + SiLU, q/k L2 norm, beta/decay gates.  Returns fp32
+    ``q, k [T, KH, kd]``, ``v [T, H, vd]``, ``beta, decay [T, H]``."""
+    _device(proj, conv, a_decay, dt_bias)
+    if proj.dtype not in _DTYPES or proj.dim() != 2 or proj.stride(1) != 1:
+        raise ValueError("proj must be a [tokens, width] float32/bfloat16 view with unit column stride")
+    for t in (conv, a_decay, dt_bias):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("conv, a_decay and dt_bias must be contiguous float32")
+    T = proj.shape[0]
+    taps = conv.shape[-1]
+    dev = proj.device
+    f32 = torch.float32
+    q = torch.empty((T, key_heads, key_dim), dtype=f32, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty((T, value_heads, value_dim), dtype=f32, device=dev)
+    beta = torch.empty((T, value_heads), dtype=f32, device=dev)
+    decay = torch.empty_like(beta)
+    ld = proj.stride(0) if T > 1 else proj.shape[1]
+    check(lib().qdc_delta_prologue(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                                   decay.data_ptr(), proj.data_ptr(), _DTYPES[proj.dtype], ld,
+                                   conv.data_ptr(), taps, a_decay.data_ptr(), dt_bias.data_ptr(), T,
+                                   seq_len, key_heads, key_dim, value_heads, value_dim,
+                                   _stream(proj)), "delta_prologue")
+    return q, k, v, beta, decay
+
+
 def check_ids(ids: Sequence[int], vocab: int) -> None:
     """Host id check of ``check_sequence`` (``src/backbone.jl:417-418``)."""
     host = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))

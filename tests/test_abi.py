@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 11, names
+    assert len(names) == 12, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -208,3 +208,32 @@ int main() {
                    check=True, capture_output=True)
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=240)
     assert run.returncode == 0 and run.stdout.startswith("ok"), run.stdout
+
+
+def test_delta_prologue_validation():
+    lib = _lib.lib()
+    # q, k, v, beta, decay, proj, dtype, ld, conv, taps, a_decay, dt_bias, tokens, seq,
+    # kh, kd, vh, vd: kh=1 kd=8 vh=2 vd=8 -> qkv 32 channels, row width 32 + 16 + 4 = 52
+    pro = lambda *a: lib.qdc_delta_prologue(*a, None)  # noqa: E731
+    ok = (FAKE, FAKE + 4096, FAKE + 8192, FAKE + 12288, FAKE + 16384, FAKE + 65536, F32, 52,
+          FAKE + 131072, 4, FAKE, FAKE, 16, 8, 1, 8, 2, 8)
+
+    def call(**kw):
+        args = list(ok)
+        names = ["q", "k", "v", "beta", "decay", "proj", "dtype", "ld", "conv", "taps",
+                 "a_decay", "dt_bias", "tokens", "seq", "kh", "kd", "vh", "vd"]
+        for key, val in kw.items():
+            args[names.index(key)] = val
+        return pro(*args)
+
+    assert call(dtype=5) == -3
+    assert call(ld=51) == -2                 # narrower than q|k|v|z|a|b
+    assert call(seq=0) == -2
+    assert call(taps=0) == -2
+    assert call(kd=0) == -2
+    assert call(tokens=-1) == -2
+    assert call(tokens=1 << 26) == -2
+    assert call(q=None) == -1
+    assert call(conv=None) == -1
+    assert call(tokens=0, q=None, proj=None) == 0
+    assert call(v=FAKE + 65536 + 64) == -5   # output inside the projection

@@ -335,3 +335,52 @@ def test_delta_scan(out_dtype, B, S, KH, H, kd, vd):
     exp = np.stack([forward.delta_recurrence(q[b], k[b], v[b], beta[b], decay[b])
                     for b in range(B)])
     report(f"delta scan {B}x{S} kh{KH} h{H} kd{kd} vd{vd}", got, exp, out_dtype)
+
+
+# ------------------------------------------------ DeltaNet prologue ----------
+# (B, S, KH, kd, H, vd, taps, pad): pad > 0 widens the row stride by pad elements
+PROLOGUE_CASES = [
+    (2, 1024, 16, 128, 16, 128, 4, 0),   # Qwen3.5-0.8B DeltaNet dims, fast path
+    (2, 37, 2, 128, 4, 128, 4, 0),       # sequences break inside a 16-token tile
+    (3, 5, 1, 64, 2, 32, 4, 8),          # strided rows
+    (7, 1, 2, 16, 2, 8, 4, 0),           # every token starts a sequence
+    (2, 33, 1, 8, 4, 16, 4, 0),          # one lane per key head
+    (1, 65, 2, 2, 2, 2, 4, 0),           # fixture-sized heads: general kernel
+    (2, 19, 2, 96, 4, 40, 4, 0),         # kd/8 not a power of two: general kernel
+    (2, 21, 1, 64, 2, 64, 3, 0),         # three taps: general kernel
+    (1, 17, 1, 64, 2, 64, 4, 3),         # odd row stride: general kernel
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", PROLOGUE_CASES)
+def test_delta_prologue(dtype, case):
+    from oracle import forward
+    from qdc_amd import ops
+    B, S, KH, kd, H, vd, taps, pad = case
+    kw, vw = KH * kd, H * vd
+    cq = 2 * kw + vw
+    width = cq + vw + 2 * H
+    T = B * S
+    proj = host((T, width + pad), 41, 1.0, dtype)
+    conv = host((cq, taps), 42, 0.5)
+    a_decay = -np.exp(host((H,), 43, 0.5))
+    dt_bias = host((H,), 44, 1.0)
+    # wide gate inputs so both softplus branches and saturated sigmoids occur
+    proj[:, cq + vw:width] *= np.float32(8)
+    proj = O.round_bf16(proj) if dtype == torch.bfloat16 else proj
+    d_proj = dev(proj, dtype)[:, :width]
+    got = [back(t) for t in ops.delta_prologue(d_proj, dev(conv, torch.float32),
+                                               dev(a_decay, torch.float32),
+                                               dev(dt_bias, torch.float32), S, KH, kd, H, vd)]
+    exp = [[], [], [], [], []]
+    for b in range(B):
+        rows = proj[b * S:(b + 1) * S]
+        parts = forward.delta_prologue(rows[:, :cq], conv, rows[:, cq + vw:cq + vw + H],
+                                       rows[:, cq + vw + H:width], a_decay, dt_bias, KH, kd, H, vd)
+        for i, part in enumerate(parts):
+            exp[i].append(part)
+    for name, g, e in zip(("q", "k", "v", "beta", "decay"), got, exp):
+        e = np.concatenate(e)
+        assert g.shape == e.shape, (name, g.shape, e.shape)
+        report(f"prologue {name} {case} {dtype}", g, e, torch.float32)
