@@ -110,7 +110,7 @@ def build_kernels(dev):
     vocab, hidden, n = 248320, 1024, 16384
     table = randn((vocab, hidden), bf, 0.02)
     kernels.append(Kernel(
-        "gather_bf16", "gather_fast", 2 * n * hidden * 2 + n * 4,
+        "gather_bf16", "gather_flat", 2 * n * hidden * 2 + n * 4,
         lambda i: (torch.randint(0, vocab, (n,), generator=g, device=dev, dtype=torch.int32),
                    torch.empty((n, hidden), dtype=bf, device=dev)),
         lambda s: ops.native_gather(table, s[0], out=s[1]), [vocab, hidden, n], "bfloat16"))

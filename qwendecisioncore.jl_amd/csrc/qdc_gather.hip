@@ -1,9 +1,12 @@
 // qdc_gather.hip -- embedding gather (token id -> row copy) for gfx950, plus
 // the host-side id check and the library's version/status strings.
 //
-// Fast path: one wavefront per token row, 16-byte chunks, U chunks per lane in
-// flight before the first store.  bf16->bf16 and f32->f32 move bits;
-// bf16->f32 widens each value by a 16-bit shift, so results are bit-exact.
+// Fast path: one thread per 16-byte chunk of the output (row = thread / chunks
+// per row), nontemporal load and store: the plain-copy shape that measured
+// fastest on gfx950.  A wavefront-per-row kernel covers launches too large for
+// 32-bit thread indices.  bf16->bf16 and f32->f32 move bits; bf16->f32 widens
+// each value by a 16-bit shift, so results are bit-exact.  An id outside
+// [0, vocab) yields a zero row and sets *error_flag (when given).
 #include "qdc_common.hpp"
 
 namespace qdc {
@@ -11,8 +14,45 @@ namespace {
 
 constexpr int kUnroll = 4;
 
+// widened copy of one bf16 chunk (8 values) as two fp32 chunks, or the bits as they are
+template <typename TI, typename TO> __device__ __forceinline__ void put_chunk(TO *dst, u32x4 r) {
+    if constexpr (sizeof(TI) == sizeof(TO)) {
+        store_raw(dst, r);
+    } else {
+        u32x4 lo, hi;
+        lo[0] = r[0] << 16; lo[1] = r[0] & 0xffff0000u;
+        lo[2] = r[1] << 16; lo[3] = r[1] & 0xffff0000u;
+        hi[0] = r[2] << 16; hi[1] = r[2] & 0xffff0000u;
+        hi[2] = r[3] << 16; hi[3] = r[3] & 0xffff0000u;
+        store_raw(dst, lo);
+        store_raw(dst + 4, hi);
+    }
+}
+
 template <typename TI, typename TO>
-__global__ __launch_bounds__(kBlock) void gather_fast(TO *__restrict__ out,
+__global__ __launch_bounds__(kBlock) void gather_flat(TO *__restrict__ out,
+                                                      const TI *__restrict__ table,
+                                                      const int32_t *__restrict__ ids,
+                                                      uint32_t total, FastDiv chunks, int64_t vocab,
+                                                      int32_t *error_flag) {
+    constexpr int V = Elem<TI>::kVec;
+    const uint32_t g = blockIdx.x * kBlock + threadIdx.x;
+    if (g >= total) return;
+    const uint32_t row = fastdiv(g, chunks);
+    const uint32_t c = g - row * chunks.d;
+    const int64_t hidden = (int64_t)chunks.d * V;
+    const int64_t id = ids[row];
+    TO *dst = out + (int64_t)row * hidden + (int64_t)c * V;
+    if (id < 0 || id >= vocab) {
+        put_chunk<TI, TO>(dst, u32x4{0u, 0u, 0u, 0u});
+        if (c == 0 && error_flag) atomicOr(error_flag, 1);
+        return;
+    }
+    put_chunk<TI, TO>(dst, load_stream(table + id * hidden + (int64_t)c * V));
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void gather_rows(TO *__restrict__ out,
                                                       const TI *__restrict__ table,
                                                       const int32_t *__restrict__ ids,
                                                       int64_t n_ids, int64_t vocab,
@@ -25,16 +65,7 @@ __global__ __launch_bounds__(kBlock) void gather_fast(TO *__restrict__ out,
     TO *dst = out + row * hidden;
     const int64_t chunks = hidden / V;
     if (id < 0 || id >= vocab) {
-        for (int64_t c = lane; c < chunks; c += kWave) {
-            float zero[V] = {};
-            if constexpr (sizeof(TI) == sizeof(TO)) {
-                store_chunk(reinterpret_cast<TI *>(dst) + c * V, zero);
-            } else {
-                float lo[4] = {}, hi[4] = {};
-                store_chunk(dst + c * V, lo);
-                store_chunk(dst + c * V + 4, hi);
-            }
-        }
+        for (int64_t c = lane; c < chunks; c += kWave) put_chunk<TI, TO>(dst + c * V, u32x4{0u, 0u, 0u, 0u});
         if (lane == 0 && error_flag) atomicOr(error_flag, 1);
         return;
     }
@@ -50,18 +81,7 @@ __global__ __launch_bounds__(kBlock) void gather_fast(TO *__restrict__ out,
         for (int u = 0; u < kUnroll; ++u) {
             const int64_t c = base + u * kWave + lane;
             if (c >= chunks) continue;
-            if constexpr (sizeof(TI) == sizeof(TO)) {
-                reinterpret_cast<u32x4 *>(dst)[c] = r[u];
-            } else {  // bf16 -> f32: 8 values -> two 16-byte stores
-                u32x4 lo, hi;
-                lo[0] = r[u][0] << 16; lo[1] = r[u][0] & 0xffff0000u;
-                lo[2] = r[u][1] << 16; lo[3] = r[u][1] & 0xffff0000u;
-                hi[0] = r[u][2] << 16; hi[1] = r[u][2] & 0xffff0000u;
-                hi[2] = r[u][3] << 16; hi[3] = r[u][3] & 0xffff0000u;
-                u32x4 *d = reinterpret_cast<u32x4 *>(dst) + 2 * c;
-                d[0] = lo;
-                d[1] = hi;
-            }
+            put_chunk<TI, TO>(dst + c * V, r[u]);
         }
     }
 }
@@ -94,8 +114,14 @@ template <typename TI, typename TO>
 int32_t launch(void *out, const void *table, const int32_t *ids, int64_t n_ids, int64_t vocab,
                int64_t hidden, int32_t *error_flag, bool fast, hipStream_t stream) {
     const int64_t blocks = ceil_div(n_ids, kBlock / kWave);
-    if (fast && hidden % Elem<TI>::kVec == 0)
-        hipLaunchKernelGGL((gather_fast<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
+    const int64_t chunks = hidden / Elem<TI>::kVec;
+    if (fast && hidden % Elem<TI>::kVec == 0 && n_ids * chunks < ((int64_t)1 << 31)) {
+        const uint32_t total = (uint32_t)(n_ids * chunks);
+        hipLaunchKernelGGL((gather_flat<TI, TO>), dim3((uint32_t)ceil_div(total, kBlock)),
+                           dim3(kBlock), 0, stream, (TO *)out, (const TI *)table, ids, total,
+                           make_fastdiv((uint32_t)chunks), vocab, error_flag);
+    } else if (fast && hidden % Elem<TI>::kVec == 0)
+        hipLaunchKernelGGL((gather_rows<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
                            (TO *)out, (const TI *)table, ids, n_ids, vocab, hidden, error_flag);
     else
         hipLaunchKernelGGL((gather_general<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0,
@@ -141,6 +167,7 @@ extern "C" int32_t qdc_embedding_gather(void *out, int32_t out_dtype, const void
     if (n_ids < 0 || vocab < 0 || hidden < 0) return QDC_ERR_SHAPE;
     if (n_ids == 0 || hidden == 0) return QDC_OK;
     if (vocab == 0) return QDC_ERR_RANGE;
+    if (n_ids >= ((int64_t)1 << 26)) return QDC_ERR_SHAPE;  // wavefront-per-row grid limit
     if (!out || !table || !ids) return QDC_ERR_NULL;
     const int64_t ti = elem_size(table_dtype), to = elem_size(out_dtype);
     if (overlaps(out, n_ids * hidden * to, table, vocab * hidden * ti) ||

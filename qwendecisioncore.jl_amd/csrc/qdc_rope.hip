@@ -2,12 +2,13 @@
 // RoPE for the Q and K heads of full attention (one launch for both), and the
 // host-side RoPE table builder.
 //
-// Fast path (head_dim*sizeof(T) <= 1024 bytes, rotary_dim/2 a multiple of the
-// 16-byte chunk): a group of LPR = head_dim/chunk lanes owns one (token, head)
-// row, one 16-byte chunk per lane.  The row is normalised in registers; the
-// rotation partner of a lane's chunk (the same offset in the other half of the
-// rotary block) lives in lane l +/- half/chunk of the same group and is fetched
-// with a lane permute, so every input byte is read from HBM once and every
+// Fast path (head_dim a power-of-two number >= 2 of 16-byte chunks, at most
+// 128, rotary_dim/2 a multiple of the chunk): a group of LPR = chunks/2 lanes
+// owns one (token, head) row, two 16-byte chunks per lane.  The chunks are
+// dealt so that each of the first half/chunk lanes holds a whole rotation pair
+// (element i of the first rotary half and its partner i + half), so the
+// rotation needs no lane exchange and only those lanes read cos/sin.  The row
+// is normalised in registers; every input byte is read from HBM once and every
 // output byte written once.  cos/sin come from small fp32 tables (L2-resident)
 // built on the host exactly as the reference CPU path builds them.
 //
@@ -42,6 +43,15 @@ template <typename T> struct QKArgs {
     float eps;
 };
 
+// Chunk held in slot `slot` (0 or 1) by lane `lane` of a row group: lanes below
+// hc hold a rotation pair (chunk lane of the first rotary half and chunk
+// lane + hc of the second), the others hold the remaining chunks in order.
+// A bijection of [0, 2*LPR) onto the lane slots whenever hc <= LPR.
+template <int LPR> __device__ __forceinline__ int pair_chunk(int lane, int slot, int hc) {
+    if (lane < hc) return lane + slot * hc;
+    return slot == 0 ? lane + hc : lane + LPR;
+}
+
 template <typename T, int LPR>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
     constexpr int V = Elem<T>::kVec;
@@ -50,25 +60,27 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
     const Side<T> &sd = is_k ? a.k : a.q;
     const int64_t block = is_k ? (int64_t)blockIdx.x - a.q_blocks : (int64_t)blockIdx.x;
     const int lane = threadIdx.x % LPR;
-    const int group_base = (threadIdx.x % kWave) - lane;  // first lane of this row group
     const int64_t row = block * RPB + threadIdx.x / LPR;
     const bool active = row < sd.rows;
     const int hc = a.half / V;  // chunks per half of the rotary block
-    const bool rotary = lane < 2 * hc;
+    const bool rotary = lane < hc;
+    const int c0 = pair_chunk<LPR>(lane, 0, hc), c1 = pair_chunk<LPR>(lane, 1, hc);
 
-    // Every load first: the row, its norm weights and (rotary lanes) the
-    // cos/sin of its position, so the latencies overlap.
+    // Every load first: both chunks of the row, their norm weights and (rotary
+    // lanes) the cos/sin of the position, so the latencies overlap.
     uint32_t t = 0, h = 0;
-    u32x4 xr = {0u, 0u, 0u, 0u};
+    u32x4 x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
     u32x4 cr[V / 4], sr[V / 4];
     if (active) {
         t = fastdiv((uint32_t)row, sd.heads);
         h = (uint32_t)row - t * sd.heads.d;
-        xr = load_stream(sd.in + (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head + lane * V);
+        const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head;
+        x0 = load_stream(src + c0 * V);
+        x1 = load_stream(src + c1 * V);
         if (rotary) {
             const uint32_t tq = fastdiv(t, a.seq_len);
             const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
-            const int64_t i0 = pos * a.half + (lane < hc ? lane : lane - hc) * V;
+            const int64_t i0 = pos * a.half + lane * V;
 #pragma unroll
             for (int q = 0; q < V / 4; ++q) {
                 cr[q] = load_raw(a.cos + i0 + 4 * q);
@@ -76,46 +88,42 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
             }
         }
     }
-    const u32x4 wr = load_raw(sd.w + lane * V);
+    const u32x4 w0 = load_raw(sd.w + c0 * V), w1 = load_raw(sd.w + c1 * V);
 
-    float v[V];
-    unpack(xr, v);
+    float v0[V], v1[V];
+    unpack(x0, v0);
+    unpack(x1, v1);
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < V; ++j) ss += v[j] * v[j];
+    for (int j = 0; j < V; ++j) ss += v0[j] * v0[j];
+#pragma unroll
+    for (int j = 0; j < V; ++j) ss += v1[j] * v1[j];
     ss = group_sum<LPR>(ss);
-    const float s = rms_scale(ss, (float)a.dim, a.eps);
-    float wv[V];
-    unpack(wr, wv);
-#pragma unroll
-    for (int j = 0; j < V; ++j) v[j] = (v[j] * s) * (1.0f + wv[j]);
-
-    // Partner chunk of the rotation, fetched from the owning lane.  Every lane
-    // takes part in the permute (inactive rows included) so it stays uniform.
-    const int src = rotary ? (lane < hc ? lane + hc : lane - hc) : lane;
-    float p[V];
-#pragma unroll
-    for (int j = 0; j < V; ++j) p[j] = __shfl(v[j], group_base + src, kWave);
     if (!active) return;
-
-    if (rotary) {
-        float c[V], sn[V];
+    const float s = rms_scale(ss, (float)a.dim, a.eps);
+    float wv0[V], wv1[V];
+    unpack(w0, wv0);
+    unpack(w1, wv1);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        v0[j] = (v0[j] * s) * (1.0f + wv0[j]);
+        v1[j] = (v1[j] * s) * (1.0f + wv1[j]);
+    }
+    if (rotary) {  // v0 = first-half element i, v1 = its partner i + half
 #pragma unroll
         for (int q = 0; q < V / 4; ++q)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                c[4 * q + e] = __uint_as_float(cr[q][e]);
-                sn[4 * q + e] = __uint_as_float(sr[q][e]);
+                const int j = 4 * q + e;
+                const float c = __uint_as_float(cr[q][e]), sn = __uint_as_float(sr[q][e]);
+                const float a0 = v0[j], b0 = v1[j];
+                v0[j] = a0 * c - b0 * sn;
+                v1[j] = b0 * c + a0 * sn;
             }
-        if (lane < hc) {
-#pragma unroll
-            for (int j = 0; j < V; ++j) v[j] = v[j] * c[j] - p[j] * sn[j];
-        } else {
-#pragma unroll
-            for (int j = 0; j < V; ++j) v[j] = v[j] * c[j] + p[j] * sn[j];
-        }
     }
-    store_chunk(sd.out + (int64_t)t * sd.out_tok + (int64_t)h * sd.out_head + lane * V, v);
+    T *dst = sd.out + (int64_t)t * sd.out_tok + (int64_t)h * sd.out_head;
+    store_chunk(dst + c0 * V, v0);
+    store_chunk(dst + c1 * V, v1);
 }
 
 constexpr int kMaxGeneralRotary = 1024;
@@ -175,9 +183,11 @@ template <typename T>
 int32_t launch(QKArgs<T> a, bool fast, hipStream_t stream) {
     constexpr int V = Elem<T>::kVec;
     const int64_t chunks = a.dim / V;
-    if (fast && a.dim % V == 0 && a.half % V == 0 && chunks <= kWave &&
-        (chunks & (chunks - 1)) == 0) {
-        const int64_t rpb = kBlock / chunks;
+    // two chunks per lane: LPR = chunks / 2 lanes per row, a power of two <= 64
+    const int64_t lpr = chunks / 2;
+    if (fast && a.dim % V == 0 && a.half % V == 0 && chunks >= 2 && chunks % 2 == 0 && lpr <= kWave &&
+        (lpr & (lpr - 1)) == 0) {
+        const int64_t rpb = kBlock / lpr;
         a.q_blocks = ceil_div(a.q.rows, rpb);
         const int64_t blocks = a.q_blocks + ceil_div(a.k.rows, rpb);
 #define QDC_QK(LPR)                                                                          \
@@ -185,7 +195,7 @@ int32_t launch(QKArgs<T> a, bool fast, hipStream_t stream) {
         hipLaunchKernelGGL((qk_norm_rope_fast<T, LPR>), dim3((uint32_t)blocks), dim3(kBlock), 0, \
                            stream, a);                                                       \
         return launch_status();
-        switch (chunks) {
+        switch (lpr) {
             QDC_QK(1)
             QDC_QK(2)
             QDC_QK(4)

@@ -127,6 +127,8 @@ QK_CASES = [
     (40, 3, 1, 64, 0, 40, 1e7),         # no rotation
     (33, 2, 2, 128, 128, 11, 1e4),      # full rotary, sequences of 11
     (19, 2, 1, 96, 24, 19, 1e6),        # 12-wide halves: general kernel
+    (9, 3, 1, 16, 16, 5, 1e4),          # two bf16 chunks per row: one lane per row
+    (7, 2, 1, 24, 16, 7, 1e4),          # odd chunk count: general kernel
 ]
 
 
