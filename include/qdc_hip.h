@@ -203,6 +203,34 @@ int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta, float *dec
                            int64_t tokens, int64_t seq_len, int64_t key_heads, int64_t key_dim,
                            int64_t value_heads, int64_t value_dim, hipStream_t stream);
 
+/*
+ * Masked, scaled softmax of attention score rows: scores fp32 [batch, heads,
+ * queries, keys] (contiguous); query q of a row sits at position q + q_offset;
+ * key i is visible when i <= position and (mask == NULL or mask[b * keys + i]
+ * != 0); value = scores * scale if visible else -floatmax(Float32); probs =
+ * exp(value - max) / sum (fp32 or bf16, contiguous like scores; may equal
+ * scores when fp32).  A row with no visible key gets 1/keys everywhere.
+ * Replaces attention_softmax_kernel! (ext/amdgpu_attention.jl:61-88, launch
+ * :150-156; generic mask and softmax src/backbone.jl:237-242, 252-254).
+ */
+int32_t qdc_attention_softmax(void *probs, int32_t probs_dtype, const float *scores,
+                              const int32_t *mask, int64_t batch, int64_t heads,
+                              int64_t queries, int64_t keys, int64_t q_offset, float scale,
+                              hipStream_t stream);
+
+/*
+ * Output-gate merge: out[t, h*head_dim + r] = values[b, h, s, r] *
+ * sigmoid(gate[t*gate_tok + h*gate_head + r]) for t = b*seq + s; values fp32
+ * [batch, heads, seq, head_dim] contiguous (the PV GEMM output), gate and out
+ * in gate_dtype / out_dtype with the given token and head strides (elements).
+ * Replaces merge_gate_kernel! (ext/amdgpu_attention.jl:90-106, launch :159-166;
+ * generic src/backbone.jl:256-258).
+ */
+int32_t qdc_attention_gate(void *out, int32_t out_dtype, const float *values, const void *gate,
+                           int32_t gate_dtype, int64_t batch, int64_t seq, int64_t heads,
+                           int64_t head_dim, int64_t gate_tok, int64_t gate_head, int64_t out_tok,
+                           hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,8 +12,8 @@ laid out as stored (PyTorch ``[out, in]``), which is the reference's Julia
 ``bf16=True`` runs the same algorithm with bf16 storage (RNE,
 ``src/safetensors.jl:37-42``) of the activations a bf16 device pipeline keeps in
 bf16: the normalised GEMM inputs, the outputs of the input-side projections
-(q||gate, k, v, qkv, z, a, b, gate, up), the normed+rotated q/k, the merged
-attention output, the DeltaNet recurrence and gated-norm outputs and the SwiGLU
+(q||gate, k, v, qkv, z, a, b, gate, up), the normed+rotated q/k, the attention
+probabilities, the merged attention output, the DeltaNet recurrence and gated-norm outputs and the SwiGLU
 output.  The residual stream and the outputs of the residual-side projections
 (o_proj, out_proj, down_proj) stay fp32.  Arithmetic stays fp32 throughout.
 """
@@ -97,23 +97,46 @@ def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, 
     k = _store(ops.qk_norm_rope(kp, W[p + "self_attn.k_norm.weight"], cos, sin, cfg["rotary_dim"],
                                 cfg["eps"]), bf16)
     v = _store(_linear(x, W[p + "self_attn.v_proj.weight"]), bf16).reshape(T, KV, hd)
-    # scores_mask[i (key), j (query)] (src/backbone.jl:237-242)
-    keys = np.arange(T)[:, None]
-    queries = np.arange(T)[None, :]
-    smask = np.where((keys <= queries) & (mask[:, None] == 1), F32(0), F32(-FLOATMAX)).astype(F32)
+    # AMDGPU form (ext/amdgpu_attention.jl:148-166): scores of every head, the
+    # masked softmax with scale inv(sqrt(dim)), the PV product, the gate merge;
+    # kv head of query head h is h // (H // KV) (src/backbone.jl:249-251)
     groups = H // KV
-    out = np.empty((T, H * hd), F32)
-    scale = F32(np.sqrt(F32(hd)))
-    for h in range(H):
-        kv = h // groups
-        scores = (k[:, kv, :] @ q[:, h, :].T).astype(F32) / scale + smask  # [key, query]
-        with np.errstate(over="ignore", invalid="ignore"):
-            probs = np.exp(scores - scores.max(axis=0, keepdims=True)).astype(F32)
-        probs /= probs.sum(axis=0, keepdims=True)
-        values = (probs.T @ v[:, kv, :]).astype(F32)  # [query, hd]
-        gate = _sigmoid(qgate[:, h, hd:])
-        out[:, h * hd:(h + 1) * hd] = values * gate
+    qh = q.transpose(1, 0, 2)                                   # [H, T, hd]
+    kh = np.repeat(k.transpose(1, 0, 2), groups, axis=0)        # [H, T, hd]
+    vh = np.repeat(v.transpose(1, 0, 2), groups, axis=0)
+    scores = (qh @ kh.transpose(0, 2, 1)).astype(F32)           # [H, query, key]
+    probs = _store(attention_softmax(scores[None], mask[None], F32(1) / np.sqrt(F32(hd)))[0],
+                   bf16)
+    values = (probs @ vh).astype(F32)                           # [H, query, hd]
+    out = attention_gate(values[None], qgate[:, :, hd:])
     return _linear(_store(out, bf16), W[p + "self_attn.o_proj.weight"])
+
+
+def attention_softmax(scores: np.ndarray, mask, scale, q_offset: int = 0) -> np.ndarray:
+    """``attention_softmax_kernel!`` (``ext/amdgpu_attention.jl:61-88``) on score
+    rows ``[B, H, Q, K]``: query q sits at position ``q + q_offset``; key i is
+    visible when ``i <= position`` and ``mask[b, i] == 1`` (``mask`` ``[B, K]`` or
+    None); value = ``scores * scale`` if visible else ``-floatmax``; then
+    ``exp(value - max) / sum``.  A row with no visible key is uniform over all K
+    keys, as in the reference."""
+    B, H, Q, K = scores.shape
+    pos = np.arange(Q)[:, None] + q_offset
+    vis = np.broadcast_to(np.arange(K)[None, :] <= pos, (B, Q, K))
+    if mask is not None:
+        vis = vis & (np.asarray(mask)[:, None, :] != 0)
+    value = np.where(vis[:, None], scores.astype(F32) * F32(scale), F32(-FLOATMAX)).astype(F32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(value - value.max(axis=-1, keepdims=True)).astype(F32)
+    return (e / e.sum(axis=-1, keepdims=True)).astype(F32)
+
+
+def attention_gate(values: np.ndarray, gate: np.ndarray) -> np.ndarray:
+    """``merge_gate_kernel!`` (``ext/amdgpu_attention.jl:90-106``): values
+    ``[B, H, S, hd]`` times ``sigmoid(gate)`` for gate ``[B*S, H, hd]``, written
+    as ``[B*S, H*hd]``."""
+    B, H, S, hd = values.shape
+    merged = values.transpose(0, 2, 1, 3).reshape(B * S, H, hd) * _sigmoid(gate)
+    return merged.reshape(B * S, H * hd).astype(F32)
 
 
 def causal_depthwise(x: np.ndarray, w: np.ndarray) -> np.ndarray:

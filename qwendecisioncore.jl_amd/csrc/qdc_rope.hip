@@ -275,9 +275,17 @@ extern "C" int32_t qdc_qk_norm_rope(void *q_out, void *k_out, const void *q_in, 
         if (pos_offset + std::min(tokens, seq_len) > table_len) return QDC_ERR_RANGE;
     }
     const int64_t es = elem_size(dtype);
-    // Strides must keep rows apart: head stride >= head_dim, token stride spans the heads.
+    // Strides must keep the rows of a side apart: token-major (head stride >=
+    // head_dim, token stride spanning the heads) or head-major (token stride >=
+    // head_dim, head stride spanning the tokens, the reference AMDGPU layout
+    // (dim, tokens, heads)).  A stride of a dimension of extent 1 is unused.
     auto strides_ok = [&](int64_t n, int64_t tok, int64_t head) {
-        return n == 0 || (head >= head_dim && tok >= (n - 1) * head + head_dim);
+        if (n == 0) return true;
+        const bool token_major = (n == 1 || head >= head_dim) &&
+                                 (tokens == 1 || tok >= (n - 1) * head + head_dim);
+        const bool head_major = (tokens == 1 || tok >= head_dim) &&
+                                (n == 1 || head >= (tokens - 1) * tok + head_dim);
+        return token_major || head_major;
     };
     if (!strides_ok(heads, q_in_tok, q_in_head) || !strides_ok(heads, q_out_tok, q_out_head) ||
         !strides_ok(kv_heads, k_in_tok, k_in_head) || !strides_ok(kv_heads, k_out_tok, k_out_head))

@@ -15,25 +15,23 @@ Per layer (``native_layer``, ``src/backbone.jl:363-388``) the fused kernels do
 the row work: the layer's input RMSNorm is fused with the previous layer's MLP
 residual add (``qdc_residual_rmsnorm``; the last one with the final norm),
 post-attention residual + RMSNorm, q/k norm + partial RoPE read straight out of
-the packed projection, the DeltaNet gated RMSNorm reading z inside the packed
-projection, and SwiGLU reading the packed gate||up GEMM output.  GEMMs, the
-attention softmax/merge and the DeltaNet convolution/recurrence are the
-"existing path" and run as PyTorch-ROCm ops (hipBLASLt GEMMs); attention
-scores are computed in fp32.
+the packed projection, the attention masked softmax and output-gate merge, the
+DeltaNet prologue (convolution, SiLU, q/k L2 norm, gates), the gated-delta
+recurrence, the DeltaNet gated RMSNorm reading z inside the packed projection,
+and SwiGLU reading the packed gate||up GEMM output.  GEMMs and the two attention
+products run through PyTorch-ROCm (hipBLASLt), with fp32 results; attention
+scores and probabilities are fp32 (probabilities stored in the model dtype for
+the PV product).
 """
 from __future__ import annotations
 
-import math
-
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from . import ops
 from .config import BackboneConfig, load_config
 from .weights import read_checkpoint
 
-FLOATMAX = float(np.finfo(np.float32).max)
 
 
 class QwenBackbone:
@@ -138,9 +136,10 @@ class QwenBackbone:
         h = ops.native_gather(self.embedding, ids.reshape(-1).contiguous(), out_dtype=torch.float32)
         normed = ops.native_rms(h, self.layers[0]["input_norm"], cfg.eps)
         maskf = mask.to(torch.float32)
+        mask32 = mask.to(torch.int32).contiguous()
         for i, layer in enumerate(self.layers):
             if layer["kind"] == "full_attention":
-                mixed = self._full_attention(layer, normed, maskf, B, S)
+                mixed = self._full_attention(layer, normed, mask32, B, S)
             else:
                 mixed = self._delta_attention(layer, normed, maskf, B, S)
             residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps)
@@ -153,32 +152,45 @@ class QwenBackbone:
             h, normed = ops.native_residual_rms(residual, down, nxt, cfg.eps)
         return normed
 
-    def _full_attention(self, layer, x, maskf, B, S):
-        """``full_attention`` (``src/backbone.jl:224-262``)."""
+    def _full_attention(self, layer, x, mask32, B, S):
+        """``full_attention`` in the AMDGPU form (``ext/amdgpu_attention.jl:108-168``;
+        generic ``src/backbone.jl:224-262``).  Q and K are normalised and rotated
+        straight into head-major per-sequence layouts ``[B, H, S, hd]`` and
+        ``[B, KV, S, hd]``: the G = H / KV query heads sharing a KV head are then one
+        ``[G*S, hd]`` block, so both products run per (sequence, KV head) without
+        expanding K or V.  The masked softmax and the gate merge are HIP kernels."""
         cfg = self.cfg
         hd, H, KV = cfg.head_dim, cfg.heads, cfg.kv_heads
+        G = H // KV
         T = B * S
+        dt = self.dtype
         proj = x @ layer["qkv"]                              # [T, 2*hd*H + 2*hd*KV]
         qgate = proj[:, :2 * hd * H].view(T, H, 2 * hd)
         k_in = proj[:, 2 * hd * H:2 * hd * H + hd * KV].view(T, KV, hd)
         v = proj[:, 2 * hd * H + hd * KV:].view(T, KV, hd)
-        q, k = ops.prepare_heads(qgate[:, :, :hd], k_in, layer["q_norm"], layer["k_norm"],
-                                 self.rope_tables(S) if cfg.rotary_dim else None, cfg.rotary_dim,
-                                 cfg.eps, seq_len=S)
-        groups = H // KV
-        qf = q.float().view(B, S, H, hd).permute(0, 2, 1, 3).contiguous()
-        kf = k.float().view(B, S, KV, hd).permute(0, 2, 1, 3).repeat_interleave(groups, 1)
-        vf = v.float().view(B, S, KV, hd).permute(0, 2, 1, 3).repeat_interleave(groups, 1)
-        scores = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) / math.sqrt(hd)
-        # key i is visible to query j when i <= j and mask[i] == 1 (src/backbone.jl:237-242)
-        keys = torch.arange(S, device=x.device)
-        allowed = (keys[None, :] <= keys[:, None])[None] & (maskf[:, None, :] == 1)
-        scores = scores + torch.where(allowed, 0.0, -FLOATMAX)[:, None]
-        probs = torch.softmax(scores, dim=-1)
-        values = torch.matmul(probs, vf.contiguous())        # [B, H, S, hd]
-        gate = torch.sigmoid(qgate[:, :, hd:].float())       # [T, H, hd]
-        merged = values.permute(0, 2, 1, 3).reshape(T, H, hd) * gate
-        return self._mm32(merged.reshape(T, H * hd).to(self.dtype), layer["out"])
+        tables = self.rope_tables(S) if cfg.rotary_dim else None
+        q = torch.empty((B, H, S, hd), dtype=dt, device=self.device)
+        k = torch.empty((B, KV, S, hd), dtype=dt, device=self.device)
+        for b in range(B):
+            rows = slice(b * S, (b + 1) * S)
+            ops.prepare_heads(qgate[rows, :, :hd], k_in[rows], layer["q_norm"], layer["k_norm"],
+                              tables, cfg.rotary_dim, cfg.eps, seq_len=S,
+                              q_out=q[b].permute(1, 0, 2), k_out=k[b].permute(1, 0, 2))
+        kt = k.transpose(-1, -2).contiguous().view(B * KV, hd, S)
+        vh = v.view(B, S, KV, hd).permute(0, 2, 1, 3).contiguous().view(B * KV, S, hd)
+        scores = self._bmm32(q.view(B * KV, G * S, hd), kt)          # [B*KV, G*S, S] fp32
+        scale = float(np.float32(1) / np.sqrt(np.float32(hd)))      # inv(sqrt(Float32(dim)))
+        probs = ops.attention_softmax(scores.view(B, H, S, S), mask32, scale, out_dtype=dt,
+                                      out=scores.view(B, H, S, S) if dt == torch.float32 else None)
+        values = self._bmm32(probs.view(B * KV, G * S, S), vh)       # [B, H, S, hd] fp32
+        merged = ops.attention_gate(values.view(B, H, S, hd), qgate[:, :, hd:], out_dtype=dt)
+        return self._mm32(merged, layer["out"])
+
+    def _bmm32(self, a, b):
+        """Batched product with an fp32 result (fp32 accumulate for bf16 inputs)."""
+        if a.dtype == torch.float32:
+            return torch.bmm(a, b)
+        return torch.bmm(a, b, out_dtype=torch.float32)
 
     def _delta_attention(self, layer, x, maskf, B, S):
         """Gated DeltaNet (``src/backbone.jl:284-345``; recurrent form

@@ -328,6 +328,58 @@ def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor
     return q, k, v, beta, decay
 
 
+# ------------------------------------------------------------- attention ---
+def attention_softmax(scores: torch.Tensor, mask: torch.Tensor | None, scale: float,
+                      q_offset: int = 0, out_dtype=None, out: torch.Tensor | None = None):
+    """Masked, scaled softmax of score rows ``[B, H, Q, K]`` (fp32, contiguous):
+    query ``q`` sits at position ``q + q_offset``; key ``i`` is visible when
+    ``i <= position`` and ``mask[b, i] != 0`` (``mask`` int32 ``[B, K]`` or
+    None).  Returns probs ``[B, H, Q, K]`` in ``out_dtype`` (default fp32);
+    ``out=scores`` runs in place."""
+    _device(scores)
+    if scores.dtype != torch.float32 or scores.dim() != 4 or not scores.is_contiguous():
+        raise ValueError("scores must be a contiguous float32 [B, H, Q, K] tensor")
+    B, H, Q, K = scores.shape
+    if mask is not None:
+        _device(mask)
+        if mask.dtype != torch.int32 or mask.shape != (B, K) or not mask.is_contiguous():
+            raise ValueError("mask must be a contiguous int32 [B, K] tensor")
+    if out is None:
+        out = torch.empty(scores.shape, dtype=out_dtype or torch.float32, device=scores.device)
+    if out.shape != scores.shape or not out.is_contiguous() or out.dtype not in _DTYPES:
+        raise ValueError("out must be a contiguous float32/bfloat16 tensor shaped like scores")
+    check(lib().qdc_attention_softmax(out.data_ptr(), _DTYPES[out.dtype], scores.data_ptr(),
+                                      mask.data_ptr() if mask is not None else 0, B, H, Q, K,
+                                      q_offset, float(scale), _stream(scores)),
+          "attention_softmax")
+    return out
+
+
+def attention_gate(values: torch.Tensor, gate: torch.Tensor, out_dtype=None,
+                   out: torch.Tensor | None = None):
+    """Output-gate merge ``out[t, h*hd + r] = values[b, h, s, r] * sigmoid(gate[t, h, r])``
+    for ``t = b*S + s``: ``values`` fp32 ``[B, H, S, hd]`` contiguous (the PV
+    product), ``gate`` a ``[B*S, H, hd]`` view with unit element stride (the gate
+    half of the q||gate projection).  Returns ``[B*S, H*hd]``."""
+    _device(values, gate)
+    if values.dtype != torch.float32 or values.dim() != 4 or not values.is_contiguous():
+        raise ValueError("values must be a contiguous float32 [B, H, S, hd] tensor")
+    B, H, S, hd = values.shape
+    if gate.dtype not in _DTYPES or gate.shape != (B * S, H, hd) or gate.stride(2) != 1:
+        raise ValueError("gate must be a [B*S, H, hd] view with unit element stride")
+    if out is None:
+        out = torch.empty((B * S, H * hd), dtype=out_dtype or gate.dtype, device=values.device)
+    if out.dtype not in _DTYPES or out.shape != (B * S, H * hd) or out.stride(1) != 1:
+        raise ValueError("out must be [B*S, H*hd] with unit element stride")
+    tok = out.stride(0) if B * S > 1 else H * hd
+    gtok = gate.stride(0) if B * S > 1 else H * gate.stride(1)
+    check(lib().qdc_attention_gate(out.data_ptr(), _DTYPES[out.dtype], values.data_ptr(),
+                                   gate.data_ptr(), _DTYPES[gate.dtype], B, S, H, hd, gtok,
+                                   gate.stride(1) if H > 1 else hd, tok, _stream(values)),
+          "attention_gate")
+    return out
+
+
 def check_ids(ids: Sequence[int], vocab: int) -> None:
     """Host id check of ``check_sequence`` (``src/backbone.jl:417-418``)."""
     host = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))

@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 12, names
+    assert len(names) == 14, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -237,3 +237,32 @@ def test_delta_prologue_validation():
     assert call(conv=None) == -1
     assert call(tokens=0, q=None, proj=None) == 0
     assert call(v=FAKE + 65536 + 64) == -5   # output inside the projection
+
+
+def test_attention_softmax_validation():
+    lib = _lib.lib()
+    # probs, dtype, scores, mask, batch, heads, queries, keys, q_offset, scale
+    sm = lambda *a: lib.qdc_attention_softmax(*a, None)  # noqa: E731
+    assert sm(FAKE, 7, FAKE + 65536, None, 1, 2, 8, 8, 0, 0.5) == -3
+    assert sm(FAKE, F32, FAKE + 65536, None, 1, -2, 8, 8, 0, 0.5) == -2
+    assert sm(FAKE, F32, FAKE + 65536, None, 1, 2, 8, 8, -1, 0.5) == -2
+    assert sm(FAKE, F32, FAKE + 65536, None, 1 << 20, 64, 1, 8, 0, 0.5) == -2  # 2^26 rows
+    assert sm(None, F32, FAKE, None, 1, 2, 8, 8, 0, 0.5) == -1
+    assert sm(None, F32, None, None, 0, 2, 8, 8, 0, 0.5) == 0
+    assert sm(FAKE, BF16, FAKE, None, 1, 2, 8, 8, 0, 0.5) == -5     # in place needs fp32
+    assert sm(FAKE + 64, F32, FAKE, None, 1, 2, 8, 8, 0, 0.5) == -5  # partial overlap
+    assert sm(FAKE, F32, FAKE + 65536, FAKE + 16, 1, 2, 8, 8, 0, 0.5) == -5  # writes the mask
+
+
+def test_attention_gate_validation():
+    lib = _lib.lib()
+    # out, out dtype, values, gate, gate dtype, batch, seq, heads, dim, gate_tok, gate_head, out_tok
+    ga = lambda *a: lib.qdc_attention_gate(*a, None)  # noqa: E731
+    assert ga(FAKE, 9, FAKE + 65536, FAKE + 131072, F32, 1, 4, 2, 8, 32, 16, 16) == -3
+    assert ga(FAKE, F32, FAKE + 65536, FAKE + 131072, F32, 1, 4, 0, 8, 32, 16, 16) == -2
+    assert ga(FAKE, F32, FAKE + 65536, FAKE + 131072, F32, 1, 4, 2, 8, 32, 4, 16) == -2
+    assert ga(FAKE, F32, FAKE + 65536, FAKE + 131072, F32, 1, 4, 2, 8, 32, 16, 8) == -2
+    assert ga(None, F32, FAKE + 65536, FAKE + 131072, F32, 1, 4, 2, 8, 32, 16, 16) == -1
+    assert ga(None, F32, None, None, F32, 0, 4, 2, 8, 32, 16, 16) == 0
+    assert ga(FAKE + 65536 + 32, F32, FAKE + 65536, FAKE + 131072, F32, 1, 4, 2, 8, 32, 16,
+              16) == -5

@@ -386,3 +386,106 @@ def test_delta_prologue(dtype, case):
         e = np.concatenate(e)
         assert g.shape == e.shape, (name, g.shape, e.shape)
         report(f"prologue {name} {case} {dtype}", g, e, torch.float32)
+
+
+# ------------------------------------------------ attention row work ---------
+# (B, H, Q, K, q_offset, mask kind): "rand" = 30% of keys masked, "none" = no mask,
+# "dead" = some sequences whose first keys are all masked (rows with no visible key)
+SOFTMAX_CASES = [
+    (2, 8, 2048, 2048, 0, "rand"),   # Qwen3.5-0.8B full attention, 2 of the 8 sequences
+    (1, 3, 37, 37, 0, "rand"),
+    (2, 2, 5, 8, 0, "dead"),
+    (1, 2, 16, 100, 84, "rand"),     # a chunk of queries at the end of a 100-key context
+    (1, 1, 7, 2560, 2553, "none"),   # more keys than the register path holds: general kernel
+    (1, 2, 9, 13, 4, "rand"),        # keys % 4 != 0: general kernel
+]
+
+
+def _softmax_inputs(case):
+    B, H, Q, K, off, kind = case
+    scores = host((B, H, Q, K), 51, 4.0)
+    mask = None
+    if kind != "none":
+        mask = (np.random.default_rng(52).random((B, K)) > 0.3).astype(np.int32)
+        if kind == "dead":
+            mask[1, :4] = 0
+    return scores, mask
+
+
+@pytest.mark.parametrize("out_dtype", DTYPES)
+@pytest.mark.parametrize("case", SOFTMAX_CASES)
+def test_attention_softmax(out_dtype, case):
+    from oracle import forward
+    from qdc_amd import ops
+    B, H, Q, K, off, kind = case
+    scores, mask = _softmax_inputs(case)
+    scale = 1.0 / np.sqrt(np.float32(256))
+    got = ops.attention_softmax(dev(scores, torch.float32),
+                                dev(mask, torch.int32) if mask is not None else None,
+                                float(scale), off, out_dtype=out_dtype)
+    exp = forward.attention_softmax(scores, mask, np.float32(scale), off)
+    got = back(got)
+    report(f"softmax {case} -> {out_dtype}", got, exp, out_dtype)
+    if out_dtype == torch.float32:
+        # causally hidden keys are exactly zero unless the row sees no key at all
+        pos = np.arange(Q)[:, None] + off
+        hidden = np.broadcast_to(np.arange(K)[None, :] > pos, got.shape)
+        dead = np.isclose(exp, 1.0 / K).all(-1, keepdims=True)
+        assert np.all(got[hidden & ~np.broadcast_to(dead, got.shape)] == 0)
+
+
+def test_attention_softmax_in_place():
+    from oracle import forward
+    from qdc_amd import ops
+    case = (2, 4, 64, 64, 0, "rand")
+    scores, mask = _softmax_inputs(case)
+    d = dev(scores, torch.float32)
+    out = ops.attention_softmax(d, dev(mask, torch.int32), 0.0625, out=d)
+    assert out.data_ptr() == d.data_ptr()
+    report("softmax in place", back(d), forward.attention_softmax(scores, mask, 0.0625),
+           torch.float32)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,S,H,hd", [(8, 2048, 8, 256), (2, 37, 4, 64), (1, 5, 3, 12),
+                                      (3, 1, 2, 8)])
+def test_attention_gate(dtype, B, S, H, hd):
+    from oracle import forward
+    from qdc_amd import ops
+    values = host((B, H, S, hd), 61, 1.0)
+    qgate = host((B * S, H, 2 * hd), 62, 2.0, dtype)      # interleaved q||gate projection
+    got = ops.attention_gate(dev(values, torch.float32), dev(qgate, dtype)[:, :, hd:])
+    assert got.dtype == dtype and got.shape == (B * S, H * hd)
+    exp = forward.attention_gate(values, qgate[:, :, hd:])
+    report(f"gate {B}x{S} h{H} hd{hd} {dtype}", back(got), exp, dtype)
+
+
+def test_attention_gate_fp32_out_from_bf16_gate():
+    from oracle import forward
+    from qdc_amd import ops
+    B, S, H, hd = 2, 33, 8, 256
+    values = host((B, H, S, hd), 63, 1.0)
+    gate = host((B * S, H, hd), 64, 2.0, torch.bfloat16)
+    got = ops.attention_gate(dev(values, torch.float32), dev(gate, torch.bfloat16),
+                             out_dtype=torch.float32)
+    report("gate bf16 -> f32", back(got), forward.attention_gate(values, gate), torch.float32)
+
+
+def test_qk_norm_rope_head_major_output():
+    # the reference AMDGPU layout (dim, tokens, heads): q/k written head-major
+    from qdc_amd import ops
+    T, H, KV, hd, rd, seq = 40, 4, 2, 64, 16, 20
+    qgate = host((T, H, 2 * hd), 71, 1.0)
+    k = host((T, KV, hd), 72, 1.0)
+    qn, kn = host((hd,), 73, 0.02), host((hd,), 74, 0.02)
+    tables = ops.rope_tables(seq, rd, 1e7, DEV)
+    q_hm = torch.empty((H, T, hd), device=DEV)
+    k_hm = torch.empty((KV, T, hd), device=DEV)
+    ops.prepare_heads(dev(qgate, torch.float32)[:, :, :hd], dev(k, torch.float32),
+                      dev(qn, torch.float32), dev(kn, torch.float32), tables, rd, 1e-6,
+                      seq_len=seq, q_out=q_hm.permute(1, 0, 2), k_out=k_hm.permute(1, 0, 2))
+    cos, sin = O.rope_tables(seq, rd, 1e7)
+    report("q head-major", back(q_hm).transpose(1, 0, 2),
+           O.qk_norm_rope(qgate[:, :, :hd], qn, cos, sin, rd, 1e-6, seq), torch.float32)
+    report("k head-major", back(k_hm).transpose(1, 0, 2),
+           O.qk_norm_rope(k, kn, cos, sin, rd, 1e-6, seq), torch.float32)

@@ -230,3 +230,81 @@ def test_swiglu_invariants():
     # silu(x)*u is linear in u
     u2 = ramp(np.cos, (4, 256))
     np.testing.assert_array_equal(O.swiglu(g, u2 * np.float32(2)), O.swiglu(g, u2) * np.float32(2))
+
+
+# mistakes planted in the attention and DeltaNet row work of oracle/forward.py
+_fwd = {name: getattr(forward, name) for name in ("attention_softmax", "attention_gate",
+                                                  "delta_prologue")}
+FORWARD_MUTANTS = {
+    "softmax mask ignored": ("attention_softmax", lambda s, m, scale, q_offset=0:
+                             _fwd["attention_softmax"](s, None, scale, q_offset)),
+    "softmax scale dropped": ("attention_softmax", lambda s, m, scale, q_offset=0:
+                              _fwd["attention_softmax"](s, m, 1.0, q_offset)),
+    "softmax not causal": ("attention_softmax", lambda s, m, scale, q_offset=0:
+                           _fwd["attention_softmax"](s, m, scale, q_offset + s.shape[-1])),
+    "gate not applied": ("attention_gate", lambda v, g: _fwd["attention_gate"](v, g * 0 + 80)),
+    "prologue q not scaled": ("delta_prologue", lambda *a: (lambda r: (r[0] * np.float32(
+        np.sqrt(a[7])), *r[1:]))(_fwd["delta_prologue"](*a))),
+    "prologue decay sign": ("delta_prologue", lambda *a: (lambda r: (*r[:4], -r[4]))(
+        _fwd["delta_prologue"](*a))),
+}
+
+
+@pytest.mark.parametrize("mutant", sorted(FORWARD_MUTANTS))
+def test_goldens_catch_planted_forward_mistakes(native_fixture, transformers_golden, monkeypatch,
+                                                mutant):
+    # the fixture checks the last position under masks; the transformers golden
+    # checks every position of an unmasked sequence (causality)
+    import dataclasses
+    from qdc_amd.config import plumbing_config
+    from qdc_amd.weights import random_weights
+    name, fn = FORWARD_MUTANTS[mutant]
+    monkeypatch.setattr(forward, name, fn)
+    cases = [c for c in native_fixture["cases"] if c[0].startswith(("ref04", "cuda13"))]
+    bad = [n for n, got, exp in fixture_logits(native_fixture, cases)
+           if not isapprox(got, exp, 2e-5, 2e-5)]
+    vocab, T, seed = (int(v) for v in transformers_golden["model/meta"])
+    cfg = dataclasses.replace(plumbing_config(), vocab=vocab)
+    got = forward.backbone_hidden(random_weights(cfg, seed=seed), cfg.as_dict(),
+                                  transformers_golden["model/ids"], np.ones(T, np.int8))
+    if normwise(got, transformers_golden["model/hidden"]) >= 2e-6:
+        bad.append("transformers plumbing")
+    assert bad, f"planted mistake '{mutant}' went unnoticed"
+
+
+def test_attention_softmax_against_scipy():
+    from scipy.special import softmax
+    rng = np.random.default_rng(5)
+    B, H, Q, K = 2, 3, 9, 12
+    scores = rng.standard_normal((B, H, Q, K), dtype=np.float32) * np.float32(4)
+    mask = (rng.random((B, K)) > 0.3).astype(np.int32)
+    mask[1, :] = 0
+    mask[1, 7] = 1          # batch 1: queries 0..3 (offset 3) see no unmasked key
+    for q_offset in (0, 3):
+        got = forward.attention_softmax(scores, mask, 0.125, q_offset)
+        for b in range(B):
+            for h in range(H):
+                for q in range(Q):
+                    vis = [i for i in range(K) if i <= q + q_offset and mask[b, i]]
+                    row = got[b, h, q]
+                    if not vis:  # no visible key: uniform over every key (reference behaviour)
+                        assert np.array_equal(row, np.full(K, np.float32(1) / np.float32(K)))
+                        continue
+                    exp = np.zeros(K, np.float64)
+                    exp[vis] = softmax(scores[b, h, q, vis].astype(np.float64) * 0.125)
+                    assert np.abs(row - exp).max() < 1e-6
+                    assert np.all(row[[i for i in range(K) if i not in vis]] == 0)
+
+
+def test_attention_gate_against_scipy():
+    from scipy.special import expit
+    rng = np.random.default_rng(6)
+    B, H, S, hd = 2, 3, 5, 4
+    values = rng.standard_normal((B, H, S, hd), dtype=np.float32)
+    gate = rng.standard_normal((B * S, H, hd), dtype=np.float32) * np.float32(3)
+    got = forward.attention_gate(values, gate)
+    for b in range(B):
+        for s in range(S):
+            for h in range(H):
+                exp = values[b, h, s] * expit(gate[b * S + s, h].astype(np.float64))
+                assert np.abs(got[b * S + s, h * hd:(h + 1) * hd] - exp).max() < 1e-6
