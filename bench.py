@@ -137,6 +137,47 @@ def build_kernels(dev):
                    torch.empty((Tr, Hr), dtype=bf, device=dev), torch.empty((Tr, Hr), dtype=bf, device=dev)),
         lambda s: ops.native_residual_rms(s[0], s[1], wr, 1e-6, residual=s[2], out=s[3]),
         [Tr, Hr], "bfloat16"))
+
+    # Attention row work of one full-attention layer (8 sequences of 2048, 8 heads).
+    # Softmax: the causally visible scores are read (the rest are -floatmax by
+    # definition and never loaded), every probability is written.
+    Ba, Ha, Sa = 8, 8, 2048
+    amask = torch.ones((Ba, Sa), dtype=torch.int32, device=dev)
+    kernels.append(Kernel(
+        "attn_softmax_bf16", "softmax_rows_fast",
+        Ba * Ha * Sa * (Sa + 1) // 2 * 4 + Ba * Ha * Sa * Sa * 2 + Ba * Sa * 4,
+        lambda i: (randn((Ba, Ha, Sa, Sa), f32),
+                   torch.empty((Ba, Ha, Sa, Sa), dtype=bf, device=dev)),
+        lambda s: ops.attention_softmax(s[0], amask, 0.0625, out=s[1]), [Ba, Ha, Sa, Sa],
+        "float32->bfloat16"))
+    hda = 256
+    kernels.append(Kernel(
+        "attn_gate_bf16", "gate_merge_fast",
+        Ba * Ha * Sa * hda * 4 + 2 * Ba * Sa * Ha * hda * 2,
+        lambda i: (randn((Ba, Ha, Sa, hda), f32), randn((Ba * Sa, Ha, 2 * hda), bf),
+                   torch.empty((Ba * Sa, Ha * hda), dtype=bf, device=dev)),
+        lambda s: ops.attention_gate(s[0], s[1][:, :, hda:], out=s[2]), [Ba * Sa, Ha, hda],
+        "bfloat16"))
+
+    # DeltaNet prologue of one layer: 16384 tokens, 16 key/value heads of 128,
+    # packed projection [qkv | z | a | b] in bf16 (z is not read), fp32 outputs.
+    Tp, hp, dp = 16384, 16, 128
+    cqp = 3 * hp * dp
+    widthp = cqp + hp * dp + 2 * hp
+    convp = randn((cqp, 4), f32, 0.5)
+    a_dec = -torch.exp(randn((hp,), f32, 0.5))
+    dtb = randn((hp,), f32)
+    kernels.append(Kernel(
+        "delta_prologue_bf16", "delta_prologue_fast",
+        Tp * (cqp + 2 * hp) * 2 + Tp * (cqp + 2 * hp) * 4 + cqp * 4 * 4 + 2 * hp * 4,
+        lambda i: (randn((Tp, widthp), bf),
+                   torch.empty((Tp, hp, dp), dtype=f32, device=dev),
+                   torch.empty((Tp, hp, dp), dtype=f32, device=dev),
+                   torch.empty((Tp, hp, dp), dtype=f32, device=dev),
+                   torch.empty((Tp, hp), dtype=f32, device=dev),
+                   torch.empty((Tp, hp), dtype=f32, device=dev)),
+        lambda s: ops.delta_prologue(s[0], convp, a_dec, dtb, 2048, hp, dp, hp, dp, out=s[1:]),
+        [Tp, hp, dp], "bfloat16->float32"))
     return kernels
 
 

@@ -13,19 +13,20 @@
 // qk_normalize_kernel! and the beta/decay broadcasts, ext/amdgpu_delta.jl:1-33, 83-113, 154-159.
 //
 // Fast path: a thread owns 8 consecutive channels (one 16-byte bf16 chunk of the
-// projection row) for a tile of kTile consecutive tokens and slides a K-tap
-// window down the tile, so each projection row is read once from HBM (plus a
-// K-1 row halo per tile from L2).  The kd/8 lanes of a key head are an aligned
+// projection row) for a tile of 16 (bf16) or 8 (fp32) consecutive tokens,
+// loads the tile's rows and the K-1 halo rows before it in one go, then slides
+// a K-tap window down the tile, so each projection row is read once from HBM
+// (the halo comes from L2).  The kd/8 lanes of a key head are an aligned
 // lane group, so the L2 norm reduces inside the group (DPP).  Outputs are fp32
 // (the recurrence reads fp32).  One extra row of blocks computes the gates.
 #include <cmath>
+#include <type_traits>
 
 #include "qdc_common.hpp"
 
 namespace qdc {
 namespace {
 
-constexpr int kTile = 16;   // tokens per thread
 constexpr int kTaps = 4;    // fast-path convolution width (the Qwen3.5 default)
 
 struct Prologue {
@@ -50,26 +51,18 @@ __device__ __forceinline__ float softplus_f(float x) {
     return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
 }
 
-template <typename T> __device__ __forceinline__ void load8(const T *p, float (&v)[8]);
-template <> __device__ __forceinline__ void load8<bf16_t>(const bf16_t *p, float (&v)[8]) {
-    unpack(load_raw(p), v);
-}
-template <> __device__ __forceinline__ void load8<float>(const float *p, float (&v)[8]) {
-    float a[4], b[4];
-    unpack(load_raw(p), a);
-    unpack(load_raw(p + 4), b);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = a[i];
-        v[4 + i] = b[i];
-    }
-}
+// Tokens per thread: the tile's rows plus the kTaps-1 halo rows are all loaded
+// before the first is used, so a thread keeps (tile + 3) 16-byte-per-8-channel
+// rows in flight.
+template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 16 : 8; }
 
 template <typename T, int LPH>
 __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
-    const int64_t t0 = (int64_t)blockIdx.x * kTile;
+    constexpr int kTileT = tile_for<T>();
+    constexpr int kRows = kTileT + kTaps - 1;  // rows t0-3 .. t0+tile-1
+    const int64_t t0 = (int64_t)blockIdx.x * kTileT;
     if (blockIdx.y == gridDim.y - 1) {  // gates row of the grid
-        for (int i = threadIdx.x; i < kTile * a.vh; i += kBlock) {
+        for (int i = threadIdx.x; i < kTileT * a.vh; i += kBlock) {
             const int64_t t = t0 + i / a.vh;
             const int h = i % a.vh;
             if (t >= a.tokens) continue;
@@ -87,62 +80,79 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     const bool is_q = ci < a.qk_chunks / 2, is_k = !is_q && ci < a.qk_chunks;
     const T *base = reinterpret_cast<const T *>(a.proj) + c0;
 
+    // position of t0 in its sequence; rows before that sequence's start are zero
+    // for every token of the tile
+    const uint32_t s0 = (uint32_t)t0 - fastdiv((uint32_t)t0, a.seq) * a.seq.d;
+    const int64_t seq_start = t0 - s0;
+    Frag<T, 8> rows[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int64_t t = t0 - (kTaps - 1) + r;
+        if (live && t >= seq_start && t < a.tokens) {
+            rows[r] = load_frag<T, 8>(base + t * a.ld);
+        } else {
+#pragma unroll
+            for (int i = 0; i < Frag<T, 8>::kN; ++i) rows[r].r[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
     float w[8][kTaps];
 #pragma unroll
     for (int c = 0; c < 8; ++c)
 #pragma unroll
         for (int j = 0; j < kTaps; ++j) w[c][j] = live ? a.conv[(c0 + c) * kTaps + j] : 0.0f;
 
-    // win[j] holds input row t - (kTaps-1) + j; rows before the tile are the halo
-    float win[kTaps][8];
-#pragma unroll
-    for (int j = 0; j < kTaps; ++j)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) win[j][c] = 0.0f;
-#pragma unroll
-    for (int j = 1; j < kTaps; ++j) {
-        const int64_t t = t0 - kTaps + j;  // becomes slot j-1 after the first slide
-        if (live && t >= 0 && t < a.tokens) load8<T>(base + t * a.ld, win[j]);
-    }
-
-    for (int tt = 0; tt < kTile; ++tt) {
+    const int64_t kw = (int64_t)a.kh * a.kd, vw = (int64_t)a.vh * a.vd;
+    // A later sequence starts inside the tile only when fewer than kTileT
+    // positions remain in t0's sequence; only then do taps need a per-token mask.
+    const bool inner_start = a.seq.d - s0 < (uint32_t)kTileT;
+    auto token = [&](int tt, auto masked) {
         const int64_t t = t0 + tt;
         const bool tok = t < a.tokens;
-        // slide the window and bring in row t
+        uint32_t s = 0;  // position of t in its sequence (masked tiles only)
+        if constexpr (decltype(masked)::value)
+            s = tok ? (uint32_t)t - fastdiv((uint32_t)t, a.seq) * a.seq.d : 0u;
+        float x[kTaps][8];
 #pragma unroll
-        for (int j = 0; j < kTaps - 1; ++j)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) win[j][c] = win[j + 1][c];
-        if (live && tok) load8<T>(base + t * a.ld, win[kTaps - 1]);
-        // taps reaching before the start of this token's sequence read zeros
-        const uint32_t s = tok ? (uint32_t)t - fastdiv((uint32_t)t, a.seq) * a.seq.d : 0u;
+        for (int j = 0; j < kTaps; ++j) unpack(rows[tt + j], x[j]);  // row t - (kTaps-1) + j
         float m[8];
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
+            // tap j multiplies row t - (kTaps-1) + j; fused multiply-add per tap
             float acc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kTaps; ++j)
-                if (s >= (uint32_t)(kTaps - 1 - j)) acc = acc + win[j][c] * w[c][j];
+            for (int j = 0; j < kTaps; ++j) {
+                if constexpr (decltype(masked)::value) {
+                    if (s >= (uint32_t)(kTaps - 1 - j)) acc = __builtin_fmaf(x[j][c], w[c][j], acc);
+                } else {
+                    acc = __builtin_fmaf(x[j][c], w[c][j], acc);
+                }
+            }
             m[c] = silu(acc);
         }
         float ss = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) ss += m[c] * m[c];
+        for (int c = 0; c < 8; ++c) ss = __builtin_fmaf(m[c], m[c], ss);
         ss = group_sum<LPH>(ss);  // whole aligned head groups: q/k rows only use it
-        if (!live || !tok) continue;
-        float *dst;
-        if (is_q || is_k) {
-            const float scale = is_q ? 1.0f / (__builtin_sqrtf(ss + 1e-6f) * a.sqrt_kd)
-                                     : 1.0f / __builtin_sqrtf(ss + 1e-6f);
+        if (live && tok) {
+            float *dst;
+            if (is_q || is_k) {
+                const float scale = is_q ? 1.0f / (__builtin_sqrtf(ss + 1e-6f) * a.sqrt_kd)
+                                         : 1.0f / __builtin_sqrtf(ss + 1e-6f);
 #pragma unroll
-            for (int c = 0; c < 8; ++c) m[c] = m[c] * scale;
-            const int64_t kw = (int64_t)a.kh * a.kd;
-            dst = is_q ? a.q + t * kw + c0 : a.k + t * kw + (c0 - kw);
-        } else {
-            const int64_t vw = (int64_t)a.vh * a.vd;
-            dst = a.v + t * vw + (c0 - 2 * (int64_t)a.kh * a.kd);
+                for (int c = 0; c < 8; ++c) m[c] = m[c] * scale;
+                dst = is_q ? a.q + t * kw + c0 : a.k + t * kw + (c0 - kw);
+            } else {
+                dst = a.v + t * vw + (c0 - 2 * kw);
+            }
+            store_frag<8>(dst, m);
         }
-        store_frag<8>(dst, m);
+    };
+    if (!inner_start) {
+#pragma unroll
+        for (int tt = 0; tt < kTileT; ++tt) token(tt, std::false_type{});
+    } else {
+#pragma unroll
+        for (int tt = 0; tt < kTileT; ++tt) token(tt, std::true_type{});
     }
 }
 
@@ -195,7 +205,8 @@ int32_t launch(const Prologue &p, bool fast, hipStream_t stream) {
     if (fast && p.kd % 8 == 0 && p.vd % 8 == 0 && p.taps == kTaps && lph <= kWave &&
         (lph & (lph - 1)) == 0) {
         // x: token tiles; y: channel blocks plus one for the gates
-        const dim3 grid((uint32_t)ceil_div(p.tokens, kTile), (uint32_t)ceil_div(p.chunks, kBlock) + 1);
+        const dim3 grid((uint32_t)ceil_div(p.tokens, tile_for<T>()),
+                        (uint32_t)ceil_div(p.chunks, kBlock) + 1);
 #define QDC_PRO(L)                                                                               \
     case L:                                                                                      \
         hipLaunchKernelGGL((delta_prologue_fast<T, L>), grid, dim3(kBlock), 0, stream, p);     \

@@ -9,59 +9,158 @@
 //     f = exp(decay[t]);  u = beta[t] * (v[t] - f * S k[t]);
 //     S = f * S + u k[t]^T;  out[t] = S q[t]
 //
-// Mapping: a wavefront is 4 groups of 16 lanes; each group owns R consecutive
-// value rows of one (b, h) and splits the key dimension across its lanes (lane
-// i holds key components i*KPL .. i*KPL+KPL-1, loaded as 16-byte chunks), so
-// both dot products per row and token reduce over 16 lanes with 4 DPP steps and
-// no cross-row traffic.  The state (R x KPL values per lane) stays in
-// registers; the next token's k, q, v, beta and decay are loaded while the
-// current token is computed.
+// Mapping: a workgroup (4 wavefronts = 16 groups of 16 lanes) owns 16*R
+// consecutive value rows of one (b, h); each 16-lane group owns R rows and splits
+// the key dimension across its lanes, so both dot products per row and token
+// reduce over 16 lanes with 4 DPP steps.  The state (R x KPL values per lane)
+// stays in registers for the whole sequence.  Tokens are processed in chunks of
+// kChunk: the chunk's k, q (key head g), v (the block's rows), beta and decay are
+// staged in LDS by the whole workgroup, and the next chunk's global loads are
+// issued before the current chunk's steps run, so the sequential steps read
+// only LDS.  Outputs of a chunk are gathered in LDS and written as whole rows.
+#include <type_traits>
+
 #include "qdc_common.hpp"
 
 namespace qdc {
 namespace {
 
-constexpr int kGroup = 16;        // lanes per key split
-constexpr int kGroups = kWave / kGroup;
-constexpr int kRowsPerGroup = 2;  // value rows per 16-lane group
+constexpr int kGroup = 16;                       // lanes per key split
+constexpr int kGroupsPerBlock = kBlock / kGroup; // 16
+constexpr int kChunk = 16;                       // tokens staged per LDS buffer
 
-template <int KPL> __device__ __forceinline__ void load_keys(const float *p, bool full, int valid,
+// Key component held in slot i of lane `lane`: blocks of 4 consecutive keys
+// dealt round-robin over the 16 lanes (conflict-free 16-byte LDS reads) when a
+// lane holds a multiple of 4 keys, else KPL consecutive keys.
+template <int KPL> __device__ __forceinline__ int key_of(int lane, int i) {
+    if constexpr (KPL % 4 == 0) return (i / 4) * (4 * kGroup) + lane * 4 + (i % 4);
+    else return lane * KPL + i;
+}
+
+template <int KPL> __device__ __forceinline__ void read_keys(const float *row, int lane,
                                                              float (&out)[KPL]) {
-    if (KPL % 4 == 0 && full) {
+    if constexpr (KPL % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < KPL; i += 4) {
-            const f32x4 c = *reinterpret_cast<const f32x4 *>(p + i);
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(row + key_of<KPL>(lane, i));
             out[i] = c.x; out[i + 1] = c.y; out[i + 2] = c.z; out[i + 3] = c.w;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) out[i] = i < valid ? p[i] : 0.0f;
+        for (int i = 0; i < KPL; ++i) out[i] = row[key_of<KPL>(lane, i)];
     }
 }
 
-template <int KPL, typename TO>
-__global__ __launch_bounds__(kWave) void delta_scan(
-    TO *__restrict__ out, const float *__restrict__ q, const float *__restrict__ k,
-    const float *__restrict__ v, const float *__restrict__ beta, const float *__restrict__ decay,
-    int S, int H, int KH, int KD, int vd, int groups, bool vec) {
-    constexpr int R = kRowsPerGroup;
-    const int lane = threadIdx.x % kGroup;
-    const int grp = threadIdx.x / kGroup;
-    const int r0 = (blockIdx.x * kGroups + grp) * R;  // first value row of this group
+struct ScanArgs {
+    void *out;
+    const float *q, *k, *v, *beta, *decay;
+    int S, H, KH, KD, vd, groups;
+};
+
+template <int KPL, int R, bool VEC, typename TO>
+__global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
+    constexpr int KP = KPL * kGroup;             // padded key dimension
+    constexpr int RB = R * kGroupsPerBlock;      // value rows per workgroup
+    // chunk elements per thread for the staged loads (upper bounds)
+    constexpr int KQ_ITEMS = VEC ? (kChunk * KP / 4 + kBlock - 1) / kBlock
+                                 : (kChunk * KP + kBlock - 1) / kBlock;
+    constexpr int V_ITEMS = (kChunk * RB + kBlock - 1) / kBlock;
+    __shared__ __align__(16) float sk[2][kChunk][KP];
+    __shared__ __align__(16) float sq[2][kChunk][KP];
+    __shared__ float sv[2][kChunk][RB];
+    __shared__ float sb[2][kChunk], sd[2][kChunk];
+    __shared__ float so[kChunk][RB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid % kGroup, grp = tid / kGroup;
     const int h = blockIdx.y, b = blockIdx.z;
-    const int g = h / groups;
-    // this lane's key components [j0, j0 + valid); lanes past key_dim hold zeros
-    const int j0 = lane * KPL;
-    const int valid = max(0, min(KPL, KD - j0));
-    // 16-byte key loads need 16-byte aligned q/k and key_dim % 4 == 0 (checked on the host)
-    const bool full = vec && valid == KPL;
-    const int64_t k_tok = (int64_t)KH * KD, v_tok = (int64_t)H * vd, s_tok = H;
-    const float *kp = k + (int64_t)b * S * k_tok + (int64_t)g * KD + min(j0, KD - 1);
-    const float *qp = q + (int64_t)b * S * k_tok + (int64_t)g * KD + min(j0, KD - 1);
-    const float *vp = v + (int64_t)b * S * v_tok + (int64_t)h * vd;
-    const float *bp = beta + (int64_t)b * S * s_tok + h;
-    const float *dp = decay + (int64_t)b * S * s_tok + h;
-    TO *op = out + (int64_t)b * S * v_tok + (int64_t)h * vd;
+    const int g = h / a.groups;
+    const int row0 = blockIdx.x * RB;            // first value row of the workgroup
+    const int KD = a.KD, S = a.S;
+    const int64_t k_tok = (int64_t)a.KH * KD, v_tok = (int64_t)a.H * a.vd;
+    const float *kb = a.k + (int64_t)b * S * k_tok + (int64_t)g * KD;
+    const float *qb = a.q + (int64_t)b * S * k_tok + (int64_t)g * KD;
+    const float *vb = a.v + (int64_t)b * S * v_tok + (int64_t)h * a.vd;
+    const float *bb = a.beta + (int64_t)b * S * a.H + h;
+    const float *db = a.decay + (int64_t)b * S * a.H + h;
+    TO *ob = reinterpret_cast<TO *>(a.out) + (int64_t)b * S * v_tok + (int64_t)h * a.vd;
+
+    // padded key components stay zero for the whole launch
+    for (int i = tid; i < 2 * kChunk * KP; i += kBlock) {
+        (&sk[0][0][0])[i] = 0.0f;
+        (&sq[0][0][0])[i] = 0.0f;
+    }
+
+    // staged registers of one chunk
+    using Item = typename std::conditional<VEC, f32x4, float>::type;
+    Item rk[KQ_ITEMS], rq[KQ_ITEMS];
+    float rv[V_ITEMS], rb = 0.0f, rd = 0.0f;
+    const int kd4 = KD / 4;
+    auto fetch = [&](int c) {  // global -> registers for chunk c
+        const int t0 = c * kChunk;
+        const int n = min(kChunk, S - t0);
+#pragma unroll
+        for (int p = 0; p < KQ_ITEMS; ++p) {
+            const int idx = tid + p * kBlock;
+            rk[p] = Item{};
+            rq[p] = Item{};
+            if constexpr (VEC) {
+                const int tt = idx / kd4, j4 = idx - tt * kd4;
+                if (tt < n) {
+                    const int64_t off = (int64_t)(t0 + tt) * k_tok + j4 * 4;
+                    rk[p] = *reinterpret_cast<const f32x4 *>(kb + off);
+                    rq[p] = *reinterpret_cast<const f32x4 *>(qb + off);
+                }
+            } else {
+                const int tt = idx / KD, j = idx - tt * KD;
+                if (tt < n) {
+                    const int64_t off = (int64_t)(t0 + tt) * k_tok + j;
+                    rk[p] = kb[off];
+                    rq[p] = qb[off];
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < V_ITEMS; ++p) {
+            const int idx = tid + p * kBlock;
+            const int tt = idx / RB, r = idx - tt * RB;
+            rv[p] = (tt < n && row0 + r < a.vd) ? vb[(int64_t)(t0 + tt) * v_tok + row0 + r] : 0.0f;
+        }
+        if (tid < n) {
+            rb = bb[(int64_t)(t0 + tid) * a.H];
+            rd = db[(int64_t)(t0 + tid) * a.H];
+        }
+    };
+    auto stage = [&](int c, int buf) {  // registers -> LDS buffer for chunk c
+        const int n = min(kChunk, S - c * kChunk);
+#pragma unroll
+        for (int p = 0; p < KQ_ITEMS; ++p) {
+            const int idx = tid + p * kBlock;
+            if constexpr (VEC) {
+                const int tt = idx / kd4, j4 = idx - tt * kd4;
+                if (tt < n) {  // rows are staged in natural key order
+                    *reinterpret_cast<f32x4 *>(&sk[buf][tt][j4 * 4]) = rk[p];
+                    *reinterpret_cast<f32x4 *>(&sq[buf][tt][j4 * 4]) = rq[p];
+                }
+            } else {
+                const int tt = idx / KD, j = idx - tt * KD;
+                if (tt < n) {
+                    sk[buf][tt][j] = rk[p];
+                    sq[buf][tt][j] = rq[p];
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < V_ITEMS; ++p) {
+            const int idx = tid + p * kBlock;
+            const int tt = idx / RB;
+            if (tt < kChunk) sv[buf][tt][idx - tt * RB] = rv[p];
+        }
+        if (tid < n) {
+            sb[buf][tid] = rb;
+            sd[buf][tid] = rd;
+        }
+    };
 
     float st[R][KPL];
 #pragma unroll
@@ -69,52 +168,57 @@ __global__ __launch_bounds__(kWave) void delta_scan(
 #pragma unroll
         for (int i = 0; i < KPL; ++i) st[r][i] = 0.0f;
 
-    float kn[KPL], qn[KPL], vn[R], bn = 0.0f, dn = 0.0f;
-    auto fetch = [&](int t) {
-        load_keys<KPL>(kp + (int64_t)t * k_tok, full, valid, kn);
-        load_keys<KPL>(qp + (int64_t)t * k_tok, full, valid, qn);
+    const int chunks = (S + kChunk - 1) / kChunk;
+    __syncthreads();  // zero padding written
+    fetch(0);
+    stage(0, 0);
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < chunks) fetch(c + 1);  // in flight during this chunk's steps
+        const int n = min(kChunk, S - c * kChunk);
+        for (int tt = 0; tt < n; ++tt) {
+            float kt[KPL], qt[KPL];
+            read_keys<KPL>(&sk[buf][tt][0], lane, kt);
+            read_keys<KPL>(&sq[buf][tt][0], lane, qt);
+            const float bt = sb[buf][tt], f = __expf(sd[buf][tt]);
+            float pred[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) vn[r] = r0 + r < vd ? vp[(int64_t)t * v_tok + r0 + r] : 0.0f;
-        bn = bp[(int64_t)t * s_tok];
-        dn = dp[(int64_t)t * s_tok];
-    };
-    if (S > 0) fetch(0);
-    for (int t = 0; t < S; ++t) {
-        float kt[KPL], qt[KPL], vt[R];
+            for (int r = 0; r < R; ++r) {
+                float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) {
-            kt[i] = kn[i];
-            qt[i] = qn[i];
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) vt[r] = vn[r];
-        const float bt = bn, f = __expf(dn);
-        if (t + 1 < S) fetch(t + 1);
-
-        float pred[R], o[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < KPL; ++i) s += st[r][i] * kt[i];
-            pred[r] = group_sum<kGroup>(s);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float u = bt * (vt[r] - f * pred[r]);
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < KPL; ++i) {
-                st[r][i] = f * st[r][i] + u * kt[i];
-                s += st[r][i] * qt[i];
+                for (int i = 0; i < KPL; ++i) s = __builtin_fmaf(st[r][i], kt[i], s);
+                pred[r] = group_sum<kGroup>(s);
             }
-            o[r] = group_sum<kGroup>(s);
-        }
-        // lane r of the group stores row r0 + r
-        float mine = 0.0f;
+            float o[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) mine = lane == r ? o[r] : mine;
-        if (lane < R && r0 + lane < vd) op[(int64_t)t * v_tok + r0 + lane] = from_f32<TO>(mine);
+            for (int r = 0; r < R; ++r) {
+                const float u = bt * (sv[buf][tt][grp * R + r] - f * pred[r]);
+                float s = 0.0f;
+#pragma unroll
+                for (int i = 0; i < KPL; ++i) {
+                    st[r][i] = __builtin_fmaf(u, kt[i], f * st[r][i]);
+                    s = __builtin_fmaf(st[r][i], qt[i], s);
+                }
+                o[r] = group_sum<kGroup>(s);
+            }
+            if (lane < R) {
+                float mine = o[0];
+#pragma unroll
+                for (int r = 1; r < R; ++r) mine = lane == r ? o[r] : mine;
+                so[tt][grp * R + lane] = mine;
+            }
+        }
+        __syncthreads();  // steps done: `so` complete, buffer `buf` free
+        if (c + 1 < chunks) stage(c + 1, buf ^ 1);
+#pragma unroll
+        for (int p = 0; p < V_ITEMS; ++p) {
+            const int idx = tid + p * kBlock;
+            const int tt = idx / RB, r = idx - tt * RB;
+            if (tt < n && row0 + r < a.vd)
+                ob[(int64_t)(c * kChunk + tt) * v_tok + row0 + r] = from_f32<TO>(so[tt][r]);
+        }
+        __syncthreads();  // next buffer staged, `so` read
     }
 }
 
@@ -137,29 +241,46 @@ extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, 
         value_dim >= ((int64_t)1 << 24))
         return QDC_ERR_SHAPE;
     if (!out || !q || !k || !v || !beta || !decay) return QDC_ERR_NULL;
-    const int rows_per_block = kGroups * kRowsPerGroup;
-    const dim3 grid((uint32_t)ceil_div(value_dim, rows_per_block), (uint32_t)heads,
-                    (uint32_t)batch);
-    const int groups = (int)(heads / key_heads);
-    const int S = (int)seq, H = (int)heads, KH = (int)key_heads, KD = (int)key_dim;
-    const int vd = (int)value_dim;
-#define QDC_SCAN(KPL, TO)                                                                       \
-    hipLaunchKernelGGL((delta_scan<KPL, TO>), grid, dim3(kWave), 0, stream, (TO *)out, q, k, v,  \
-                       beta, decay, S, H, KH, KD, vd, groups, vec);                              \
-    return launch_status();
-    const int64_t kpl = ceil_div(key_dim, kGroup);
+    ScanArgs a{};
+    a.out = out;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.beta = beta;
+    a.decay = decay;
+    a.S = (int)seq;
+    a.H = (int)heads;
+    a.KH = (int)key_heads;
+    a.KD = (int)key_dim;
+    a.vd = (int)value_dim;
+    a.groups = (int)(heads / key_heads);
+    // Two value rows per 16-lane group, or one when that leaves too few
+    // workgroups to occupy the GPU (single sequences with few heads).
+    const int64_t blocks2 = ceil_div(value_dim, 2 * kGroupsPerBlock) * heads * batch;
+    const bool two = blocks2 >= 512;
+    const int64_t rb = (two ? 2 : 1) * kGroupsPerBlock;
+    const dim3 grid((uint32_t)ceil_div(value_dim, rb), (uint32_t)heads, (uint32_t)batch);
     const bool vec = aligned16(q) && aligned16(k) && key_dim % 4 == 0;
-    if (out_dtype == QDC_BF16) {
-        if (kpl <= 1) { QDC_SCAN(1, bf16_t) }
-        if (kpl <= 2) { QDC_SCAN(2, bf16_t) }
-        if (kpl <= 4) { QDC_SCAN(4, bf16_t) }
-        if (kpl <= 8) { QDC_SCAN(8, bf16_t) }
-        QDC_SCAN(16, bf16_t)
-    }
-    if (kpl <= 1) { QDC_SCAN(1, float) }
-    if (kpl <= 2) { QDC_SCAN(2, float) }
-    if (kpl <= 4) { QDC_SCAN(4, float) }
-    if (kpl <= 8) { QDC_SCAN(8, float) }
-    QDC_SCAN(16, float)
+    const int64_t kpl = ceil_div(key_dim, kGroup);
+#define QDC_SCAN(KPL, R, VEC, TO)                                                              \
+    hipLaunchKernelGGL((delta_scan<KPL, R, VEC, TO>), grid, dim3(kBlock), 0, stream, a);      \
+    return launch_status();
+#define QDC_SCAN_R(KPL, VEC, TO)                                                               \
+    if (two) { QDC_SCAN(KPL, 2, VEC, TO) }                                                     \
+    QDC_SCAN(KPL, 1, VEC, TO)
+#define QDC_SCAN_V(KPL, TO)                                                                    \
+    if (vec) { QDC_SCAN_R(KPL, true, TO) }                                                     \
+    QDC_SCAN_R(KPL, false, TO)
+#define QDC_SCAN_K(TO)                                                                         \
+    if (kpl <= 1) { QDC_SCAN_V(1, TO) }                                                        \
+    if (kpl <= 2) { QDC_SCAN_V(2, TO) }                                                        \
+    if (kpl <= 4) { QDC_SCAN_V(4, TO) }                                                        \
+    if (kpl <= 8) { QDC_SCAN_V(8, TO) }                                                        \
+    QDC_SCAN_V(16, TO)
+    if (out_dtype == QDC_BF16) { QDC_SCAN_K(bf16_t) }
+    QDC_SCAN_K(float)
+#undef QDC_SCAN_K
+#undef QDC_SCAN_V
+#undef QDC_SCAN_R
 #undef QDC_SCAN
 }

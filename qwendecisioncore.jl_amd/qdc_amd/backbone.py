@@ -30,7 +30,7 @@ import torch
 
 from . import ops
 from .config import BackboneConfig, load_config
-from .weights import read_checkpoint
+from .weights import read_checkpoint_tensors
 
 
 
@@ -99,9 +99,12 @@ class QwenBackbone:
     @classmethod
     def from_directory(cls, directory: str, device="cuda:0",
                        dtype: torch.dtype = torch.float32) -> "QwenBackbone":
-        """A local safetensors checkpoint directory (no network access)."""
+        """A local safetensors checkpoint directory (no network access).  Tensors
+        load straight onto ``device`` in their stored dtype; with ``dtype=bfloat16``
+        a BF16 checkpoint is never widened to fp32 (the packed projection weights
+        are assembled on the device in bf16)."""
         cfg = load_config(directory)
-        weights = read_checkpoint(directory)
+        weights = read_checkpoint_tensors(directory, device=device)
         cfg = BackboneConfig(**{**cfg.as_dict(), "vocab": weights["embed_tokens.weight"].shape[0],
                                 "intermediate": weights["layers.0.mlp.gate_proj.weight"].shape[0],
                                 "layer_types": cfg.layer_types})

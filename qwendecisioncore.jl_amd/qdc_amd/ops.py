@@ -300,10 +300,11 @@ def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Te
 
 def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor,
                    dt_bias: torch.Tensor, seq_len: int, key_heads: int, key_dim: int,
-                   value_heads: int, value_dim: int):
+                   value_heads: int, value_dim: int, out=None):
     """DeltaNet prologue on the packed projection ``[T, q|k|v|z|a|b]`` (rows
     contiguous): causal conv + SiLU, q/k L2 norm, beta/decay gates.  Returns fp32
-    ``q, k [T, KH, kd]``, ``v [T, H, vd]``, ``beta, decay [T, H]``."""
+    ``q, k [T, KH, kd]``, ``v [T, H, vd]``, ``beta, decay [T, H]`` (into ``out``,
+    a tuple of five such contiguous tensors, when given)."""
     _device(proj, conv, a_decay, dt_bias)
     if proj.dtype not in _DTYPES or proj.dim() != 2 or proj.stride(1) != 1:
         raise ValueError("proj must be a [tokens, width] float32/bfloat16 view with unit column stride")
@@ -314,11 +315,14 @@ def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor
     taps = conv.shape[-1]
     dev = proj.device
     f32 = torch.float32
-    q = torch.empty((T, key_heads, key_dim), dtype=f32, device=dev)
-    k = torch.empty_like(q)
-    v = torch.empty((T, value_heads, value_dim), dtype=f32, device=dev)
-    beta = torch.empty((T, value_heads), dtype=f32, device=dev)
-    decay = torch.empty_like(beta)
+    shapes = [(T, key_heads, key_dim), (T, key_heads, key_dim), (T, value_heads, value_dim),
+              (T, value_heads), (T, value_heads)]
+    if out is None:
+        out = [torch.empty(sh, dtype=f32, device=dev) for sh in shapes]
+    elif any(o.dtype != f32 or tuple(o.shape) != sh or not o.is_contiguous()
+             for o, sh in zip(out, shapes)):
+        raise ValueError("out must be five contiguous float32 tensors of the output shapes")
+    q, k, v, beta, decay = out
     ld = proj.stride(0) if T > 1 else proj.shape[1]
     check(lib().qdc_delta_prologue(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
                                    decay.data_ptr(), proj.data_ptr(), _DTYPES[proj.dtype], ld,

@@ -4,6 +4,7 @@
 
 ``read_checkpoint`` follows ``read_native_weights`` (``src/safetensors.jl:3-35``)
 and the name canonicalisation of ``QwenBackbone`` (``src/backbone.jl:107-134``);
+``read_checkpoint_tensors`` is the device loader that keeps BF16 weights in bf16;
 ``random_weights`` builds the synthetic random-init backbones.
 """
 from __future__ import annotations
@@ -89,26 +90,51 @@ def random_device_weights(cfg: BackboneConfig, seed: int = 0, device="cuda:0", d
     return out
 
 
-def read_checkpoint(directory: str) -> dict:
-    """Load every ``language_model.*`` tensor of a local safetensors checkpoint
-    (single file or sharded index) widened to fp32 (``src/safetensors.jl:28-30``)."""
-    from safetensors.numpy import load_file  # safe loader: no code from the file is run
-
+def _checkpoint_files(directory: str) -> list:
+    """The safetensors files of a local checkpoint: ``model.safetensors`` or the
+    shards named by ``model.safetensors.index.json`` (``src/safetensors.jl:3-17``)."""
     single = os.path.join(directory, "model.safetensors")
     if os.path.isfile(single):
-        files = ["model.safetensors"]
-    else:
-        with open(os.path.join(directory, "model.safetensors.index.json")) as f:
-            files = sorted(set(json.load(f)["weight_map"].values()))
-    out = {}
+        return ["model.safetensors"]
+    with open(os.path.join(directory, "model.safetensors.index.json")) as f:
+        files = sorted(set(json.load(f)["weight_map"].values()))
     for fname in files:
         if os.path.isabs(fname) or ".." in fname.split("/"):
             raise ValueError(f"Unsafe shard path {fname}.")
-        for name, value in load_file(os.path.join(directory, fname)).items():
-            at = name.find("language_model.")
-            if at < 0:
-                continue
-            if value.dtype == np.uint16:  # raw bf16 bits
-                value = (value.astype(np.uint32) << 16).view(np.float32)
-            out[name[at + len("language_model."):]] = np.asarray(value, dtype=np.float32)
+    return files
+
+
+def _strip(name: str):
+    at = name.find("language_model.")
+    return None if at < 0 else name[at + len("language_model."):]
+
+
+def read_checkpoint_tensors(directory: str, device="cpu") -> dict:
+    """Every ``language_model.*`` tensor of a local safetensors checkpoint as a
+    torch tensor in its stored dtype, loaded straight onto ``device``: BF16
+    weights stay bf16 (no fp32 widening, half the bytes of the widened load of
+    ``src/safetensors.jl:28-30``).  Safe loader: nothing in the file is executed."""
+    from safetensors.torch import load_file
+
+    out = {}
+    for fname in _checkpoint_files(directory):
+        for name, value in load_file(os.path.join(directory, fname), device=str(device)).items():
+            key = _strip(name)
+            if key is not None:
+                out[key] = value
+    return out
+
+
+def read_checkpoint(directory: str) -> dict:
+    """Load every ``language_model.*`` tensor of a local safetensors checkpoint
+    (single file or sharded index) widened to fp32 numpy (``src/safetensors.jl:28-30``)."""
+    import torch
+
+    out = {}
+    for key, value in read_checkpoint_tensors(directory, device="cpu").items():
+        if value.dtype == torch.bfloat16:  # widen: bits << 16, exact
+            bits = value.contiguous().view(torch.int16).numpy().view(np.uint16)
+            out[key] = (bits.astype(np.uint32) << 16).view(np.float32)
+        else:
+            out[key] = value.to(torch.float32).numpy()
     return out

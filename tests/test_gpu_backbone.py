@@ -215,3 +215,24 @@ def test_full_depth_qwen35_backbone(dtype):
     print(f"full-depth qwen3.5 bf16: GPU vs fp32 oracle {err32:.2e}; bf16-storage oracle vs fp32 "
           f"oracle {drift:.2e}; GPU vs bf16-storage oracle {normwise(got, expbf):.2e}", flush=True)
     assert err32 <= max(1e-2, 1.25 * drift)
+
+
+def test_bf16_checkpoint_directory(native_fixture, tmp_path):
+    """QwenBackbone(dir) on a BF16 safetensors checkpoint: loaded onto the GPU in
+    bf16 (no widening) and packed there; the forward equals the in-memory build of
+    the same weights bit for bit, and the fp32 build matches the oracle."""
+    from test_checkpoint import _write
+    from qdc_amd import backbone
+    weights = _write(str(tmp_path))                      # bf16-representable fp32 arrays
+    cfg = fixture_cfg(native_fixture)
+    from_dir = backbone.QwenBackbone.from_directory(str(tmp_path), "cuda:0", torch.bfloat16)
+    assert from_dir.layers[0]["gate_up"].dtype == torch.bfloat16
+    in_mem = model_for(weights, cfg, torch.bfloat16)
+    name, ids, mask, _ = native_fixture["cases"][3]
+    a = backbone.backbone_hidden(from_dir, ids[0], mask[0])
+    b = backbone.backbone_hidden(in_mem, ids[0], mask[0])
+    assert np.array_equal(a, b)
+    wide = backbone.QwenBackbone.from_directory(str(tmp_path), "cuda:0", torch.float32)
+    exp = forward.backbone_hidden(weights, native_fixture["cfg"], ids[0], mask[0])
+    got = backbone.backbone_hidden(wide, ids[0], mask[0])
+    assert normwise(got, exp) <= 1e-5, normwise(got, exp)
