@@ -13,13 +13,24 @@ A step is one launch of each fused kernel over its synthetic batch:
   gated_rms_bf16     DeltaNet output x, z [16384, 16, 128] bf16
   residual_rms_bf16  x, mixed [16384, 1024] bf16 -> residual, normalised
 
+The same run measures the kernels that widen the path around the attention and
+DeltaNet layers (reported under "widened", not in `value`):
+
+  attn_softmax_bf16    masked softmax of scores [8, 8, 2048, 2048] fp32 -> bf16
+                       (causally hidden scores are never read)
+  attn_gate_bf16       PV output [8, 8, 2048, 256] fp32 x sigmoid(gate) -> bf16
+  delta_prologue_bf16  DeltaNet conv + SiLU + q/k L2 norm + gates, 16384 tokens,
+                       16 key/value heads of 128, packed bf16 projection -> fp32
+  delta_scan_bf16      gated delta rule over 8 x 2048 tokens, 16 heads 128 x 128
+                       (bound by vector ALU issue; reported in TFLOP/s too)
+
 Inputs are resident in HBM before timing.  Every kernel cycles through
 several input/output buffer sets totalling more than 512 MB, so the 256 MB
 last-level cache cannot serve repeated launches.  The K launches of each
 kernel are captured once in a HIP graph (no host launch overhead between the
 few-microsecond kernels) and replayed between HIP events recorded on the same
 stream; a kernel's average launch duration is its replay time / K.  value =
-total algorithmic bytes of the K steps / total time (GB/s).  Algorithmic bytes
+total algorithmic bytes of the K steps / total time of the fused row kernels (GB/s).  Algorithmic bytes
 = inputs read once + outputs written once + parameter vectors (+ RoPE tables).
 
 The CPU baseline times the C oracle (a single-threaded restatement of the
@@ -45,6 +56,7 @@ for _p in (ROOT, os.path.join(ROOT, "qwendecisioncore.jl_amd")):
 
 METRIC = "achieved HBM GB/s (% of peak) per fused kernel; backbone_hidden tokens/s"
 PEAK_GBS = 8000.0            # MI355X HBM3E
+VALU_PEAK_TF = 78.6          # fp32 FMA on the vector ALUs without packed-fp32 instructions
 ROTATE_BYTES = 640 << 20     # > 2x the 256 MB last-level cache
 PMC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
 
@@ -56,9 +68,11 @@ def _sets(set_bytes: int) -> int:
 class Kernel:
     """One fused kernel at its benchmark shape with rotating buffer sets."""
 
-    def __init__(self, name, symbol, algo_bytes, make_set, launch, shape, dtype):
+    def __init__(self, name, symbol, algo_bytes, make_set, launch, shape, dtype, group="hot",
+                 flops=None):
         self.name, self.symbol, self.algo_bytes = name, symbol, algo_bytes
         self.shape, self.dtype = shape, dtype
+        self.group, self.flops = group, flops  # "hot": the fused row kernels; "next": widened
         self.launch = launch
         self.sets = [make_set(i) for i in range(_sets(algo_bytes))]
         self.graph = None
@@ -149,7 +163,7 @@ def build_kernels(dev):
         lambda i: (randn((Ba, Ha, Sa, Sa), f32),
                    torch.empty((Ba, Ha, Sa, Sa), dtype=bf, device=dev)),
         lambda s: ops.attention_softmax(s[0], amask, 0.0625, out=s[1]), [Ba, Ha, Sa, Sa],
-        "float32->bfloat16"))
+        "float32->bfloat16", group="next"))
     hda = 256
     kernels.append(Kernel(
         "attn_gate_bf16", "gate_merge_fast",
@@ -157,7 +171,7 @@ def build_kernels(dev):
         lambda i: (randn((Ba, Ha, Sa, hda), f32), randn((Ba * Sa, Ha, 2 * hda), bf),
                    torch.empty((Ba * Sa, Ha * hda), dtype=bf, device=dev)),
         lambda s: ops.attention_gate(s[0], s[1][:, :, hda:], out=s[2]), [Ba * Sa, Ha, hda],
-        "bfloat16"))
+        "bfloat16", group="next"))
 
     # DeltaNet prologue of one layer: 16384 tokens, 16 key/value heads of 128,
     # packed projection [qkv | z | a | b] in bf16 (z is not read), fp32 outputs.
@@ -177,7 +191,27 @@ def build_kernels(dev):
                    torch.empty((Tp, hp), dtype=f32, device=dev),
                    torch.empty((Tp, hp), dtype=f32, device=dev)),
         lambda s: ops.delta_prologue(s[0], convp, a_dec, dtb, 2048, hp, dp, hp, dp, out=s[1:]),
-        [Tp, hp, dp], "bfloat16->float32"))
+        [Tp, hp, dp], "bfloat16->float32", group="next"))
+
+    # DeltaNet recurrence of one layer (not a row kernel: bound by the sequential
+    # per-token state update, reported with its bytes for reference)
+    Bs, Ss = 8, 2048
+
+    def scan_set(i):
+        qs = torch.nn.functional.normalize(randn((Bs, Ss, hp, dp), f32), dim=-1) / math.sqrt(dp)
+        ks = torch.nn.functional.normalize(randn((Bs, Ss, hp, dp), f32), dim=-1)
+        return (qs, ks, randn((Bs, Ss, hp, dp), f32),
+                torch.sigmoid(randn((Bs, Ss, hp), f32)), -torch.rand((Bs, Ss, hp), generator=g,
+                                                                        device=dev),
+                torch.empty((Bs, Ss, hp, dp), dtype=bf, device=dev))
+    kernels.append(Kernel(
+        "delta_scan_bf16", "delta_scan",
+        Bs * Ss * hp * dp * 4 * 3 + Bs * Ss * hp * 4 * 2 + Bs * Ss * hp * dp * 2,
+        scan_set,
+        lambda s: ops.delta_scan(s[0], s[1], s[2], s[3], s[4], bf, out=s[5]),
+        [Bs, Ss, hp, dp], "float32->bfloat16", group="next",
+        # per (token, head, value row, key): 2 (S k) + 3 (f S + u k) + 2 (S q)
+        flops=7 * Bs * Ss * hp * dp * dp))
     return kernels
 
 
@@ -302,6 +336,66 @@ def fused_sequence(cfg, dev, tokens):
     return run
 
 
+def widened_sequence(cfg, dev, batch, seq):
+    """The widened kernels of one bf16 forward: per full-attention layer the
+    masked softmax and the gate merge, per DeltaNet layer the prologue and the
+    recurrence, on buffers of the forward's shapes."""
+    import torch
+    from qdc_amd import ops
+    bf, f32 = torch.bfloat16, torch.float32
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    rn = lambda shape, dt: torch.randn(shape, generator=g, device=dev).to(dt)  # noqa: E731
+    T = batch * seq
+    H, hd = cfg.heads, cfg.head_dim
+    scores = rn((batch, H, seq, seq), f32)
+    probs = torch.empty(scores.shape, dtype=bf, device=dev)
+    mask = torch.ones((batch, seq), dtype=torch.int32, device=dev)
+    values = rn((batch, H, seq, hd), f32)
+    qgate = rn((T, H, 2 * hd), bf)
+    merged = torch.empty((T, H * hd), dtype=bf, device=dev)
+    kh, kd, vh, vd = cfg.key_heads, cfg.key_dim, cfg.value_heads, cfg.value_dim
+    cq = 2 * kh * kd + vh * vd
+    proj = rn((T, cq + vh * vd + 2 * vh), bf)
+    conv = rn((cq, cfg.conv_kernel), f32)
+    a_dec, dtb = -torch.exp(rn((vh,), f32)), rn((vh,), f32)
+    outs = [torch.empty(sh, dtype=f32, device=dev)
+            for sh in ((T, kh, kd), (T, kh, kd), (T, vh, vd), (T, vh), (T, vh))]
+    scanned = torch.empty((batch, seq, vh, vd), dtype=bf, device=dev)
+    scale = 1.0 / math.sqrt(hd)
+
+    def run():
+        for kind in cfg.layer_types:
+            if kind == "full_attention":
+                ops.attention_softmax(scores, mask, scale, out=probs)
+                ops.attention_gate(values, qgate[:, :, hd:], out=merged)
+            else:
+                q, k, v, beta, decay = ops.delta_prologue(proj, conv, a_dec, dtb, seq, kh, kd,
+                                                          vh, vd, out=outs)
+                ops.delta_scan(q.view(batch, seq, kh, kd), k.view(batch, seq, kh, kd),
+                               v.view(batch, seq, vh, vd), beta.view(batch, seq, vh),
+                               decay.view(batch, seq, vh), out=scanned)
+    return run
+
+
+def _graph_ms(run):
+    """Time one replay of `run` captured in a HIP graph (after one eager call)."""
+    import torch
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
+        run()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b)
+
+
 def e2e_benchmark(dev, steps=3, warmup=1):
     """backbone_hidden of the random-init Qwen3.5-0.8B-like backbone (24 layers,
     bf16 weights/activations, fp32 residual stream) on 8 sequences of 2048."""
@@ -333,27 +427,20 @@ def e2e_benchmark(dev, steps=3, warmup=1):
     ms = start.elapsed_time(end) / steps
     del model
     torch.cuda.empty_cache()
-    # fused kernels of one forward, replayed from a graph on buffers of the same shapes
-    run = fused_sequence(cfg, dev, E2E_BATCH * E2E_SEQ)
-    run()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
-        run()
-    graph.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    fused_ms = a.elapsed_time(b)
+    # this library's kernels of one forward, replayed from graphs on buffers of
+    # the forward's shapes: the fused row kernels, then the widened kernels
+    fused_ms = _graph_ms(fused_sequence(cfg, dev, E2E_BATCH * E2E_SEQ))
+    torch.cuda.empty_cache()
+    widened_ms = _graph_ms(widened_sequence(cfg, dev, E2E_BATCH, E2E_SEQ))
+    torch.cuda.empty_cache()
     return {"workload": "random-init Qwen3.5-0.8B-like backbone, 24 layers (18 DeltaNet + 6 full), "
                         "hidden 1024, vocab 248320, bf16 weights and activations, fp32 residual",
             "batch": E2E_BATCH, "seq_len": E2E_SEQ, "ms_per_forward": round(ms, 3),
             "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (ms / 1e3), 1),
             "fused_kernels_ms": round(fused_ms, 3),
             "fused_kernel_time_share": round(fused_ms / ms, 4),
+            "widened_kernels_ms": round(widened_ms, 3),
+            "widened_kernel_time_share": round(widened_ms / ms, 4),
             "steps": steps, "warmup": warmup}
 
 
@@ -465,30 +552,43 @@ def main():
     check_replay(kernels, args.steps)
     for k in kernels:  # one untimed replay
         k.graph.replay()
-    total_ms = time_gpu(kernels, args.steps)
-    step_bytes = sum(k.algo_bytes for k in kernels)
-    value = step_bytes * args.steps / (total_ms / 1e3) / 1e9
-    per = {k.name: {"shape": k.shape, "dtype": k.dtype, "bytes": k.algo_bytes,
-                    "us": round(k.avg_ms * 1e3, 3),
-                    "gbs": round(k.algo_bytes / (k.avg_ms / 1e3) / 1e9, 1),
-                    "pct_peak": round(100 * k.algo_bytes / (k.avg_ms / 1e3) / 1e9 / PEAK_GBS, 1)}
-           for k in kernels}
-    dom = max(kernels, key=lambda k: k.avg_ms)
+    time_gpu(kernels, args.steps)
+    hot = [k for k in kernels if k.group == "hot"] or kernels
+    hot_ms = sum(k.avg_ms for k in hot) * args.steps
+    step_bytes = sum(k.algo_bytes for k in hot)
+    value = step_bytes * args.steps / (hot_ms / 1e3) / 1e9
+
+    def entry(k):
+        e = {"shape": k.shape, "dtype": k.dtype, "bytes": k.algo_bytes,
+             "us": round(k.avg_ms * 1e3, 3),
+             "gbs": round(k.algo_bytes / (k.avg_ms / 1e3) / 1e9, 1),
+             "pct_peak": round(100 * k.algo_bytes / (k.avg_ms / 1e3) / 1e9 / PEAK_GBS, 1)}
+        if k.flops:
+            tf = k.flops / (k.avg_ms / 1e3) / 1e12
+            e.update(bound="valu", tflops=round(tf, 2), valu_peak_tflops=VALU_PEAK_TF,
+                     pct_valu_peak=round(100 * tf / VALU_PEAK_TF, 1))
+        return e
+
+    per = {k.name: entry(k) for k in hot}
+    widened = {k.name: entry(k) for k in kernels if k.group != "hot"}
+    dom = max(hot, key=lambda k: k.avg_ms)
     achieved = dom.algo_bytes / (dom.avg_ms / 1e3) / 1e9
     traffic = load_traffic(dom.name)
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 4),
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(hot_ms / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "fused row kernels of one Qwen3.5-0.8B-like layer set: "
-                               + ", ".join(k.name for k in kernels),
+                               + ", ".join(k.name for k in hot),
                    "storage": "bf16 and fp32 as named per kernel", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": dom.name, "achieved": round(achieved, 1),
                      "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes": dom.algo_bytes},
         "kernels": per,
     }
+    if widened:
+        line["widened"] = widened
     if not args.no_e2e:
         for k in kernels:  # release the kernel benchmark's buffers first
             k.sets, k.graph = None, None

@@ -28,6 +28,7 @@ namespace qdc {
 namespace {
 
 constexpr int kTaps = 4;    // fast-path convolution width (the Qwen3.5 default)
+constexpr uint32_t kXcds = 8;  // accelerator complex dies of an MI355X
 
 struct Prologue {
     const void *proj;
@@ -60,7 +61,12 @@ template <typename T, int LPH>
 __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     constexpr int kTileT = tile_for<T>();
     constexpr int kRows = kTileT + kTaps - 1;  // rows t0-3 .. t0+tile-1
-    const int64_t t0 = (int64_t)blockIdx.x * kTileT;
+    // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2); give
+    // each XCD a contiguous run of tiles so a tile's halo rows were just read by
+    // the previous tile on the same XCD and come from its L2.
+    uint32_t tile = blockIdx.x;
+    if (gridDim.x % kXcds == 0) tile = (tile % kXcds) * (gridDim.x / kXcds) + tile / kXcds;
+    const int64_t t0 = (int64_t)tile * kTileT;
     if (blockIdx.y == gridDim.y - 1) {  // gates row of the grid
         for (int i = threadIdx.x; i < kTileT * a.vh; i += kBlock) {
             const int64_t t = t0 + i / a.vh;

@@ -278,10 +278,11 @@ def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
 
 
 def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
-               decay: torch.Tensor, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+               decay: torch.Tensor, out_dtype: torch.dtype = torch.float32,
+               out: torch.Tensor | None = None) -> torch.Tensor:
     """Gated delta rule recurrence (the DeltaNet "existing path", not a fused
     row op): contiguous fp32 q, k ``[B, S, KH, kd]``, v ``[B, S, H, vd]``, beta and
-    decay ``[B, S, H]`` -> ``[B, S, H, vd]`` in ``out_dtype``."""
+    decay ``[B, S, H]`` -> ``[B, S, H, vd]`` in ``out_dtype`` (or into ``out``)."""
     _device(q, k, v, beta, decay)
     for t in (q, k, v, beta, decay):
         if t.dtype != torch.float32 or not t.is_contiguous():
@@ -291,7 +292,11 @@ def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Te
     if q.shape != k.shape or v.shape[:2] != (B, S) or beta.shape != (B, S, H) or \
             decay.shape != (B, S, H):
         raise ValueError("inconsistent delta_scan shapes")
-    out = torch.empty((B, S, H, vd), dtype=out_dtype, device=q.device)
+    if out is None:
+        out = torch.empty((B, S, H, vd), dtype=out_dtype, device=q.device)
+    if out.shape != (B, S, H, vd) or out.dtype not in _DTYPES or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [B, S, H, vd] float32/bfloat16 tensor")
+    out_dtype = out.dtype
     check(lib().qdc_delta_scan(out.data_ptr(), _DTYPES[out_dtype], q.data_ptr(), k.data_ptr(),
                                v.data_ptr(), beta.data_ptr(), decay.data_ptr(), B, S, H, KH, kd,
                                vd, _stream(q)), "delta_scan")
