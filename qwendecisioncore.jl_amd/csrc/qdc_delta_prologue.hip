@@ -12,12 +12,12 @@
 // gates src/backbone.jl:293-296; AMDGPU causal_depthwise_kernel! /
 // qk_normalize_kernel! and the beta/decay broadcasts, ext/amdgpu_delta.jl:1-33, 83-113, 154-159.
 //
-// Fast path: a thread owns 8 consecutive channels (one 16-byte bf16 chunk of the
-// projection row) for a tile of 16 (bf16) or 8 (fp32) consecutive tokens,
-// loads the tile's rows and the K-1 halo rows before it in one go, then slides
-// a K-tap window down the tile, so each projection row is read once from HBM
-// (the halo comes from L2).  The kd/8 lanes of a key head are an aligned
-// lane group, so the L2 norm reduces inside the group (DPP).  Outputs are fp32
+// Fast path: a thread owns 4 consecutive channels for a tile of 32 (bf16) or 16
+// (fp32) consecutive tokens, loads the tile's rows and the K-1 halo rows before
+// it in one go, then slides a K-tap window down the tile, so each projection row
+// is read once from HBM (the halo comes from L2) and each output chunk is one
+// whole 16-byte store.  The kd/4 lanes of a key head are an aligned lane group,
+// so the L2 norm reduces inside the group.  Outputs are fp32
 // (the recurrence reads fp32).  One extra row of blocks computes the gates.
 #include <cmath>
 #include <type_traits>
@@ -40,8 +40,9 @@ struct Prologue {
     int64_t tokens;
     FastDiv seq;            // sequence length (positions reset per sequence)
     int kh, kd, vh, vd, taps;
-    int chunks;             // qkv channels / 8
-    int qk_chunks;          // 2*kh*kd / 8
+    int chunks;             // qkv channels / 4
+    int qk_chunks;          // 2*kh*kd / 4
+    uint32_t blocks_per_tile;  // fast path: channel blocks + 1 gates block
     float sqrt_kd;
 };
 
@@ -52,22 +53,50 @@ __device__ __forceinline__ float softplus_f(float x) {
     return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
 }
 
-// Tokens per thread: the tile's rows plus the kTaps-1 halo rows are all loaded
-// before the first is used, so a thread keeps (tile + 3) 16-byte-per-8-channel
-// rows in flight.
-template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 16 : 8; }
+// A thread owns 4 channels: 8 bytes of a bf16 (16 of an fp32) projection row
+// and exactly one 16-byte fp32 output chunk, so every load and store
+// instruction of a wavefront covers whole cache lines.  Tokens per thread: the
+// tile's rows plus the kTaps-1 halo rows are all loaded before the first is used.
+template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 32 : 16; }
+
+template <typename T> struct Raw4;  // 4 channels of one projection row
+template <> struct Raw4<bf16_t> {
+    typedef uint32_t type __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ void unpack(type r, float (&v)[4]) {
+        v[0] = __uint_as_float(r[0] << 16); v[1] = __uint_as_float(r[0] & 0xffff0000u);
+        v[2] = __uint_as_float(r[1] << 16); v[3] = __uint_as_float(r[1] & 0xffff0000u);
+    }
+};
+template <> struct Raw4<float> {
+    typedef u32x4 type;
+    static __device__ __forceinline__ void unpack(type r, float (&v)[4]) {
+        v[0] = __uint_as_float(r[0]); v[1] = __uint_as_float(r[1]);
+        v[2] = __uint_as_float(r[2]); v[3] = __uint_as_float(r[3]);
+    }
+};
 
 template <typename T, int LPH>
 __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
+    using Raw = typename Raw4<T>::type;
     constexpr int kTileT = tile_for<T>();
     constexpr int kRows = kTileT + kTaps - 1;  // rows t0-3 .. t0+tile-1
-    // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2); give
-    // each XCD a contiguous run of tiles so a tile's halo rows were just read by
-    // the previous tile on the same XCD and come from its L2.
-    uint32_t tile = blockIdx.x;
-    if (gridDim.x % kXcds == 0) tile = (tile % kXcds) * (gridDim.x / kXcds) + tile / kXcds;
+    // One-dimensional grid of tiles x channel blocks (the last block of a tile
+    // computes the gates).  Workgroups are dealt round-robin to the 8 XCDs (each
+    // with its own L2): XCD z gets a contiguous run of tiles and, for each tile,
+    // all its channel blocks in a row, so whole projection rows are read together
+    // and a tile's halo rows were just read by the previous tile on the same XCD.
+    const uint32_t nblk = a.blocks_per_tile, tiles = gridDim.x / nblk;
+    uint32_t tile, cblk;
+    if (tiles % kXcds == 0) {
+        const uint32_t z = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
+        tile = z * (tiles / kXcds) + k / nblk;
+        cblk = k % nblk;
+    } else {
+        tile = blockIdx.x / nblk;
+        cblk = blockIdx.x % nblk;
+    }
     const int64_t t0 = (int64_t)tile * kTileT;
-    if (blockIdx.y == gridDim.y - 1) {  // gates row of the grid
+    if (cblk == nblk - 1) {  // the gates block of this tile
         for (int i = threadIdx.x; i < kTileT * a.vh; i += kBlock) {
             const int64_t t = t0 + i / a.vh;
             const int h = i % a.vh;
@@ -80,9 +109,9 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
         }
         return;
     }
-    const int ci = blockIdx.y * kBlock + threadIdx.x;  // chunk of 8 channels
+    const int ci = cblk * kBlock + threadIdx.x;  // quad of 4 channels
     const bool live = ci < a.chunks;
-    const int c0 = (live ? ci : 0) * 8;
+    const int c0 = (live ? ci : 0) * 4;
     const bool is_q = ci < a.qk_chunks / 2, is_k = !is_q && ci < a.qk_chunks;
     const T *base = reinterpret_cast<const T *>(a.proj) + c0;
 
@@ -90,20 +119,16 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     // for every token of the tile
     const uint32_t s0 = (uint32_t)t0 - fastdiv((uint32_t)t0, a.seq) * a.seq.d;
     const int64_t seq_start = t0 - s0;
-    Frag<T, 8> rows[kRows];
+    Raw rows[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         const int64_t t = t0 - (kTaps - 1) + r;
-        if (live && t >= seq_start && t < a.tokens) {
-            rows[r] = load_frag<T, 8>(base + t * a.ld);
-        } else {
-#pragma unroll
-            for (int i = 0; i < Frag<T, 8>::kN; ++i) rows[r].r[i] = u32x4{0u, 0u, 0u, 0u};
-        }
+        rows[r] = Raw{};
+        if (live && t >= seq_start && t < a.tokens) rows[r] = *reinterpret_cast<const Raw *>(base + t * a.ld);
     }
-    float w[8][kTaps];
+    float w[4][kTaps];
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int j = 0; j < kTaps; ++j) w[c][j] = live ? a.conv[(c0 + c) * kTaps + j] : 0.0f;
 
@@ -117,12 +142,12 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
         uint32_t s = 0;  // position of t in its sequence (masked tiles only)
         if constexpr (decltype(masked)::value)
             s = tok ? (uint32_t)t - fastdiv((uint32_t)t, a.seq) * a.seq.d : 0u;
-        float x[kTaps][8];
+        float x[kTaps][4];
 #pragma unroll
-        for (int j = 0; j < kTaps; ++j) unpack(rows[tt + j], x[j]);  // row t - (kTaps-1) + j
-        float m[8];
+        for (int j = 0; j < kTaps; ++j) Raw4<T>::unpack(rows[tt + j], x[j]);  // row t - (kTaps-1) + j
+        float m[4];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < 4; ++c) {
             // tap j multiplies row t - (kTaps-1) + j; fused multiply-add per tap
             float acc = 0.0f;
 #pragma unroll
@@ -137,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
         }
         float ss = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) ss = __builtin_fmaf(m[c], m[c], ss);
+        for (int c = 0; c < 4; ++c) ss = __builtin_fmaf(m[c], m[c], ss);
         ss = group_sum<LPH>(ss);  // whole aligned head groups: q/k rows only use it
         if (live && tok) {
             float *dst;
@@ -145,12 +170,12 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
                 const float scale = is_q ? 1.0f / (__builtin_sqrtf(ss + 1e-6f) * a.sqrt_kd)
                                          : 1.0f / __builtin_sqrtf(ss + 1e-6f);
 #pragma unroll
-                for (int c = 0; c < 8; ++c) m[c] = m[c] * scale;
+                for (int c = 0; c < 4; ++c) m[c] = m[c] * scale;
                 dst = is_q ? a.q + t * kw + c0 : a.k + t * kw + (c0 - kw);
             } else {
                 dst = a.v + t * vw + (c0 - 2 * kw);
             }
-            store_frag<8>(dst, m);
+            store_chunk(dst, m);
         }
     };
     if (!inner_start) {
@@ -207,15 +232,15 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_general(Prologue a) {
 
 template <typename T>
 int32_t launch(const Prologue &p, bool fast, hipStream_t stream) {
-    const int lph = p.kd / 8;
-    if (fast && p.kd % 8 == 0 && p.vd % 8 == 0 && p.taps == kTaps && lph <= kWave &&
+    const int lph = p.kd / 4;
+    if (fast && p.kd % 4 == 0 && p.vd % 4 == 0 && p.taps == kTaps && lph <= kWave &&
         (lph & (lph - 1)) == 0) {
-        // x: token tiles; y: channel blocks plus one for the gates
-        const dim3 grid((uint32_t)ceil_div(p.tokens, tile_for<T>()),
-                        (uint32_t)ceil_div(p.chunks, kBlock) + 1);
+        Prologue q = p;
+        q.blocks_per_tile = (uint32_t)ceil_div(p.chunks, kBlock) + 1;
+        const dim3 grid((uint32_t)(ceil_div(p.tokens, tile_for<T>()) * q.blocks_per_tile));
 #define QDC_PRO(L)                                                                               \
     case L:                                                                                      \
-        hipLaunchKernelGGL((delta_prologue_fast<T, L>), grid, dim3(kBlock), 0, stream, p);     \
+        hipLaunchKernelGGL((delta_prologue_fast<T, L>), grid, dim3(kBlock), 0, stream, q);     \
         return launch_status();
         switch (lph) {
             QDC_PRO(1)
@@ -284,12 +309,13 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
     p.vh = (int)value_heads;
     p.vd = (int)value_dim;
     p.taps = (int)taps;
-    p.chunks = (int)(cq / 8);
-    p.qk_chunks = (int)(2 * kw / 8);
+    p.chunks = (int)(cq / 4);
+    p.qk_chunks = (int)(2 * kw / 4);
     // sqrt(Float32(key_dim)) of src/backbone.jl:313 / src/backbone_cpu.jl:516
     p.sqrt_kd = std::sqrt((float)key_dim);
-    const bool fast = aligned16(proj) && (ld * es) % 16 == 0 && aligned16(q) && aligned16(k) &&
-                      aligned16(v) && cq % 8 == 0;
+    // 4-channel pieces: 8-byte (bf16) or 16-byte (fp32) aligned projection rows
+    const bool fast = ((uintptr_t)proj % (4 * es)) == 0 && (ld * es) % (4 * es) == 0 &&
+                      aligned16(q) && aligned16(k) && aligned16(v) && cq % 4 == 0;
     if (proj_dtype == QDC_BF16) return launch<bf16_t>(p, fast, stream);
     return launch<float>(p, fast, stream);
 }

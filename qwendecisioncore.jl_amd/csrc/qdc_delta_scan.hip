@@ -222,6 +222,249 @@ __global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked form on the matrix cores (fp32 MFMA 16x16x4).  For a chunk of kC = 16
+// tokens with state S0 (kept transposed, S^T [kd, vd]), log-decays d and their
+// running sums g (g_i = d_0 + ... + d_i), the recurrence above is exactly
+//     A[i][p] = beta_i exp(g_i - g_p) (k_i . k_p)   (p < i),  T = (I + A)^-1
+//     U = T diag(beta) (V - diag(e^g) Z),   Z = K S0^T        (the deltas u_i)
+//     O = diag(e^g) Q S0^T + P U,   P[i][p] = exp(g_i - g_p) (q_i . k_p)  (p <= i)
+//     S^T <- e^(g_15) S^T + (diag(e^(g_15 - g)) K)^T U
+// (a partial last chunk is padded with k = q = v = 0, beta = 0, d = 0).  A
+// workgroup owns 64 value rows of one (sequence, head), 16 per wavefront; the
+// state tile of a wavefront lives in MFMA accumulator layout (lane l, register j:
+// S^T[16a + 4(l/16) + j][16w + l%16]), which is also the B-operand layout the
+// next chunk's S^T products read, so the state never leaves registers.  Per chunk:
+// wavefronts 1 and 2 form K K^T and Q K^T on the matrix cores and turn them into
+// A and P; wavefront 0 inverts I + A by forward substitution (one lane per column)
+// while the others already run Z and Q S0^T; then every wavefront finishes U, O
+// and its state update (104 MFMAs per wavefront and chunk).  k, q, v, beta and d
+// of the next chunk are in flight from HBM the whole time.
+constexpr int kC = 16;        // tokens per chunk: one MFMA tile edge
+constexpr int kRowsWG = 64;   // value rows per workgroup, 16 per wavefront
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Inclusive prefix sum over each 16-lane row of a wavefront (DPP row shifts;
+// lanes shifted in from outside the row contribute 0).
+__device__ __forceinline__ float row_prefix_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, true));
+    return v;
+}
+
+template <int KB, typename TO>
+__global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
+    constexpr int KD = 16 * KB;             // key dimension
+    constexpr int KS = KD + 4;              // LDS row stride of k/q rows (bank spread)
+    constexpr int MS = kC + 1;              // row stride of the small matrices read by column
+    constexpr int KQ_ITEMS = (kC * KD / 4 + kBlock - 1) / kBlock;  // 16-byte loads per thread
+    __shared__ __align__(16) float sK[2][kC][KS];
+    __shared__ __align__(16) float sQ[2][kC][KS];
+    __shared__ __align__(16) float sV[2][kC][kRowsWG];
+    __shared__ float sBeta[2][kC], sG[2][kC];  // beta and the running log-decay sums g
+    __shared__ __align__(16) float sA[kC][kC];  // read as whole rows by the inverse
+    __shared__ float sP[kC][MS], sTb[kC][MS];
+    __shared__ float sO[kC][kRowsWG + 1];
+
+    const int tid = threadIdx.x;
+    const int w = tid / kWave, l = tid % kWave, lr = l % 16, lg = l / 16;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int g = h / a.groups;
+    const int row0 = blockIdx.x * kRowsWG;
+    const int wrow = 16 * w;                      // this wavefront's rows within the workgroup
+    const bool live = row0 + wrow < a.vd;         // value_dim % 16 == 0: whole tile or none
+    const int S = a.S;
+    const int64_t k_tok = (int64_t)a.KH * KD, v_tok = (int64_t)a.H * a.vd;
+    const float *kb = a.k + (int64_t)b * S * k_tok + (int64_t)g * KD;
+    const float *qb = a.q + (int64_t)b * S * k_tok + (int64_t)g * KD;
+    const float *vb = a.v + (int64_t)b * S * v_tok + (int64_t)h * a.vd + row0;
+    const float *bb = a.beta + (int64_t)b * S * a.H + h;
+    const float *db = a.decay + (int64_t)b * S * a.H + h;
+    TO *ob = reinterpret_cast<TO *>(a.out) + (int64_t)b * S * v_tok + (int64_t)h * a.vd + row0;
+
+    f32x4 rk[KQ_ITEMS], rq[KQ_ITEMS], rv;
+    float rs = 0.0f;  // beta (threads 0..15) or decay (threads 16..31) of one token
+    constexpr int kd4 = KD / 4;
+    auto fetch = [&](int c) {
+        const int t0 = c * kC, n = min(kC, S - t0);
+#pragma unroll
+        for (int p = 0; p < KQ_ITEMS; ++p) {
+            const int idx = tid + p * kBlock;
+            const int tt = idx / kd4, j4 = idx - tt * kd4;
+            rk[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+            rq[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (tt < n) {
+                const int64_t off = (int64_t)(t0 + tt) * k_tok + j4 * 4;
+                rk[p] = *reinterpret_cast<const f32x4 *>(kb + off);
+                rq[p] = *reinterpret_cast<const f32x4 *>(qb + off);
+            }
+        }
+        {   // v: 16 tokens x 64 rows, one 16-byte piece per thread
+            const int tt = tid / 16, r4 = (tid % 16) * 4;
+            rv = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (tt < n && row0 + r4 < a.vd)
+                rv = *reinterpret_cast<const f32x4 *>(vb + (int64_t)(t0 + tt) * v_tok + r4);
+        }
+        rs = 0.0f;
+        if (tid < kC && tid < n) rs = bb[(int64_t)(t0 + tid) * a.H];
+        else if (tid >= kC && tid < 2 * kC && tid - kC < n) rs = db[(int64_t)(t0 + tid - kC) * a.H];
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < KQ_ITEMS; ++p) {
+            const int idx = tid + p * kBlock;
+            const int tt = idx / kd4, j4 = idx - tt * kd4;
+            if (tt < kC) {
+                *reinterpret_cast<f32x4 *>(&sK[buf][tt][j4 * 4]) = rk[p];
+                *reinterpret_cast<f32x4 *>(&sQ[buf][tt][j4 * 4]) = rq[p];
+            }
+        }
+        *reinterpret_cast<f32x4 *>(&sV[buf][tid / 16][(tid % 16) * 4]) = rv;
+        // lanes 16..31 hold the 16 decays: one row of the wavefront
+        const float g_run = row_prefix_sum(rs);
+        if (tid < kC) sBeta[buf][tid] = rs;
+        else if (tid < 2 * kC) sG[buf][tid - kC] = g_run;
+    };
+
+    f32x4 st[KB];
+#pragma unroll
+    for (int i = 0; i < KB; ++i) st[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int chunks = (S + kC - 1) / kC;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < chunks) fetch(c + 1);  // in flight while this chunk is computed
+        const int n = min(kC, S - c * kC);
+        const float *gs = sG[buf];
+
+        // K K^T -> A (wavefront 1), Q K^T -> P (wavefront 2); lane l, register j
+        // holds entry [4(l/16) + j][l%16] of the 16x16 product
+        if (w == 1 || w == 2) {
+            const float(*x)[KS] = w == 1 ? sK[buf] : sQ[buf];
+            // four independent accumulation chains (keys 4(l/16) + j of every
+            // 16-key block), summed at the end
+            f32x4 part[4] = {};
+#pragma unroll
+            for (int i = 0; i < KB; ++i) {
+                const f32x4 xa = *reinterpret_cast<const f32x4 *>(&x[lr][16 * i + 4 * lg]);
+                const f32x4 ka = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][16 * i + 4 * lg]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) part[j] = mfma4(xa[j], ka[j], part[j]);
+            }
+            const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 4 * lg + j, p = lr;
+                const float e = p <= i ? expf(gs[i] - gs[p]) : 0.0f;
+                if (w == 1) sA[i][p] = p < i ? sBeta[buf][i] * e * acc[j] : 0.0f;
+                else sP[i][p] = e * acc[j];
+            }
+        }
+        __syncthreads();
+
+        // wavefront 0: T = (I + A)^-1 by forward substitution, column m per lane,
+        // stored as Tb = T diag(beta)
+        if (w == 0 && l < kC) {
+            const int m = l;
+            float col[kC];
+#pragma unroll
+            for (int i = 0; i < kC; ++i) col[i] = i == m ? 1.0f : 0.0f;
+#pragma unroll
+            for (int i = 1; i < kC; ++i) {
+                float row[kC];
+#pragma unroll
+                for (int p4 = 0; p4 < (i + 3) / 4; ++p4) {
+                    const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sA[i][4 * p4]);
+                    row[4 * p4] = v4.x; row[4 * p4 + 1] = v4.y;
+                    row[4 * p4 + 2] = v4.z; row[4 * p4 + 3] = v4.w;
+                }
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int p = 0; p < i; p += 2) {
+                    s0 = __builtin_fmaf(row[p], col[p], s0);
+                    if (p + 1 < i) s1 = __builtin_fmaf(row[p + 1], col[p + 1], s1);
+                }
+                if (i > m) col[i] = -(s0 + s1);
+            }
+            const float bm = sBeta[buf][m];
+#pragma unroll
+            for (int i = 0; i < kC; ++i) sTb[i][m] = col[i] * bm;
+        }
+
+        // Z = K S0^T and Y = diag(e^g) Q S0^T (independent of T)
+        f32x4 Z = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            // two chains each for Z and Q S0^T; Y = diag(e^g) Q S0^T scales the
+            // 4 result rows afterwards
+            f32x4 z0 = {}, z1 = {}, y0 = {}, y1 = {};
+#pragma unroll
+            for (int i = 0; i < KB; ++i) {
+                const f32x4 kv = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][16 * i + 4 * lg]);
+                const f32x4 qv = *reinterpret_cast<const f32x4 *>(&sQ[buf][lr][16 * i + 4 * lg]);
+                z0 = mfma4(kv[0], st[i][0], z0);
+                y0 = mfma4(qv[0], st[i][0], y0);
+                z1 = mfma4(kv[1], st[i][1], z1);
+                y1 = mfma4(qv[1], st[i][1], y1);
+                z0 = mfma4(kv[2], st[i][2], z0);
+                y0 = mfma4(qv[2], st[i][2], y0);
+                z1 = mfma4(kv[3], st[i][3], z1);
+                y1 = mfma4(qv[3], st[i][3], y1);
+            }
+            Z = z0 + z1;
+            Y = y0 + y1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Y[j] *= expf(gs[4 * lg + j]);
+        }
+        __syncthreads();  // Tb ready
+
+        if (live) {
+            const float gl = gs[kC - 1];
+            // R = V - diag(e^g) Z in accumulator layout = the B operand of U = Tb R
+            f32x4 R;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                R[j] = sV[buf][4 * lg + j][wrow + lr] - expf(gs[4 * lg + j]) * Z[j];
+            f32x4 U = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) U = mfma4(sTb[lr][4 * lg + i], R[i], U);
+            f32x4 O = Y;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O = mfma4(sP[lr][4 * lg + i], U[i], O);
+            // S^T update; the decay weights e^(g_15 - g_tau) scale U's rows (the
+            // lane's register i is token 4(l/16) + i)
+            f32x4 Ue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Ue[i] = U[i] * expf(gl - gs[4 * lg + i]);
+            const float gll = expf(gl);
+#pragma unroll
+            for (int t = 0; t < KB; ++t) {
+                f32x4 acc = st[t] * gll;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc = mfma4(sK[buf][4 * lg + i][16 * t + lr], Ue[i], acc);
+                st[t] = acc;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sO[4 * lg + j][wrow + lr] = O[j];
+        }
+        __syncthreads();
+        if (c + 1 < chunks) stage(buf ^ 1);
+        for (int e = tid; e < kC * kRowsWG; e += kBlock) {
+            const int tt = e / kRowsWG, r = e - tt * kRowsWG;
+            if (tt < n && row0 + r < a.vd)
+                ob[(int64_t)(c * kC + tt) * v_tok + r] = from_f32<TO>(sO[tt][r]);
+        }
+        __syncthreads();
+    }
+}
+
 }  // namespace
 }  // namespace qdc
 
@@ -260,6 +503,28 @@ extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, 
     const bool two = blocks2 >= 512;
     const int64_t rb = (two ? 2 : 1) * kGroupsPerBlock;
     const dim3 grid((uint32_t)ceil_div(value_dim, rb), (uint32_t)heads, (uint32_t)batch);
+    // matrix-core chunked form: key_dim a multiple of 16 (<= 256), value_dim of 16
+    if (key_dim % 16 == 0 && value_dim % 16 == 0 && aligned16(q) && aligned16(k) &&
+        aligned16(v)) {
+        const dim3 cgrid((uint32_t)ceil_div(value_dim, kRowsWG), (uint32_t)heads,
+                         (uint32_t)batch);
+#define QDC_CHUNKED(KB)                                                                        \
+    if (key_dim == 16 * KB) {                                                                  \
+        if (out_dtype == QDC_BF16)                                                             \
+            hipLaunchKernelGGL((delta_scan_chunked<KB, bf16_t>), cgrid, dim3(kBlock), 0,       \
+                               stream, a);                                                     \
+        else                                                                                   \
+            hipLaunchKernelGGL((delta_scan_chunked<KB, float>), cgrid, dim3(kBlock), 0,        \
+                               stream, a);                                                     \
+        return launch_status();                                                                \
+    }
+        QDC_CHUNKED(1)
+        QDC_CHUNKED(2)
+        QDC_CHUNKED(4)
+        QDC_CHUNKED(8)
+        QDC_CHUNKED(16)
+#undef QDC_CHUNKED
+    }
     const bool vec = aligned16(q) && aligned16(k) && key_dim % 4 == 0;
     const int64_t kpl = ceil_div(key_dim, kGroup);
 #define QDC_SCAN(KPL, R, VEC, TO)                                                              \

@@ -86,7 +86,9 @@ def test_from_directory_packs_bf16_without_widening(tmp_path):
             a = p + "linear_attn."
             packed = torch.cat([t(a + n) for n in ("in_proj_qkv.weight", "in_proj_z.weight",
                                                    "in_proj_a.weight", "in_proj_b.weight")]).t()
-            assert torch.equal(layer["proj"], packed)
+            width = packed.shape[1]
+            assert torch.equal(layer["proj"][:, :width], packed)
+            assert layer["proj"].shape[1] % 256 == 0 and not layer["proj"][:, width:].any()
             assert layer["conv"].dtype == torch.float32
         else:
             a = p + "self_attn."

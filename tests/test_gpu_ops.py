@@ -318,10 +318,13 @@ def test_residual_rmsnorm_fp32_stream(mixed_dtype, out_dtype, rows, width):
 
 # ------------------------------------------------ DeltaNet recurrence --------
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,S,KH,H,kd,vd", [(2, 37, 2, 4, 128, 128), (1, 5, 1, 2, 64, 20),
-                                            (3, 64, 16, 16, 128, 128), (1, 9, 1, 1, 256, 8),
-                                            (2, 65, 1, 2, 2, 2), (1, 17, 2, 6, 96, 33)])
-def test_delta_scan(out_dtype, B, S, KH, H, kd, vd):
+@pytest.mark.parametrize("B,S,KH,H,kd,vd,dscale", [
+    (2, 37, 2, 4, 128, 128, 2.0), (3, 64, 16, 16, 128, 128, 2.0),   # matrix-core chunked form
+    (1, 33, 1, 2, 64, 48, 2.0), (2, 16, 1, 1, 16, 16, 2.0), (1, 50, 2, 2, 32, 16, 2.0),
+    (1, 300, 1, 1, 256, 32, 2.0), (1, 40, 1, 2, 128, 128, 40.0),    # strong decay
+    (1, 5, 1, 2, 64, 20, 2.0), (1, 9, 1, 1, 256, 8, 2.0),           # recurrent kernel
+    (2, 65, 1, 2, 2, 2, 2.0), (1, 17, 2, 6, 96, 33, 2.0)])
+def test_delta_scan(out_dtype, B, S, KH, H, kd, vd, dscale):
     from oracle import forward
     from qdc_amd import ops
     rng = np.random.default_rng(32)
@@ -331,12 +334,12 @@ def test_delta_scan(out_dtype, B, S, KH, H, kd, vd):
     k /= np.linalg.norm(k, axis=-1, keepdims=True)
     v = rng.standard_normal((B, S, H, vd), dtype=np.float32)
     beta = rng.random((B, S, H), dtype=np.float32)
-    decay = -rng.random((B, S, H), dtype=np.float32) * np.float32(2)
+    decay = -rng.random((B, S, H), dtype=np.float32) * np.float32(dscale)
     got = back(ops.delta_scan(*(dev(a, torch.float32) for a in (q, k, v, beta, decay)),
                               out_dtype=out_dtype))
     exp = np.stack([forward.delta_recurrence(q[b], k[b], v[b], beta[b], decay[b])
                     for b in range(B)])
-    report(f"delta scan {B}x{S} kh{KH} h{H} kd{kd} vd{vd}", got, exp, out_dtype)
+    report(f"delta scan {B}x{S} kh{KH} h{H} kd{kd} vd{vd} decay*{dscale}", got, exp, out_dtype)
 
 
 # ------------------------------------------------ DeltaNet prologue ----------
