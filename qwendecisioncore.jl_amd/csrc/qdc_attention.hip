@@ -7,7 +7,9 @@
 // and key i, value = scores*scale when i <= j and mask[b, i] != 0, else
 // -floatmax(Float32); probs = exp(value - max) / sum(exp(value - max)).  A query
 // with no visible unmasked key therefore spreads 1/keys over every key, as the
-// reference does.
+// reference does.  exp runs on the hardware exp2 unit and the row sum is
+// inverted once (the accurate library exp and a division per element made the
+// kernel vector-ALU bound).
 //
 // Fast path: one wavefront per score row held in registers (keys <= 2048, 16-byte
 // chunks dealt round-robin over the 64 lanes so every load instruction covers a
@@ -40,6 +42,14 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __shfl_xor(v, 16, kWave));
     v = fmaxf(v, __shfl_xor(v, 32, kWave));
     return v;
+}
+
+// exp(v - peak) for v <= peak on the hardware exp2 unit: exp2((v - peak) log2 e).
+// The product's rounding perturbs the exponent by |v - peak| * 2^-24, i.e. a
+// relative error of ~6e-8 |v - peak| on a value exp(v - peak): below 1e-6 for
+// every term that is not already negligible next to the row maximum's 1.
+__device__ __forceinline__ float exp_shifted(float v, float peak) {
+    return __builtin_amdgcn_exp2f((v - peak) * 1.4426950408889634f);
 }
 
 struct Softmax {
@@ -105,13 +115,17 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_fast(Softmax a) {
     const bool none = peak == -FLT_MAX;  // no visible unmasked key: every key gets 1/keys
     float total = 0.0f;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c)
+    for (int c = 0; c < CPL; ++c) {
+        const int64_t k0 = ((int64_t)c * kWave + lane) * 4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            v[c][e] = expf(v[c][e] - peak);
+            // chunks past the query hold -floatmax only: exp is 0
+            v[c][e] = k0 < visible ? exp_shifted(v[c][e], peak) : 0.0f;
             total += v[c][e];
         }
+    }
     total = group_sum<kWave>(total);
+    const float inv_total = 1.0f / total;
     TO *dst = reinterpret_cast<TO *>(a.probs) + row * a.keys;
     const float uniform = 1.0f / (float)a.keys;
 #pragma unroll
@@ -121,7 +135,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_fast(Softmax a) {
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            o[e] = none ? uniform : (k0 + e < visible ? v[c][e] / total : 0.0f);
+            o[e] = none ? uniform : (k0 + e < visible ? v[c][e] * inv_total : 0.0f);
         store4<TO>(dst + k0, o);
     }
 }
@@ -144,12 +158,13 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_general(Softmax a) {
     peak = wave_max(peak);
     const bool none = peak == -FLT_MAX;
     float total = 0.0f;
-    for (int64_t k = lane; k < visible; k += kWave) total += expf(value(k) - peak);
+    for (int64_t k = lane; k < visible; k += kWave) total += exp_shifted(value(k), peak);
     total = group_sum<kWave>(total);
+    const float inv_total = 1.0f / total;
     TO *dst = reinterpret_cast<TO *>(a.probs) + row * a.keys;
     const float uniform = 1.0f / (float)a.keys;
     for (int64_t k = lane; k < a.keys; k += kWave) {
-        const float o = none ? uniform : (k < visible ? expf(value(k) - peak) / total : 0.0f);
+        const float o = none ? uniform : (k < visible ? exp_shifted(value(k), peak) * inv_total : 0.0f);
         dst[k] = from_f32<TO>(o);
     }
 }
