@@ -138,16 +138,17 @@ class QwenBackbone:
 
     # ------------------------------------------------------------ forward --
     @torch.no_grad()
-    def forward(self, ids: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    def forward(self, ids: torch.Tensor, mask: torch.Tensor | None) -> torch.Tensor:
         """Final-normalised hidden states ``[B*S, hidden]`` (device, fp32)
-        for device ids ``[B, S]`` (int32) and mask ``[B, S]`` (0/1)."""
+        for device ids ``[B, S]`` (int32) and mask ``[B, S]`` (0/1); ``mask=None``
+        means every token is kept (no masking work is done)."""
         B, S = ids.shape
         cfg = self.cfg
         # residual stream h in fp32 (a bf16 table widens exactly while gathered)
         h = ops.native_gather(self.embedding, ids.reshape(-1).contiguous(), out_dtype=torch.float32)
         normed = ops.native_rms(h, self.layers[0]["input_norm"], cfg.eps)
-        maskf = mask.to(torch.float32)
-        mask32 = mask.to(torch.int32).contiguous()
+        maskf = None if mask is None else mask.to(torch.float32)
+        mask32 = None if mask is None else mask.to(torch.int32).contiguous()
         for i, layer in enumerate(self.layers):
             if layer["kind"] == "full_attention":
                 mixed = self._full_attention(layer, normed, mask32, B, S)
@@ -211,7 +212,8 @@ class QwenBackbone:
         T = B * S
         kw, vw = kd * kh, vd * vh
         cq = 2 * kw + vw
-        masked = x * maskf.reshape(T, 1).to(x.dtype)
+        # masked tokens are zeroed before the projections (src/backbone.jl:286)
+        masked = x if maskf is None else x * maskf.reshape(T, 1).to(x.dtype)
         proj = masked @ layer["proj"]      # [T, cq + vw + 2*vh (+ zero padding)]
         # conv + SiLU, q/k L2 norm and the beta/decay gates in one pass
         q, k, v, beta, decay = ops.delta_prologue(proj, layer["conv"], layer["a_decay"],
@@ -248,6 +250,8 @@ def _device_inputs(model, ids, mask):
         ids, mask = ids[0], mask[0]
     check_sequence(model, ids, mask)
     d_ids = torch.from_numpy(ids.astype(np.int32)).to(model.device).view(1, -1)
+    if mask.all():  # nothing masked: the forward skips the masking work
+        return d_ids, None
     d_mask = torch.from_numpy(mask.astype(np.int32)).to(model.device).view(1, -1)
     return d_ids, d_mask
 
@@ -270,10 +274,12 @@ def backbone_last_hidden(model: QwenBackbone, ids, mask) -> np.ndarray:
     return backbone_hidden(model, ids, mask)[-1]
 
 
-def batch_backbone_hidden(model: QwenBackbone, ids: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+def batch_backbone_hidden(model: QwenBackbone, ids: torch.Tensor,
+                          mask: torch.Tensor | None) -> torch.Tensor:
     """Every position of ``B`` equal-length sequences at once: device int32 ids
-    ``[B, S]`` and 0/1 mask ``[B, S]`` -> ``[B, S, hidden]`` on the device.  RoPE
-    positions restart at 0 for every row.  Ids are not re-checked here: device
-    ids outside the vocabulary gather zero rows (see ``ops.native_gather``)."""
+    ``[B, S]`` and 0/1 mask ``[B, S]`` (None: nothing masked) -> ``[B, S, hidden]``
+    on the device.  RoPE positions restart at 0 for every row.  Ids are not
+    re-checked here: device ids outside the vocabulary gather zero rows (see
+    ``ops.native_gather``)."""
     B, S = ids.shape
     return model.forward(ids.to(torch.int32).contiguous(), mask).view(B, S, -1)
