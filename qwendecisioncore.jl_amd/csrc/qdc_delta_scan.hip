@@ -234,12 +234,18 @@ __global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
 // workgroup owns 64 value rows of one (sequence, head), 16 per wavefront; the
 // state tile of a wavefront lives in MFMA accumulator layout (lane l, register j:
 // S^T[16a + 4(l/16) + j][16w + l%16]), which is also the B-operand layout the
-// next chunk's S^T products read, so the state never leaves registers.  Per chunk:
-// wavefronts 1 and 2 form K K^T and Q K^T on the matrix cores and turn them into
-// A and P; wavefront 0 inverts I + A by forward substitution (one lane per column)
-// while the others already run Z and Q S0^T; then every wavefront finishes U, O
-// and its state update (104 MFMAs per wavefront and chunk).  k, q, v, beta and d
-// of the next chunk are in flight from HBM the whole time.
+// next chunk's S^T products read, so the state never leaves registers.
+//
+// Everything that does not involve the state (K K^T, Q K^T, A, P and the
+// triangular inverse) is prepared one chunk ahead, overlapped with the current
+// chunk's state products: per chunk c the workgroup runs
+//     phase 1: Z, Q S0^T of chunk c (all wavefronts) | K K^T -> A, Q K^T -> P of
+//              chunk c+1 (wavefronts 1, 2)
+//     phase 2: U, O, state update of chunk c (all) | (I + A)^-1 of chunk c+1 by
+//              forward substitution (wavefront 0, one lane per column)
+//     phase 3: stage chunk c+2 (its global loads were issued before phase 1) and
+//              write chunk c's outputs
+// with three barriers; k, q, v live in three LDS buffers, P and T diag(beta) in two.
 constexpr int kC = 16;        // tokens per chunk: one MFMA tile edge
 constexpr int kRowsWG = 64;   // value rows per workgroup, 16 per wavefront
 
@@ -262,13 +268,14 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
     constexpr int KD = 16 * KB;             // key dimension
     constexpr int KS = KD + 4;              // LDS row stride of k/q rows (bank spread)
     constexpr int MS = kC + 1;              // row stride of the small matrices read by column
+    constexpr int NB = 3;                   // k/q/v buffers: current, prepared, staging
     constexpr int KQ_ITEMS = (kC * KD / 4 + kBlock - 1) / kBlock;  // 16-byte loads per thread
-    __shared__ __align__(16) float sK[2][kC][KS];
-    __shared__ __align__(16) float sQ[2][kC][KS];
-    __shared__ __align__(16) float sV[2][kC][kRowsWG];
-    __shared__ float sBeta[2][kC], sG[2][kC];  // beta and the running log-decay sums g
-    __shared__ __align__(16) float sA[kC][kC];  // read as whole rows by the inverse
-    __shared__ float sP[kC][MS], sTb[kC][MS];
+    __shared__ __align__(16) float sK[NB][kC][KS];
+    __shared__ __align__(16) float sQ[NB][kC][KS];
+    __shared__ __align__(16) float sV[NB][kC][kRowsWG];
+    __shared__ float sBeta[NB][kC], sG[NB][kC];  // beta and the running log-decay sums g
+    __shared__ __align__(16) float sA[kC][kC];   // read as whole rows by the inverse
+    __shared__ float sP[2][kC][MS], sTb[2][kC][MS];
     __shared__ float sO[kC][kRowsWG + 1];
 
     const int tid = threadIdx.x;
@@ -330,80 +337,86 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
         if (tid < kC) sBeta[buf][tid] = rs;
         else if (tid < 2 * kC) sG[buf][tid - kC] = g_run;
     };
+    // K K^T -> A (wavefront 1) or Q K^T -> P (wavefront 2) of the chunk in buffer
+    // `buf`; lane l, register j holds entry [4(l/16) + j][l%16] of the product
+    auto products = [&](int buf, int pb) {
+        const float(*x)[KS] = w == 1 ? sK[buf] : sQ[buf];
+        f32x4 part[4] = {};
+#pragma unroll
+        for (int i = 0; i < KB; ++i) {
+            const f32x4 xa = *reinterpret_cast<const f32x4 *>(&x[lr][16 * i + 4 * lg]);
+            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][16 * i + 4 * lg]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part[j] = mfma4(xa[j], ka[j], part[j]);
+        }
+        const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+        const float *gs = sG[buf];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = 4 * lg + j, p = lr;
+            const float e = p <= i ? expf(gs[i] - gs[p]) : 0.0f;
+            if (w == 1) sA[i][p] = p < i ? sBeta[buf][i] * e * acc[j] : 0.0f;
+            else sP[pb][i][p] = e * acc[j];
+        }
+    };
+    // T = (I + A)^-1 by forward substitution (lane m owns column m), stored as
+    // Tb = T diag(beta)
+    auto inverse = [&](int buf, int pb) {
+        const int m = l;
+        float col[kC];
+#pragma unroll
+        for (int i = 0; i < kC; ++i) col[i] = i == m ? 1.0f : 0.0f;
+#pragma unroll
+        for (int i = 1; i < kC; ++i) {
+            float row[kC];
+#pragma unroll
+            for (int p4 = 0; p4 < (i + 3) / 4; ++p4) {
+                const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sA[i][4 * p4]);
+                row[4 * p4] = v4.x; row[4 * p4 + 1] = v4.y;
+                row[4 * p4 + 2] = v4.z; row[4 * p4 + 3] = v4.w;
+            }
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int p = 0; p < i; p += 2) {
+                s0 = __builtin_fmaf(row[p], col[p], s0);
+                if (p + 1 < i) s1 = __builtin_fmaf(row[p + 1], col[p + 1], s1);
+            }
+            if (i > m) col[i] = -(s0 + s1);
+        }
+        const float bm = sBeta[buf][m];
+#pragma unroll
+        for (int i = 0; i < kC; ++i) sTb[pb][i][m] = col[i] * bm;
+    };
 
     f32x4 st[KB];
 #pragma unroll
     for (int i = 0; i < KB; ++i) st[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int chunks = (S + kC - 1) / kC;
+    // prologue: chunks 0 and 1 staged, chunk 0 prepared
     fetch(0);
     stage(0);
+    if (chunks > 1) {
+        fetch(1);
+        stage(1);
+    }
     __syncthreads();
+    if (w == 1 || w == 2) products(0, 0);
+    __syncthreads();
+    if (w == 0 && l < kC) inverse(0, 0);
+    __syncthreads();
+
     for (int c = 0; c < chunks; ++c) {
-        const int buf = c & 1;
-        if (c + 1 < chunks) fetch(c + 1);  // in flight while this chunk is computed
+        const int buf = c % NB, nbuf = (c + 1) % NB, pb = c & 1;
+        const bool ahead = c + 1 < chunks;
+        if (c + 2 < chunks) fetch(c + 2);  // in flight during this chunk's phases
         const int n = min(kC, S - c * kC);
         const float *gs = sG[buf];
 
-        // K K^T -> A (wavefront 1), Q K^T -> P (wavefront 2); lane l, register j
-        // holds entry [4(l/16) + j][l%16] of the 16x16 product
-        if (w == 1 || w == 2) {
-            const float(*x)[KS] = w == 1 ? sK[buf] : sQ[buf];
-            // four independent accumulation chains (keys 4(l/16) + j of every
-            // 16-key block), summed at the end
-            f32x4 part[4] = {};
-#pragma unroll
-            for (int i = 0; i < KB; ++i) {
-                const f32x4 xa = *reinterpret_cast<const f32x4 *>(&x[lr][16 * i + 4 * lg]);
-                const f32x4 ka = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][16 * i + 4 * lg]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) part[j] = mfma4(xa[j], ka[j], part[j]);
-            }
-            const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = 4 * lg + j, p = lr;
-                const float e = p <= i ? expf(gs[i] - gs[p]) : 0.0f;
-                if (w == 1) sA[i][p] = p < i ? sBeta[buf][i] * e * acc[j] : 0.0f;
-                else sP[i][p] = e * acc[j];
-            }
-        }
-        __syncthreads();
-
-        // wavefront 0: T = (I + A)^-1 by forward substitution, column m per lane,
-        // stored as Tb = T diag(beta)
-        if (w == 0 && l < kC) {
-            const int m = l;
-            float col[kC];
-#pragma unroll
-            for (int i = 0; i < kC; ++i) col[i] = i == m ? 1.0f : 0.0f;
-#pragma unroll
-            for (int i = 1; i < kC; ++i) {
-                float row[kC];
-#pragma unroll
-                for (int p4 = 0; p4 < (i + 3) / 4; ++p4) {
-                    const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sA[i][4 * p4]);
-                    row[4 * p4] = v4.x; row[4 * p4 + 1] = v4.y;
-                    row[4 * p4 + 2] = v4.z; row[4 * p4 + 3] = v4.w;
-                }
-                float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-                for (int p = 0; p < i; p += 2) {
-                    s0 = __builtin_fmaf(row[p], col[p], s0);
-                    if (p + 1 < i) s1 = __builtin_fmaf(row[p + 1], col[p + 1], s1);
-                }
-                if (i > m) col[i] = -(s0 + s1);
-            }
-            const float bm = sBeta[buf][m];
-#pragma unroll
-            for (int i = 0; i < kC; ++i) sTb[i][m] = col[i] * bm;
-        }
-
-        // Z = K S0^T and Y = diag(e^g) Q S0^T (independent of T)
+        // phase 1: Z = K S0^T and Q S0^T (two chains each); the next chunk's
+        // K K^T / Q K^T on wavefronts 1 and 2
         f32x4 Z = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
         if (live) {
-            // two chains each for Z and Q S0^T; Y = diag(e^g) Q S0^T scales the
-            // 4 result rows afterwards
             f32x4 z0 = {}, z1 = {}, y0 = {}, y1 = {};
 #pragma unroll
             for (int i = 0; i < KB; ++i) {
@@ -420,25 +433,28 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
             }
             Z = z0 + z1;
             Y = y0 + y1;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) Y[j] *= expf(gs[4 * lg + j]);
         }
-        __syncthreads();  // Tb ready
+        if (ahead && (w == 1 || w == 2)) products(nbuf, pb ^ 1);
+        __syncthreads();
 
+        // phase 2: U, O and the state update of chunk c; the next chunk's inverse
         if (live) {
             const float gl = gs[kC - 1];
             // R = V - diag(e^g) Z in accumulator layout = the B operand of U = Tb R
             f32x4 R;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                R[j] = sV[buf][4 * lg + j][wrow + lr] - expf(gs[4 * lg + j]) * Z[j];
+            for (int j = 0; j < 4; ++j) {
+                const float eg = expf(gs[4 * lg + j]);
+                R[j] = sV[buf][4 * lg + j][wrow + lr] - eg * Z[j];
+                Y[j] *= eg;  // Y = diag(e^g) Q S0^T
+            }
             f32x4 U = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) U = mfma4(sTb[lr][4 * lg + i], R[i], U);
+            for (int i = 0; i < 4; ++i) U = mfma4(sTb[pb][lr][4 * lg + i], R[i], U);
             f32x4 O = Y;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) O = mfma4(sP[lr][4 * lg + i], U[i], O);
-            // S^T update; the decay weights e^(g_15 - g_tau) scale U's rows (the
+            for (int i = 0; i < 4; ++i) O = mfma4(sP[pb][lr][4 * lg + i], U[i], O);
+            // state update; the decay weights e^(g_15 - g_tau) scale U's rows (the
             // lane's register i is token 4(l/16) + i)
             f32x4 Ue;
 #pragma unroll
@@ -454,8 +470,11 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) sO[4 * lg + j][wrow + lr] = O[j];
         }
+        if (ahead && w == 0 && l < kC) inverse(nbuf, pb ^ 1);
         __syncthreads();
-        if (c + 1 < chunks) stage(buf ^ 1);
+
+        // phase 3: stage chunk c+2, write chunk c
+        if (c + 2 < chunks) stage((c + 2) % NB);
         for (int e = tid; e < kC * kRowsWG; e += kBlock) {
             const int tt = e / kRowsWG, r = e - tt * kRowsWG;
             if (tt < n && row0 + r < a.vd)
