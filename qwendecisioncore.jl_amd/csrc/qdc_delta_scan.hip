@@ -263,13 +263,21 @@ __device__ __forceinline__ float row_prefix_sum(float v) {
     return v;
 }
 
-template <int KB, typename TO>
-__global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
+// KSPLIT = 2 gives every 16-row tile two wavefronts, each holding half of the
+// key blocks of the state: Z and Q S0^T are summed from the two halves through
+// LDS, U and O are formed by both, and each updates its own half of S^T.  That
+// doubles the wavefronts (two per SIMD at the 0.8B shapes) so one wavefront's
+// waits overlap the other's matrix work.
+template <int KB, int KSPLIT, typename TO>
+__global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a) {
+    constexpr int NT = kBlock * KSPLIT;      // threads per workgroup
+    constexpr int KBW = KB / KSPLIT;         // key blocks of the state per wavefront
+    static_assert(KB % KSPLIT == 0, "key blocks split evenly");
     constexpr int KD = 16 * KB;             // key dimension
     constexpr int KS = KD + 4;              // LDS row stride of k/q rows (bank spread)
     constexpr int MS = kC + 1;              // row stride of the small matrices read by column
     constexpr int NB = 3;                   // k/q/v buffers: current, prepared, staging
-    constexpr int KQ_ITEMS = (kC * KD / 4 + kBlock - 1) / kBlock;  // 16-byte loads per thread
+    constexpr int KQ_ITEMS = (kC * KD / 4 + NT - 1) / NT;  // 16-byte loads per thread
     __shared__ __align__(16) float sK[NB][kC][KS];
     __shared__ __align__(16) float sQ[NB][kC][KS];
     __shared__ __align__(16) float sV[NB][kC][kRowsWG];
@@ -277,9 +285,12 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
     __shared__ __align__(16) float sA[kC][kC];   // read as whole rows by the inverse
     __shared__ float sP[2][kC][MS], sTb[2][kC][MS];
     __shared__ float sO[kC][kRowsWG + 1];
+    __shared__ float sPart[KSPLIT > 1 ? 2 * KSPLIT * 4 : 1][kC][kC + 1];  // Z / Q S0^T halves
 
     const int tid = threadIdx.x;
-    const int w = tid / kWave, l = tid % kWave, lr = l % 16, lg = l / 16;
+    const int wv = tid / kWave, l = tid % kWave, lr = l % 16, lg = l / 16;
+    const int w = wv % 4;                         // row tile of this wavefront
+    const int kh = wv / 4;                        // key half (KSPLIT = 2)
     const int h = blockIdx.y, b = blockIdx.z;
     const int g = h / a.groups;
     const int row0 = blockIdx.x * kRowsWG;
@@ -301,7 +312,7 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
         const int t0 = c * kC, n = min(kC, S - t0);
 #pragma unroll
         for (int p = 0; p < KQ_ITEMS; ++p) {
-            const int idx = tid + p * kBlock;
+            const int idx = tid + p * NT;
             const int tt = idx / kd4, j4 = idx - tt * kd4;
             rk[p] = f32x4{0.f, 0.f, 0.f, 0.f};
             rq[p] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -314,7 +325,7 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
         {   // v: 16 tokens x 64 rows, one 16-byte piece per thread
             const int tt = tid / 16, r4 = (tid % 16) * 4;
             rv = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (tt < n && row0 + r4 < a.vd)
+            if (tid < kC * kRowsWG / 4 && tt < n && row0 + r4 < a.vd)
                 rv = *reinterpret_cast<const f32x4 *>(vb + (int64_t)(t0 + tt) * v_tok + r4);
         }
         rs = 0.0f;
@@ -324,14 +335,14 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
     auto stage = [&](int buf) {
 #pragma unroll
         for (int p = 0; p < KQ_ITEMS; ++p) {
-            const int idx = tid + p * kBlock;
+            const int idx = tid + p * NT;
             const int tt = idx / kd4, j4 = idx - tt * kd4;
             if (tt < kC) {
                 *reinterpret_cast<f32x4 *>(&sK[buf][tt][j4 * 4]) = rk[p];
                 *reinterpret_cast<f32x4 *>(&sQ[buf][tt][j4 * 4]) = rq[p];
             }
         }
-        *reinterpret_cast<f32x4 *>(&sV[buf][tid / 16][(tid % 16) * 4]) = rv;
+        if (tid < kC * kRowsWG / 4) *reinterpret_cast<f32x4 *>(&sV[buf][tid / 16][(tid % 16) * 4]) = rv;
         // lanes 16..31 hold the 16 decays: one row of the wavefront
         const float g_run = row_prefix_sum(rs);
         if (tid < kC) sBeta[buf][tid] = rs;
@@ -388,9 +399,9 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
         for (int i = 0; i < kC; ++i) sTb[pb][i][m] = col[i] * bm;
     };
 
-    f32x4 st[KB];
+    f32x4 st[KBW];  // state key blocks kh*KBW .. kh*KBW + KBW - 1
 #pragma unroll
-    for (int i = 0; i < KB; ++i) st[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < KBW; ++i) st[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int chunks = (S + kC - 1) / kC;
     // prologue: chunks 0 and 1 staged, chunk 0 prepared
@@ -401,9 +412,9 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
         stage(1);
     }
     __syncthreads();
-    if (w == 1 || w == 2) products(0, 0);
+    if (kh == 0 && (w == 1 || w == 2)) products(0, 0);
     __syncthreads();
-    if (w == 0 && l < kC) inverse(0, 0);
+    if (wv == 0 && l < kC) inverse(0, 0);
     __syncthreads();
 
     for (int c = 0; c < chunks; ++c) {
@@ -419,9 +430,10 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
         if (live) {
             f32x4 z0 = {}, z1 = {}, y0 = {}, y1 = {};
 #pragma unroll
-            for (int i = 0; i < KB; ++i) {
-                const f32x4 kv = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][16 * i + 4 * lg]);
-                const f32x4 qv = *reinterpret_cast<const f32x4 *>(&sQ[buf][lr][16 * i + 4 * lg]);
+            for (int i = 0; i < KBW; ++i) {
+                const int kk = 16 * (kh * KBW + i) + 4 * lg;
+                const f32x4 kv = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][kk]);
+                const f32x4 qv = *reinterpret_cast<const f32x4 *>(&sQ[buf][lr][kk]);
                 z0 = mfma4(kv[0], st[i][0], z0);
                 y0 = mfma4(qv[0], st[i][0], y0);
                 z1 = mfma4(kv[1], st[i][1], z1);
@@ -433,9 +445,25 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
             }
             Z = z0 + z1;
             Y = y0 + y1;
+            if constexpr (KSPLIT > 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sPart[(0 * KSPLIT + kh) * 4 + w][4 * lg + j][lr] = Z[j];
+                    sPart[(1 * KSPLIT + kh) * 4 + w][4 * lg + j][lr] = Y[j];
+                }
+            }
         }
-        if (ahead && (w == 1 || w == 2)) products(nbuf, pb ^ 1);
+        if (ahead && kh == 0 && (w == 1 || w == 2)) products(nbuf, pb ^ 1);
         __syncthreads();
+        if constexpr (KSPLIT > 1) {  // add the other key half's partial products
+            if (live) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    Z[j] += sPart[(0 * KSPLIT + (1 - kh)) * 4 + w][4 * lg + j][lr];
+                    Y[j] += sPart[(1 * KSPLIT + (1 - kh)) * 4 + w][4 * lg + j][lr];
+                }
+            }
+        }
 
         // phase 2: U, O and the state update of chunk c; the next chunk's inverse
         if (live) {
@@ -461,21 +489,24 @@ __global__ __launch_bounds__(kBlock) void delta_scan_chunked(ScanArgs a) {
             for (int i = 0; i < 4; ++i) Ue[i] = U[i] * expf(gl - gs[4 * lg + i]);
             const float gll = expf(gl);
 #pragma unroll
-            for (int t = 0; t < KB; ++t) {
+            for (int t = 0; t < KBW; ++t) {
                 f32x4 acc = st[t] * gll;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc = mfma4(sK[buf][4 * lg + i][16 * t + lr], Ue[i], acc);
+                for (int i = 0; i < 4; ++i)
+                    acc = mfma4(sK[buf][4 * lg + i][16 * (kh * KBW + t) + lr], Ue[i], acc);
                 st[t] = acc;
             }
+            if (kh == 0) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sO[4 * lg + j][wrow + lr] = O[j];
+                for (int j = 0; j < 4; ++j) sO[4 * lg + j][wrow + lr] = O[j];
+            }
         }
-        if (ahead && w == 0 && l < kC) inverse(nbuf, pb ^ 1);
+        if (ahead && wv == 0 && l < kC) inverse(nbuf, pb ^ 1);
         __syncthreads();
 
         // phase 3: stage chunk c+2, write chunk c
         if (c + 2 < chunks) stage((c + 2) % NB);
-        for (int e = tid; e < kC * kRowsWG; e += kBlock) {
+        for (int e = tid; e < kC * kRowsWG; e += NT) {
             const int tt = e / kRowsWG, r = e - tt * kRowsWG;
             if (tt < n && row0 + r < a.vd)
                 ob[(int64_t)(c * kC + tt) * v_tok + r] = from_f32<TO>(sO[tt][r]);
@@ -527,21 +558,21 @@ extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, 
         aligned16(v)) {
         const dim3 cgrid((uint32_t)ceil_div(value_dim, kRowsWG), (uint32_t)heads,
                          (uint32_t)batch);
-#define QDC_CHUNKED(KB)                                                                        \
+#define QDC_CHUNKED(KB, KSPLIT)                                                                \
     if (key_dim == 16 * KB) {                                                                  \
         if (out_dtype == QDC_BF16)                                                             \
-            hipLaunchKernelGGL((delta_scan_chunked<KB, bf16_t>), cgrid, dim3(kBlock), 0,       \
-                               stream, a);                                                     \
+            hipLaunchKernelGGL((delta_scan_chunked<KB, KSPLIT, bf16_t>), cgrid,                \
+                               dim3(kBlock * KSPLIT), 0, stream, a);                           \
         else                                                                                   \
-            hipLaunchKernelGGL((delta_scan_chunked<KB, float>), cgrid, dim3(kBlock), 0,        \
-                               stream, a);                                                     \
+            hipLaunchKernelGGL((delta_scan_chunked<KB, KSPLIT, float>), cgrid,                 \
+                               dim3(kBlock * KSPLIT), 0, stream, a);                           \
         return launch_status();                                                                \
     }
-        QDC_CHUNKED(1)
-        QDC_CHUNKED(2)
-        QDC_CHUNKED(4)
-        QDC_CHUNKED(8)
-        QDC_CHUNKED(16)
+        QDC_CHUNKED(1, 1)
+        QDC_CHUNKED(2, 2)
+        QDC_CHUNKED(4, 2)
+        QDC_CHUNKED(8, 2)
+        QDC_CHUNKED(16, 2)
 #undef QDC_CHUNKED
     }
     const bool vec = aligned16(q) && aligned16(k) && key_dim % 4 == 0;
