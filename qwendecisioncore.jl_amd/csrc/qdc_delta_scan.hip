@@ -231,23 +231,26 @@ __global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
 //     O = diag(e^g) Q S0^T + P U,   P[i][p] = exp(g_i - g_p) (q_i . k_p)  (p <= i)
 //     S^T <- e^(g_15) S^T + (diag(e^(g_15 - g)) K)^T U
 // (a partial last chunk is padded with k = q = v = 0, beta = 0, d = 0).  A
-// workgroup owns 64 value rows of one (sequence, head), 16 per wavefront; the
-// state tile of a wavefront lives in MFMA accumulator layout (lane l, register j:
+// workgroup owns 64 value rows of one (sequence, head), 16 per row tile; the
+// state of a tile lives in MFMA accumulator layout (lane l, register j:
 // S^T[16a + 4(l/16) + j][16w + l%16]), which is also the B-operand layout the
 // next chunk's S^T products read, so the state never leaves registers.
 //
 // Everything that does not involve the state (K K^T, Q K^T, A, P and the
-// triangular inverse) is prepared one chunk ahead, overlapped with the current
-// chunk's state products: per chunk c the workgroup runs
-//     phase 1: Z, Q S0^T of chunk c (all wavefronts) | K K^T -> A, Q K^T -> P of
-//              chunk c+1 (wavefronts 1, 2)
-//     phase 2: U, O, state update of chunk c (all) | (I + A)^-1 of chunk c+1 by
-//              forward substitution (wavefront 0, one lane per column)
-//     phase 3: stage chunk c+2 (its global loads were issued before phase 1) and
-//              write chunk c's outputs
-// with three barriers; k, q, v live in three LDS buffers, P and T diag(beta) in two.
+// triangular inverse) is prepared ahead, overlapped with the state products.
+// Per chunk c the workgroup runs two phases:
+//     phase 1: Z, Q S0^T of chunk c (every wavefront); K K^T and Q K^T of chunk
+//              c+1 split over the key dimension into four products, one per
+//              SIMD; T diag(beta) of chunk c from A (the helper wavefront, the
+//              last one); chunk c-1's outputs written from LDS (the others)
+//     phase 2: U, O and the state update of chunk c (every wavefront); A (the
+//              helper) and P (the wavefront before it) of chunk c+1 from the
+//              partial products; chunk c+2 staged (its loads were issued in
+//              phase 1)
+// with one barrier after each.  k, q, v live in three LDS buffers; P and the
+// outputs in two.
 constexpr int kC = 16;        // tokens per chunk: one MFMA tile edge
-constexpr int kRowsWG = 64;   // value rows per workgroup, 16 per wavefront
+constexpr int kRowsWG = 64;   // value rows per workgroup, 16 per row tile
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -265,26 +268,31 @@ __device__ __forceinline__ float row_prefix_sum(float v) {
 
 // KSPLIT = 2 gives every 16-row tile two wavefronts, each holding half of the
 // key blocks of the state: Z and Q S0^T are summed from the two halves through
-// LDS, U and O are formed by both, and each updates its own half of S^T.  That
-// doubles the wavefronts (two per SIMD at the 0.8B shapes) so one wavefront's
-// waits overlap the other's matrix work.
+// LDS, U is formed by both, O by the first, and each updates its own half of
+// S^T.  That doubles the wavefronts (two per SIMD at the 0.8B shapes) so one
+// wavefront's waits overlap the other's matrix work.
 template <int KB, int KSPLIT, typename TO>
 __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a) {
     constexpr int NT = kBlock * KSPLIT;      // threads per workgroup
     constexpr int KBW = KB / KSPLIT;         // key blocks of the state per wavefront
     static_assert(KB % KSPLIT == 0, "key blocks split evenly");
+    static_assert(KB == 1 || KB % 2 == 0, "key blocks split into two halves");
     constexpr int KD = 16 * KB;             // key dimension
     constexpr int KS = KD + 4;              // LDS row stride of k/q rows (bank spread)
     constexpr int MS = kC + 1;              // row stride of the small matrices read by column
     constexpr int NB = 3;                   // k/q/v buffers: current, prepared, staging
     constexpr int KQ_ITEMS = (kC * KD / 4 + NT - 1) / NT;  // 16-byte loads per thread
+    constexpr int kHelper = NT / kWave - 1;  // wavefront preparing A, P and the inverse
     __shared__ __align__(16) float sK[NB][kC][KS];
     __shared__ __align__(16) float sQ[NB][kC][KS];
     __shared__ __align__(16) float sV[NB][kC][kRowsWG];
-    __shared__ float sBeta[NB][kC], sG[NB][kC];  // beta and the running log-decay sums g
+    // per token: beta, the running log-decay sum g, e^g and e^(g_15 - g)
+    __shared__ float sBeta[NB][kC], sG[NB][kC], sEg[NB][kC], sEt[NB][kC];
     __shared__ __align__(16) float sA[kC][kC];   // read as whole rows by the inverse
-    __shared__ float sP[2][kC][MS], sTb[2][kC][MS];
-    __shared__ float sO[kC][kRowsWG + 1];
+    __shared__ float sProd[4][kC][MS];           // K K^T and Q K^T, two key halves each
+    __shared__ float sP[2][kC][MS], sTb[kC][MS];
+    __shared__ float sT[kC][MS];                 // diagonal blocks of T (inverse)
+    __shared__ float sO[2][kC][kRowsWG + 1];
     __shared__ float sPart[KSPLIT > 1 ? 2 * KSPLIT * 4 : 1][kC][kC + 1];  // Z / Q S0^T halves
 
     const int tid = threadIdx.x;
@@ -345,58 +353,134 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
         if (tid < kC * kRowsWG / 4) *reinterpret_cast<f32x4 *>(&sV[buf][tid / 16][(tid % 16) * 4]) = rv;
         // lanes 16..31 hold the 16 decays: one row of the wavefront
         const float g_run = row_prefix_sum(rs);
-        if (tid < kC) sBeta[buf][tid] = rs;
-        else if (tid < 2 * kC) sG[buf][tid - kC] = g_run;
+        const float g_last = __shfl(g_run, 2 * kC - 1, kWave);
+        if (tid < kC) {
+            sBeta[buf][tid] = rs;
+        } else if (tid < 2 * kC) {
+            sG[buf][tid - kC] = g_run;
+            sEg[buf][tid - kC] = expf(g_run);
+            sEt[buf][tid - kC] = expf(g_last - g_run);
+        }
     };
-    // K K^T -> A (wavefront 1) or Q K^T -> P (wavefront 2) of the chunk in buffer
-    // `buf`; lane l, register j holds entry [4(l/16) + j][l%16] of the product
-    auto products = [&](int buf, int pb) {
-        const float(*x)[KS] = w == 1 ? sK[buf] : sQ[buf];
+    // One quarter of the next chunk's products (wavefront w of the first key
+    // half, one per SIMD): w = 0, 1 -> K K^T, w = 2, 3 -> Q K^T, each over half
+    // of the key dimension; lane l, register j holds entry [4(l/16) + j][l%16]
+    auto products = [&](int buf) {
+        const float(*x)[KS] = w < 2 ? sK[buf] : sQ[buf];
+        const int half = w & 1;
         f32x4 part[4] = {};
+        if constexpr (KB == 1) {
+            const f32x4 xa = *reinterpret_cast<const f32x4 *>(&x[lr][4 * lg]);
+            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][4 * lg]);
+            part[0] = mfma4(half ? xa[2] : xa[0], half ? ka[2] : ka[0], part[0]);
+            part[1] = mfma4(half ? xa[3] : xa[1], half ? ka[3] : ka[1], part[1]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < KB; ++i) {
-            const f32x4 xa = *reinterpret_cast<const f32x4 *>(&x[lr][16 * i + 4 * lg]);
-            const f32x4 ka = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][16 * i + 4 * lg]);
+            for (int ii = 0; ii < KB / 2; ++ii) {
+                const int i = half * (KB / 2) + ii;
+                const f32x4 xa = *reinterpret_cast<const f32x4 *>(&x[lr][16 * i + 4 * lg]);
+                const f32x4 ka = *reinterpret_cast<const f32x4 *>(&sK[buf][lr][16 * i + 4 * lg]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) part[j] = mfma4(xa[j], ka[j], part[j]);
+                for (int j = 0; j < 4; ++j) part[j] = mfma4(xa[j], ka[j], part[j]);
+            }
         }
         const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sProd[w][4 * lg + j][lr] = acc[j];
+    };
+    // A (want_a) or P of the chunk in buffer `buf` from the partial products;
+    // lane l, entry j: row 4(l/16) + j, column l%16.  One wavefront each.
+    auto finalize = [&](int buf, int pbn, bool want_a) {
         const float *gs = sG[buf];
+        const int s0 = want_a ? 0 : 2;
+        float x0[4], x1[4], gi[4], bi[4];
+        const float gp = gs[lr];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int i = 4 * lg + j, p = lr;
-            const float e = p <= i ? expf(gs[i] - gs[p]) : 0.0f;
-            if (w == 1) sA[i][p] = p < i ? sBeta[buf][i] * e * acc[j] : 0.0f;
-            else sP[pb][i][p] = e * acc[j];
+            const int i = 4 * lg + j;
+            x0[j] = sProd[s0][i][lr];
+            x1[j] = sProd[s0 + 1][i][lr];
+            gi[j] = gs[i];
+            bi[j] = sBeta[buf][i];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // all reads in flight before the first use
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = 4 * lg + j;
+            const bool keep = lr <= i;
+            const float e = expf(keep ? gi[j] - gp : 0.0f);
+            if (want_a) sA[i][lr] = lr < i ? bi[j] * e * (x0[j] + x1[j]) : 0.0f;
+            else sP[pbn][i][lr] = keep ? e * (x0[j] + x1[j]) : 0.0f;
         }
     };
-    // T = (I + A)^-1 by forward substitution (lane m owns column m), stored as
-    // Tb = T diag(beta)
-    auto inverse = [&](int buf, int pb) {
-        const int m = l;
-        float col[kC];
+    // T = (I + A)^-1 of the chunk in buffer `buf`, stored as Tb = T diag(beta).
+    // One wavefront.  Blocked: with A = [[A11, 0], [A21, A22]] in 8x8 blocks,
+    // D = diag(T11, T22) comes from forward substitution on both diagonal blocks
+    // at once (lane m < 16 owns column m of its block), and T = D - D (N D) with
+    // N = [[0, 0], [A21, 0]] (two 16x16 products on the matrix cores;
+    // T21 = -T22 A21 T11).
+    auto inverse = [&](int buf) {
+        if (l < kC) {  // D: the diagonal blocks, zeros elsewhere
+            const int m = l, b0 = m & 8, mm = m & 7;
+            float arow[8][8];
 #pragma unroll
-        for (int i = 0; i < kC; ++i) col[i] = i == m ? 1.0f : 0.0f;
+            for (int i = 1; i < 8; ++i)
 #pragma unroll
-        for (int i = 1; i < kC; ++i) {
-            float row[kC];
+                for (int p = 0; p < i; ++p) arow[i][p] = sA[b0 + i][b0 + p];
+            __builtin_amdgcn_sched_barrier(0);  // all reads in flight before the first use
+            float col[8];
 #pragma unroll
-            for (int p4 = 0; p4 < (i + 3) / 4; ++p4) {
-                const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sA[i][4 * p4]);
-                row[4 * p4] = v4.x; row[4 * p4 + 1] = v4.y;
-                row[4 * p4 + 2] = v4.z; row[4 * p4 + 3] = v4.w;
+            for (int i = 0; i < 8; ++i) col[i] = i == mm ? 1.0f : 0.0f;
+#pragma unroll
+            for (int i = 1; i < 8; ++i) {
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int p = 0; p < i; p += 2) {
+                    s0 = __builtin_fmaf(arow[i][p], col[p], s0);
+                    if (p + 1 < i) s1 = __builtin_fmaf(arow[i][p + 1], col[p + 1], s1);
+                }
+                if (i > mm) col[i] = -(s0 + s1);
             }
-            float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-            for (int p = 0; p < i; p += 2) {
-                s0 = __builtin_fmaf(row[p], col[p], s0);
-                if (p + 1 < i) s1 = __builtin_fmaf(row[p + 1], col[p + 1], s1);
+            for (int i = 0; i < 8; ++i) {
+                sT[b0 + i][m] = col[i];
+                sT[(b0 ^ 8) + i][m] = 0.0f;
             }
-            if (i > m) col[i] = -(s0 + s1);
         }
-        const float bm = sBeta[buf][m];
+        // D is read across lanes below; LDS operations of one wavefront complete
+        // in order, the fence keeps the compiler from reordering them
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // X = N D: k-slot s of step i is k = 4s + i (lane group l/16 = s)
+        const f32x4 na = *reinterpret_cast<const f32x4 *>(&sA[lr][4 * lg]);
+        const float bm = sBeta[buf][lr];
+        float db[4], da[4];
 #pragma unroll
-        for (int i = 0; i < kC; ++i) sTb[pb][i][m] = col[i] * bm;
+        for (int i = 0; i < 4; ++i) {
+            db[i] = sT[4 * lg + i][lr];  // D[k][lr]
+            da[i] = sT[lr][4 * lg + i];  // D[lr][k]
+        }
+        const bool lower = lr >= 8 && lg < 2;  // N[lr][k] nonzero only for lr >= 8, k < 8
+        f32x4 X = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X = mfma4(lower ? na[i] : 0.0f, db[i], X);
+        // Y = D X: X in accumulator layout (register i = row 4(l/16) + i) is the
+        // B operand of that same k-slot order
+        f32x4 Yd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Yd = mfma4(da[i], X[i], Yd);
+        // T = D - Y; entry (4(l/16) + j, l%16) of D is db[j]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sTb[4 * lg + j][lr] = (db[j] - Yd[j]) * bm;
+    };
+    // outputs of chunk cw (rows of sO[cw & 1]) to memory, by threads 0..nt-1
+    auto write_out = [&](int cw, int nt) {
+        const int n = min(kC, S - cw * kC);
+        const float(*so)[kRowsWG + 1] = sO[cw & 1];
+        for (int e = tid; e < kC * kRowsWG; e += nt) {
+            const int tt = e / kRowsWG, r = e - tt * kRowsWG;
+            if (tt < n && row0 + r < a.vd)
+                ob[(int64_t)(cw * kC + tt) * v_tok + r] = from_f32<TO>(so[tt][r]);
+        }
     };
 
     f32x4 st[KBW];  // state key blocks kh*KBW .. kh*KBW + KBW - 1
@@ -404,7 +488,7 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
     for (int i = 0; i < KBW; ++i) st[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int chunks = (S + kC - 1) / kC;
-    // prologue: chunks 0 and 1 staged, chunk 0 prepared
+    // prologue: chunks 0 and 1 staged, A and P of chunk 0 formed
     fetch(0);
     stage(0);
     if (chunks > 1) {
@@ -412,20 +496,19 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
         stage(1);
     }
     __syncthreads();
-    if (kh == 0 && (w == 1 || w == 2)) products(0, 0);
+    if (kh == 0) products(0);
     __syncthreads();
-    if (wv == 0 && l < kC) inverse(0, 0);
+    if (wv == kHelper) finalize(0, 0, true);
+    if (wv == kHelper - 1) finalize(0, 0, false);
     __syncthreads();
 
     for (int c = 0; c < chunks; ++c) {
         const int buf = c % NB, nbuf = (c + 1) % NB, pb = c & 1;
         const bool ahead = c + 1 < chunks;
-        if (c + 2 < chunks) fetch(c + 2);  // in flight during this chunk's phases
-        const int n = min(kC, S - c * kC);
-        const float *gs = sG[buf];
+        if (c + 2 < chunks) fetch(c + 2);  // in flight during both phases
 
-        // phase 1: Z = K S0^T and Q S0^T (two chains each); the next chunk's
-        // K K^T / Q K^T on wavefronts 1 and 2
+        // phase 1: Z = K S0^T and Q S0^T (two chains each); a quarter of the next
+        // chunk's K K^T / Q K^T; the previous chunk's outputs
         f32x4 Z = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
         if (live) {
             f32x4 z0 = {}, z1 = {}, y0 = {}, y1 = {};
@@ -453,7 +536,9 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
                 }
             }
         }
-        if (ahead && kh == 0 && (w == 1 || w == 2)) products(nbuf, pb ^ 1);
+        if (ahead && kh == 0) products(nbuf);
+        if (wv == kHelper) inverse(buf);
+        else if (c > 0) write_out(c - 1, NT - kWave);  // the helper is the last wavefront
         __syncthreads();
         if constexpr (KSPLIT > 1) {  // add the other key half's partial products
             if (live) {
@@ -465,29 +550,33 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
             }
         }
 
-        // phase 2: U, O and the state update of chunk c; the next chunk's inverse
+        // phase 2: U, O and the state update of chunk c; A and P of chunk c+1;
+        // chunk c+2 staged
         if (live) {
-            const float gl = gs[kC - 1];
             // R = V - diag(e^g) Z in accumulator layout = the B operand of U = Tb R
             f32x4 R;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float eg = expf(gs[4 * lg + j]);
+                const float eg = sEg[buf][4 * lg + j];
                 R[j] = sV[buf][4 * lg + j][wrow + lr] - eg * Z[j];
                 Y[j] *= eg;  // Y = diag(e^g) Q S0^T
             }
             f32x4 U = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) U = mfma4(sTb[pb][lr][4 * lg + i], R[i], U);
-            f32x4 O = Y;
+            for (int i = 0; i < 4; ++i) U = mfma4(sTb[lr][4 * lg + i], R[i], U);
+            if (kh == 0) {
+                f32x4 O = Y;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) O = mfma4(sP[pb][lr][4 * lg + i], U[i], O);
+                for (int i = 0; i < 4; ++i) O = mfma4(sP[pb][lr][4 * lg + i], U[i], O);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sO[pb][4 * lg + j][wrow + lr] = O[j];
+            }
             // state update; the decay weights e^(g_15 - g_tau) scale U's rows (the
             // lane's register i is token 4(l/16) + i)
             f32x4 Ue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) Ue[i] = U[i] * expf(gl - gs[4 * lg + i]);
-            const float gll = expf(gl);
+            for (int i = 0; i < 4; ++i) Ue[i] = U[i] * sEt[buf][4 * lg + i];
+            const float gll = sEg[buf][kC - 1];
 #pragma unroll
             for (int t = 0; t < KBW; ++t) {
                 f32x4 acc = st[t] * gll;
@@ -496,23 +585,13 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
                     acc = mfma4(sK[buf][4 * lg + i][16 * (kh * KBW + t) + lr], Ue[i], acc);
                 st[t] = acc;
             }
-            if (kh == 0) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) sO[4 * lg + j][wrow + lr] = O[j];
-            }
         }
-        if (ahead && wv == 0 && l < kC) inverse(nbuf, pb ^ 1);
-        __syncthreads();
-
-        // phase 3: stage chunk c+2, write chunk c
+        if (ahead && wv == kHelper) finalize(nbuf, pb ^ 1, true);
+        if (ahead && wv == kHelper - 1) finalize(nbuf, pb ^ 1, false);
         if (c + 2 < chunks) stage((c + 2) % NB);
-        for (int e = tid; e < kC * kRowsWG; e += NT) {
-            const int tt = e / kRowsWG, r = e - tt * kRowsWG;
-            if (tt < n && row0 + r < a.vd)
-                ob[(int64_t)(c * kC + tt) * v_tok + r] = from_f32<TO>(sO[tt][r]);
-        }
         __syncthreads();
     }
+    write_out(chunks - 1, NT);
 }
 
 }  // namespace
