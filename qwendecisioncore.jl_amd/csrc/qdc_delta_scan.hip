@@ -507,8 +507,12 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
         const bool ahead = c + 1 < chunks;
         if (c + 2 < chunks) fetch(c + 2);  // in flight during both phases
 
-        // phase 1: Z = K S0^T and Q S0^T (two chains each); a quarter of the next
-        // chunk's K K^T / Q K^T; the previous chunk's outputs
+        // phase 1: the previous chunk's outputs or this chunk's inverse first (their
+        // latency overlaps the other wavefront's matrix products), then Z = K S0^T
+        // and Q S0^T (two chains each) and a quarter of the next chunk's K K^T /
+        // Q K^T
+        if (wv == kHelper) inverse(buf);
+        else if (c > 0) write_out(c - 1, NT - kWave);  // the helper is the last wavefront
         f32x4 Z = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
         if (live) {
             f32x4 z0 = {}, z1 = {}, y0 = {}, y1 = {};
@@ -537,8 +541,6 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
             }
         }
         if (ahead && kh == 0) products(nbuf);
-        if (wv == kHelper) inverse(buf);
-        else if (c > 0) write_out(c - 1, NT - kWave);  // the helper is the last wavefront
         __syncthreads();
         if constexpr (KSPLIT > 1) {  // add the other key half's partial products
             if (live) {
@@ -550,8 +552,10 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
             }
         }
 
-        // phase 2: U, O and the state update of chunk c; A and P of chunk c+1;
-        // chunk c+2 staged
+        // phase 2: A and P of chunk c+1 first, then U, O and the state update of
+        // chunk c; chunk c+2 staged
+        if (ahead && wv == kHelper) finalize(nbuf, pb ^ 1, true);
+        if (ahead && wv == kHelper - 1) finalize(nbuf, pb ^ 1, false);
         if (live) {
             // R = V - diag(e^g) Z in accumulator layout = the B operand of U = Tb R
             f32x4 R;
@@ -586,8 +590,6 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
                 st[t] = acc;
             }
         }
-        if (ahead && wv == kHelper) finalize(nbuf, pb ^ 1, true);
-        if (ahead && wv == kHelper - 1) finalize(nbuf, pb ^ 1, false);
         if (c + 2 < chunks) stage((c + 2) % NB);
         __syncthreads();
     }
