@@ -243,10 +243,10 @@ __global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
 //              c+1 split over the key dimension into four products, one per
 //              SIMD; T diag(beta) of chunk c from A (the helper wavefront, the
 //              last one); chunk c-1's outputs written from LDS (the others)
-//     phase 2: U, O and the state update of chunk c (every wavefront); A (the
-//              helper) and P (the wavefront before it) of chunk c+1 from the
-//              partial products; chunk c+2 staged (its loads were issued in
-//              phase 1)
+//     phase 2: U, O and the state update of chunk c (every wavefront); A and P
+//              of chunk c+1 from the partial products (the last key part's
+//              wavefronts, a quarter each); chunk c+2 staged (its loads were
+//              issued in phase 1)
 // with one barrier after each.  k, q, v live in three LDS buffers; P and the
 // outputs in two.
 constexpr int kC = 16;        // tokens per chunk: one MFMA tile edge
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
     constexpr int MS = kC + 1;              // row stride of the small matrices read by column
     constexpr int NB = 3;                   // k/q/v buffers: current, prepared, staging
     constexpr int KQ_ITEMS = (kC * KD / 4 + NT - 1) / NT;  // 16-byte loads per thread
-    constexpr int kHelper = NT / kWave - 1;  // wavefront preparing A, P and the inverse
+    constexpr int kHelper = NT / kWave - 1;  // wavefront forming the inverse
     __shared__ __align__(16) float sK[NB][kC][KS];
     __shared__ __align__(16) float sQ[NB][kC][KS];
     __shared__ __align__(16) float sV[NB][kC][kRowsWG];
@@ -388,30 +388,19 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
 #pragma unroll
         for (int j = 0; j < 4; ++j) sProd[w][4 * lg + j][lr] = acc[j];
     };
-    // A (want_a) or P of the chunk in buffer `buf` from the partial products;
-    // lane l, entry j: row 4(l/16) + j, column l%16.  One wavefront each.
-    auto finalize = [&](int buf, int pbn, bool want_a) {
+    // A and P of the chunk in buffer `buf` from the partial products: wavefront
+    // j of the four calling forms row 4(l/16) + j, column l%16 of both (nothing
+    // reads them before the next barrier)
+    auto finalize = [&](int buf, int pbn, int j) {
         const float *gs = sG[buf];
-        const int s0 = want_a ? 0 : 2;
-        float x0[4], x1[4], gi[4], bi[4];
-        const float gp = gs[lr];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = 4 * lg + j;
-            x0[j] = sProd[s0][i][lr];
-            x1[j] = sProd[s0 + 1][i][lr];
-            gi[j] = gs[i];
-            bi[j] = sBeta[buf][i];
-        }
-        __builtin_amdgcn_sched_barrier(0);  // all reads in flight before the first use
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = 4 * lg + j;
-            const bool keep = lr <= i;
-            const float e = expf(keep ? gi[j] - gp : 0.0f);
-            if (want_a) sA[i][lr] = lr < i ? bi[j] * e * (x0[j] + x1[j]) : 0.0f;
-            else sP[pbn][i][lr] = keep ? e * (x0[j] + x1[j]) : 0.0f;
-        }
+        const int i = 4 * lg + j;
+        const float kk0 = sProd[0][i][lr], kk1 = sProd[1][i][lr];
+        const float qk0 = sProd[2][i][lr], qk1 = sProd[3][i][lr];
+        const float gi = gs[i], gp = gs[lr], bi = sBeta[buf][i];
+        const bool keep = lr <= i;
+        const float e = expf(keep ? gi - gp : 0.0f);
+        sA[i][lr] = lr < i ? bi * e * (kk0 + kk1) : 0.0f;
+        sP[pbn][i][lr] = keep ? e * (qk0 + qk1) : 0.0f;
     };
     // T = (I + A)^-1 of the chunk in buffer `buf`, stored as Tb = T diag(beta).
     // One wavefront.  Blocked: with A = [[A11, 0], [A21, A22]] in 8x8 blocks,
@@ -498,14 +487,16 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
     __syncthreads();
     if (kh == 0) products(0);
     __syncthreads();
-    if (wv == kHelper) finalize(0, 0, true);
-    if (wv == kHelper - 1) finalize(0, 0, false);
+    if (kh == KSPLIT - 1) finalize(0, 0, w);
     __syncthreads();
 
     for (int c = 0; c < chunks; ++c) {
         const int buf = c % NB, nbuf = (c + 1) % NB, pb = c & 1;
         const bool ahead = c + 1 < chunks;
-        if (c + 2 < chunks) fetch(c + 2);  // in flight during both phases
+        // chunk c+2's loads land during both phases; the first key part issues
+        // them after its matrix products so the two wavefronts of a SIMD do not
+        // queue at the memory unit together
+        if (kh != 0 && c + 2 < chunks) fetch(c + 2);
 
         // phase 1: the previous chunk's outputs or this chunk's inverse first (their
         // latency overlaps the other wavefront's matrix products), then Z = K S0^T
@@ -540,6 +531,7 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
                 }
             }
         }
+        if (kh == 0 && c + 2 < chunks) fetch(c + 2);
         if (ahead && kh == 0) products(nbuf);
         __syncthreads();
         if constexpr (KSPLIT > 1) {  // add the other key half's partial products
@@ -554,8 +546,7 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
 
         // phase 2: A and P of chunk c+1 first, then U, O and the state update of
         // chunk c; chunk c+2 staged
-        if (ahead && wv == kHelper) finalize(nbuf, pb ^ 1, true);
-        if (ahead && wv == kHelper - 1) finalize(nbuf, pb ^ 1, false);
+        if (ahead && kh == KSPLIT - 1) finalize(nbuf, pb ^ 1, w);
         if (live) {
             // R = V - diag(e^g) Z in accumulator layout = the B operand of U = Tb R
             f32x4 R;
