@@ -39,9 +39,12 @@ __device__ __forceinline__ float wave_max(float v) {
     v = dpp_max_step<0x4E>(v);
     v = dpp_max_step<0x141>(v);
     v = dpp_max_step<0x140>(v);
-    v = fmaxf(v, __shfl_xor(v, 16, kWave));
-    v = fmaxf(v, __shfl_xor(v, 32, kWave));
-    return v;
+    // across rows with the lane swaps (see group_sum): the halves hold lanes l
+    // and l ^ 16, then l and l ^ 32
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
 // exp(v - peak) for v <= peak on the hardware exp2 unit: exp2((v - peak) log2 e).

@@ -153,10 +153,21 @@ template <int V> __device__ __forceinline__ void store_frag(bf16_t *p, const flo
 // of partial sums that the partner lane adds in the other order, and fp32
 // addition is commutative).  Steps inside a 16-lane row use DPP lane swizzles
 // (quad permutes, then the half-row and row mirrors, which pair each lane with
-// one in the other quad / half); the 16- and 32-lane steps cross rows and use
-// the LDS crossbar permute.
+// one in the other quad / half).  The 16- and 32-lane steps cross rows with the
+// gfx950 lane swaps: permlane16_swap(v, v) returns {v with each odd row replaced
+// by the even row before it, v with each even row replaced by the odd row after
+// it}, so the two halves sum to v[l] + v[l ^ 16] in the same operand order on
+// both partner lanes (permlane32_swap likewise for l ^ 32).
 template <int CTRL> __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float swap_sum16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap_sum32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 template <int N> __device__ __forceinline__ float group_sum(float v) {
@@ -165,8 +176,8 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
     if constexpr (N >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
     if constexpr (N >= 8) v += dpp<0x141>(v);  // row_half_mirror: lane 7-i of 8
     if constexpr (N >= 16) v += dpp<0x140>(v); // row_mirror: lane 15-i of 16
-    if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
-    if constexpr (N >= 64) v += __shfl_xor(v, 32, kWave);
+    if constexpr (N >= 32) v = swap_sum16(v);  // lane ^ 16
+    if constexpr (N >= 64) v = swap_sum32(v);  // lane ^ 32
     return v;
 }
 
