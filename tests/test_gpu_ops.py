@@ -323,6 +323,7 @@ def test_residual_rmsnorm_fp32_stream(mixed_dtype, out_dtype, rows, width):
     (1, 33, 1, 2, 64, 48, 2.0), (2, 16, 1, 1, 16, 16, 2.0), (1, 50, 2, 2, 32, 16, 2.0),
     (1, 300, 1, 1, 256, 32, 2.0), (1, 40, 1, 2, 128, 128, 40.0),    # strong decay
     (2, 20, 1, 2, 128, 80, 2.0),                                    # two chunks, 80 rows
+    (1, 2048, 1, 2, 128, 128, 0.05),                # a whole 0.8B-shaped sequence, weak decay
     (1, 5, 1, 2, 64, 20, 2.0), (1, 9, 1, 1, 256, 8, 2.0),           # recurrent kernel
     (2, 65, 1, 2, 2, 2, 2.0), (1, 17, 2, 6, 96, 33, 2.0)])
 def test_delta_scan(out_dtype, B, S, KH, H, kd, vd, dscale):
