@@ -43,7 +43,7 @@ struct Prologue {
     int chunks;             // qkv channels / 4
     int qk_chunks;          // 2*kh*kd / 4
     uint32_t blocks_per_tile;  // fast path: channel blocks + 1 gates block
-    float sqrt_kd;
+    float sqrt_kd, inv_sqrt_kd;
 };
 
 __device__ __forceinline__ float sigmoid_f(float x) {
@@ -113,18 +113,23 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     const bool live = ci < a.chunks;
     const int c0 = (live ? ci : 0) * 4;
     const bool is_q = ci < a.qk_chunks / 2, is_k = !is_q && ci < a.qk_chunks;
-    const T *base = reinterpret_cast<const T *>(a.proj) + c0;
+    // q and k heads are whole aligned lane groups and 2*kh*kd is a multiple of
+    // 64 channels in practice, so is_qk is normally uniform per wavefront
+    const bool is_qk = is_q || is_k;
 
     // position of t0 in its sequence; rows before that sequence's start are zero
     // for every token of the tile
     const uint32_t s0 = (uint32_t)t0 - fastdiv((uint32_t)t0, a.seq) * a.seq.d;
     const int64_t seq_start = t0 - s0;
     Raw rows[kRows];
+    {
+        const T *p = reinterpret_cast<const T *>(a.proj) + c0 + (t0 - (kTaps - 1)) * a.ld;
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const int64_t t = t0 - (kTaps - 1) + r;
-        rows[r] = Raw{};
-        if (live && t >= seq_start && t < a.tokens) rows[r] = *reinterpret_cast<const Raw *>(base + t * a.ld);
+        for (int r = 0; r < kRows; ++r, p += a.ld) {
+            const int64_t t = t0 - (kTaps - 1) + r;
+            rows[r] = Raw{};
+            if (live && t >= seq_start && t < a.tokens) rows[r] = *reinterpret_cast<const Raw *>(p);
+        }
     }
     float w[4][kTaps];
 #pragma unroll
@@ -133,58 +138,61 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
         for (int j = 0; j < kTaps; ++j) w[c][j] = live ? a.conv[(c0 + c) * kTaps + j] : 0.0f;
 
     const int64_t kw = (int64_t)a.kh * a.kd, vw = (int64_t)a.vh * a.vd;
+    // this thread's output chunk of token t0 and the stride between tokens
+    const int64_t dstride = is_qk ? kw : vw;
+    float *dst = (is_q ? a.q + c0 : is_k ? a.k + (c0 - kw) : a.v + (c0 - 2 * kw)) + t0 * dstride;
+    const float qk_mul = is_q ? a.inv_sqrt_kd : 1.0f;
     // A later sequence starts inside the tile only when fewer than kTileT
     // positions remain in t0's sequence; only then do taps need a per-token mask.
     const bool inner_start = a.seq.d - s0 < (uint32_t)kTileT;
-    auto token = [&](int tt, auto masked) {
-        const int64_t t = t0 + tt;
-        const bool tok = t < a.tokens;
-        uint32_t s = 0;  // position of t in its sequence (masked tiles only)
-        if constexpr (decltype(masked)::value)
-            s = tok ? (uint32_t)t - fastdiv((uint32_t)t, a.seq) * a.seq.d : 0u;
+    auto run_tile = [&](auto masked) {
+        // the window of unpacked rows t-3 .. t (row t - (kTaps-1) + j is tap j)
         float x[kTaps][4];
 #pragma unroll
-        for (int j = 0; j < kTaps; ++j) Raw4<T>::unpack(rows[tt + j], x[j]);  // row t - (kTaps-1) + j
-        float m[4];
+        for (int j = 0; j < kTaps - 1; ++j) Raw4<T>::unpack(rows[j], x[j + 1]);
+        float *out = dst;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            // tap j multiplies row t - (kTaps-1) + j; fused multiply-add per tap
-            float acc = 0.0f;
+        for (int tt = 0; tt < kTileT; ++tt, out += dstride) {
 #pragma unroll
-            for (int j = 0; j < kTaps; ++j) {
-                if constexpr (decltype(masked)::value) {
-                    if (s >= (uint32_t)(kTaps - 1 - j)) acc = __builtin_fmaf(x[j][c], w[c][j], acc);
-                } else {
-                    acc = __builtin_fmaf(x[j][c], w[c][j], acc);
+            for (int j = 0; j < kTaps - 1; ++j)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) x[j][c] = x[j + 1][c];
+            Raw4<T>::unpack(rows[tt + kTaps - 1], x[kTaps - 1]);
+            const int64_t t = t0 + tt;
+            uint32_t s = 0;  // position of t in its sequence (masked tiles only)
+            if constexpr (decltype(masked)::value)
+                s = t < a.tokens ? (uint32_t)t - fastdiv((uint32_t)t, a.seq) * a.seq.d : 0u;
+            float m[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                // tap j multiplies row t - (kTaps-1) + j; fused multiply-add per tap
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kTaps; ++j) {
+                    if constexpr (decltype(masked)::value) {
+                        if (s >= (uint32_t)(kTaps - 1 - j)) acc = __builtin_fmaf(x[j][c], w[c][j], acc);
+                    } else {
+                        acc = __builtin_fmaf(x[j][c], w[c][j], acc);
+                    }
                 }
+                m[c] = silu(acc);
             }
-            m[c] = silu(acc);
-        }
-        float ss = 0.0f;
+            if (is_qk) {  // L2 norm over the key head (an aligned group of LPH lanes)
+                float ss = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) ss = __builtin_fmaf(m[c], m[c], ss);
-        ss = group_sum<LPH>(ss);  // whole aligned head groups: q/k rows only use it
-        if (live && tok) {
-            float *dst;
-            if (is_q || is_k) {
-                const float scale = is_q ? 1.0f / (__builtin_sqrtf(ss + 1e-6f) * a.sqrt_kd)
-                                         : 1.0f / __builtin_sqrtf(ss + 1e-6f);
+                for (int c = 0; c < 4; ++c) ss = __builtin_fmaf(m[c], m[c], ss);
+                ss = group_sum<LPH>(ss);
+                // 1/(sqrt(ss + 1e-6) sqrt(kd)) for q, 1/sqrt(ss + 1e-6) for k, each
+                // factor within an ulp or two of the correctly rounded one
+                const float scale = __builtin_amdgcn_rsqf(ss + 1e-6f) * qk_mul;
 #pragma unroll
                 for (int c = 0; c < 4; ++c) m[c] = m[c] * scale;
-                dst = is_q ? a.q + t * kw + c0 : a.k + t * kw + (c0 - kw);
-            } else {
-                dst = a.v + t * vw + (c0 - 2 * kw);
             }
-            store_chunk(dst, m);
+            if (live && t < a.tokens) store_chunk(out, m);
         }
     };
-    if (!inner_start) {
-#pragma unroll
-        for (int tt = 0; tt < kTileT; ++tt) token(tt, std::false_type{});
-    } else {
-#pragma unroll
-        for (int tt = 0; tt < kTileT; ++tt) token(tt, std::true_type{});
-    }
+    if (!inner_start) run_tile(std::false_type{});
+    else run_tile(std::true_type{});
 }
 
 // One wavefront per (token, segment); segments: q heads, k heads, the v block, the gates.
@@ -313,6 +321,7 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
     p.qk_chunks = (int)(2 * kw / 4);
     // sqrt(Float32(key_dim)) of src/backbone.jl:313 / src/backbone_cpu.jl:516
     p.sqrt_kd = std::sqrt((float)key_dim);
+    p.inv_sqrt_kd = 1.0f / p.sqrt_kd;
     // 4-channel pieces: 8-byte (bf16) or 16-byte (fp32) aligned projection rows
     const bool fast = ((uintptr_t)proj % (4 * es)) == 0 && (ld * es) % (4 * es) == 0 &&
                       aligned16(q) && aligned16(k) && aligned16(v) && cq % 4 == 0;
