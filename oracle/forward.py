@@ -178,6 +178,17 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
     return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
 
 
+def normalize_heads(x, multiplier):
+    """L2-normalise the last axis, ``x * inv(sqrt(sum(x^2) + 1e-6) * multiplier)``
+    in fp32: the loop form of ``cpu_normalize_delta_heads!``
+    (``src/backbone_cpu.jl:411-427``), also the AMDGPU ``qk_normalize_kernel!``
+    scale (``ext/amdgpu_delta.jl:1-33``)."""
+    x = np.asarray(x, dtype=F32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        squared = (x * x).sum(-1, keepdims=True, dtype=F32)
+        return (x * (F32(1) / (np.sqrt(squared + F32(1e-6)) * F32(multiplier)))).astype(F32)
+
+
 def delta_prologue(qkv, conv, a_raw, b_raw, a_decay, dt_bias, kh, kd, vh, vd):
     """Causal conv + SiLU of the qkv projection, q/k L2 normalisation and the
     gates, for one sequence (``cpu_delta_prepare``, ``src/backbone_cpu.jl:465-499``;
@@ -190,9 +201,8 @@ def delta_prologue(qkv, conv, a_raw, b_raw, a_decay, dt_bias, kh, kd, vh, vd):
     q = mixed[:, :kw].reshape(T, kh, kd)
     k = mixed[:, kw:2 * kw].reshape(T, kh, kd)
     v = mixed[:, 2 * kw:].reshape(T, vh, vd)
-    q = (q * (F32(1) / (np.sqrt((q * q).sum(-1, keepdims=True) + F32(1e-6))
-                        * np.sqrt(F32(kd))))).astype(F32)
-    k = (k * (F32(1) / np.sqrt((k * k).sum(-1, keepdims=True) + F32(1e-6)))).astype(F32)
+    q = normalize_heads(q, np.sqrt(F32(kd)))
+    k = normalize_heads(k, F32(1))
     beta = _sigmoid(b_raw)
     decay = (a_decay * _softplus(a_raw + dt_bias)).astype(F32)
     return q, k, np.ascontiguousarray(v), beta, decay

@@ -393,6 +393,45 @@ def test_delta_prologue(dtype, case):
         report(f"prologue {name} {case} {dtype}", g, e, torch.float32)
 
 
+def _same_bits_or_nan(a, b):
+    """Julia isequal on fp32 arrays: NaN equals NaN, -0 differs from +0."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | ((a.view(np.uint32) == b.view(np.uint32)) & ~np.isnan(a))))
+
+
+@pytest.mark.parametrize("KH,kd,H,vd,pad", [(1, 8, 1, 8, 2),    # fast kernel
+                                            (1, 6, 1, 6, 0)])   # general kernel
+def test_delta_prologue_special_values(KH, kd, H, vd, pad):
+    """The q/k normalisation special values of test/backbone.jl:303-312 (0, -0,
+    NaN, Inf, floatmax and the smallest denormal) through the prologue: every
+    token its own sequence and the convolution the current-row tap, so each head
+    sees silu(x) with x the special value (2^-148 becomes 2^-149)."""
+    from oracle import forward
+    from qdc_amd import ops
+    kw, vw = KH * kd, H * vd
+    cq = 2 * kw + vw
+    width = cq + vw + 2 * H
+    specials = [0.0, -0.0, np.nan, np.inf, float(np.finfo(np.float32).max), 2.0 ** -148]
+    T = len(specials)
+    proj = np.zeros((T, width + pad), np.float32)
+    proj[:, :cq] = np.array(specials, np.float32)[:, None]
+    conv = np.zeros((cq, 4), np.float32)
+    conv[:, 3] = 1.0
+    a_decay = np.full((H,), -1.0, np.float32)
+    dt_bias = np.zeros((H,), np.float32)
+    got = [back(t) for t in ops.delta_prologue(dev(proj, torch.float32)[:, :width],
+                                               dev(conv, torch.float32),
+                                               dev(a_decay, torch.float32),
+                                               dev(dt_bias, torch.float32), 1, KH, kd, H, vd)]
+    for t in range(T):
+        row = proj[t:t + 1]
+        exp = forward.delta_prologue(row[:, :cq], conv, row[:, cq + vw:cq + vw + H],
+                                     row[:, cq + vw + H:width], a_decay, dt_bias, KH, kd, H, vd)
+        for name, g, e in zip(("q", "k", "v"), got[:3], exp[:3]):
+            assert _same_bits_or_nan(g[t], e[0]), (name, specials[t], g[t], e[0])
+
+
 # ------------------------------------------------ attention row work ---------
 # (B, H, Q, K, q_offset, mask kind): "rand" = 30% of keys masked, "none" = no mask,
 # "dead" = some sequences whose first keys are all masked (rows with no visible key)

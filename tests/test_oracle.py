@@ -9,6 +9,8 @@ Checks, per oracle function:
     RoPE (rotary 16 of 64 and 64 of 256, positions reset per sequence), the
     norms, SwiGLU with special values and a 2-layer backbone;
   * the bf16 known-answer tests of test/safetensors.jl:23-25;
+  * the reference's q/k normalisation cases (sine ramps, special values:
+    test/backbone.jl:290-312);
   * closed forms and invariants (exact scale invariance, identity rotations,
     pair-norm preservation, silu(x) - silu(-x) = x, byte-equal gathers);
   * planted mistakes: each mutant of the oracle must fail the fixture.
@@ -184,6 +186,41 @@ def test_rms_closed_forms():
             w = ramp(np.cos, (width,))
             np.testing.assert_allclose(O.rms(x, w, 1e-6), _np_rms(x, w, 1e-6, True), rtol=3e-6,
                                        atol=1e-7)
+
+
+# the special values of test/backbone.jl:303-312 (fp32 denormal included)
+NORM_SPECIALS = [0.0, -0.0, np.nan, np.inf, float(np.finfo(np.float32).max),
+                 float(np.nextafter(np.float32(0), np.float32(1)))]
+
+
+def _same_bits_or_nan(a, b):
+    """Julia isequal on fp32 arrays: NaN equals NaN, -0 differs from +0."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | ((a.view(np.uint32) == b.view(np.uint32)) & ~np.isnan(a))))
+
+
+def test_normalize_heads_reference_cases():
+    """The DeltaNet q/k normalisation against test/backbone.jl:290-312: sine
+    ramps over widths 1/7/16/128, 1 or 3 heads, n = 0/1/65 and both multipliers
+    against the division form at 2e-6, and special values that must match it
+    exactly (Julia isequal)."""
+    F32 = np.float32
+    for width in (1, 7, 16, 128):
+        for heads in (1, 3):
+            for n in (0, 1, 65):
+                for mult in (F32(1), np.sqrt(F32(width))):
+                    x = np.sin(np.arange(1, width * heads * n + 1, dtype=F32)).astype(F32)
+                    x = x.reshape(n, heads, width)  # column-major (width, heads, n)
+                    exp = x / (np.sqrt((x * x).sum(-1, keepdims=True) + F32(1e-6)) * mult)
+                    np.testing.assert_allclose(forward.normalize_heads(x, mult), exp,
+                                               atol=2e-6, rtol=2e-6)
+    for v in NORM_SPECIALS:
+        x = np.full((3, 2, 8), v, np.float32)
+        with np.errstate(over="ignore", invalid="ignore"):
+            exp = (x / np.sqrt((x * x).sum(-1, keepdims=True, dtype=np.float32)
+                               + np.float32(1e-6))).astype(np.float32)
+        assert _same_bits_or_nan(forward.normalize_heads(x, np.float32(1)), exp), v
 
 
 def test_rope_closed_forms():
