@@ -19,6 +19,10 @@
  *    when the launch itself failed.
  *  - Unaligned pointers/strides or unusual widths are accepted and take a
  *    slower general kernel; the fast kernels need 16-byte alignment.
+ *  - Size limits (QDC_ERR_SHAPE beyond them) keep every launch grid below 2^32
+ *    work-items: fewer than 2^26 rows for the RMSNorm entry points (tokens *
+ *    heads for the gated norm), q rows + k rows for qdc_qk_norm_rope, ids for
+ *    the gather, score rows for the softmax and tokens for the DeltaNet prologue.
  */
 #ifndef QDC_HIP_H
 #define QDC_HIP_H

@@ -241,11 +241,13 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_general(Prologue a) {
 template <typename T>
 int32_t launch(const Prologue &p, bool fast, hipStream_t stream) {
     const int lph = p.kd / 4;
+    const int64_t fast_blocks = ceil_div(p.tokens, tile_for<T>()) * (ceil_div(p.chunks, kBlock) + 1);
+    // the fast grid is one-dimensional: fewer than 2^32 work-items
     if (fast && p.kd % 4 == 0 && p.vd % 4 == 0 && p.taps == kTaps && lph <= kWave &&
-        (lph & (lph - 1)) == 0) {
+        (lph & (lph - 1)) == 0 && fast_blocks * kBlock < ((int64_t)1 << 32)) {
         Prologue q = p;
         q.blocks_per_tile = (uint32_t)ceil_div(p.chunks, kBlock) + 1;
-        const dim3 grid((uint32_t)(ceil_div(p.tokens, tile_for<T>()) * q.blocks_per_tile));
+        const dim3 grid((uint32_t)fast_blocks);
 #define QDC_PRO(L)                                                                               \
     case L:                                                                                      \
         hipLaunchKernelGGL((delta_prologue_fast<T, L>), grid, dim3(kBlock), 0, stream, q);     \

@@ -16,8 +16,8 @@
 // first dependent instruction; streamed inputs use nontemporal loads.  The row
 // stays in registers: HBM sees each input byte read once and each output byte
 // written once.  The sum of squares is reduced across the LPR lanes (DPP inside
-// 16-lane rows, LDS-crossbar permutes across them); 64/LPR rows share a
-// wavefront, 4 wavefronts a workgroup.
+// 16-lane rows, lane swaps across them); 64/LPR rows share a wavefront, 4
+// wavefronts a workgroup.
 //
 // General path (any width, stride or alignment): one wavefront per row, scalar
 // strided accesses, two passes over the row (the second from cache).
@@ -227,8 +227,9 @@ int32_t run(const Args &a, hipStream_t stream) {
     return launch_status();
 }
 
-// Rows are addressed with 32-bit row indices in the kernels.
-constexpr int64_t kMaxRows = (int64_t)1 << 31;
+// A row takes up to 64 lanes (the general kernel one wavefront) and a grid
+// holds fewer than 2^32 work-items, so rows < 2^26.
+constexpr int64_t kMaxRows = (int64_t)1 << 26;
 
 bool all16(std::initializer_list<const void *> ptrs) {
     for (const void *p : ptrs)

@@ -264,8 +264,9 @@ extern "C" int32_t qdc_qk_norm_rope(void *q_out, void *k_out, const void *q_in, 
         rotary_dim % 2 || rotary_dim > head_dim || seq_len <= 0 || pos_offset < 0 ||
         table_len < 0)
         return QDC_ERR_SHAPE;
+    // up to a wavefront per (token, head) row in a grid of fewer than 2^32 work-items
     if (head_dim > INT32_MAX || seq_len >= ((int64_t)1 << 31) ||
-        tokens * heads >= ((int64_t)1 << 31) || tokens * kv_heads >= ((int64_t)1 << 31))
+        tokens * (heads + kv_heads) >= ((int64_t)1 << 26))
         return QDC_ERR_SHAPE;
     if (tokens == 0 || (heads == 0 && kv_heads == 0)) return QDC_OK;
     if (heads > 0 && (!q_out || !q_in || !q_norm)) return QDC_ERR_NULL;

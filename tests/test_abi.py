@@ -79,6 +79,8 @@ def test_rmsnorm_validation():
     assert rms(FAKE + 16, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32, F32) == -5  # partial overlap
     assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 16, 1e-6, 1, F32, F32) == -5  # in place, other stride
     assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32, BF16) == -5  # in place, other type
+    # up to a wavefront per row in a grid of fewer than 2^32 work-items: rows < 2^26
+    assert rms(FAKE, FAKE * 2, FAKE, 1 << 26, 8, 8, 8, 1e-6, 1, F32, F32) == -2
 
 
 def test_residual_validation():
@@ -93,6 +95,7 @@ def test_residual_validation():
     assert f(A, B, A + 4, D, W, 4, 8, 1e-6, F32, F32, F32) == -5  # residual overlaps x partially
     assert f(A, B, C, B, W, 4, 8, 1e-6, F32, BF16, F32) == -5  # out on mixed of another type
     assert f(A, B, C, D, W, 0, 8, 1e-6, F32, F32, F32) == 0
+    assert f(A, B, C, D, W, 1 << 26, 8, 1e-6, F32, F32, F32) == -2  # rows < 2^26
 
 
 def test_gated_validation():
@@ -104,6 +107,7 @@ def test_gated_validation():
     assert f(A, X, None, W, 4, 2, 8, 16, 16, 16, 1e-6, F32) == -1
     assert f(Z, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, F32) == -5  # out on z
     assert f(A, X, Z, W, 0, 2, 8, 16, 16, 16, 1e-6, F32) == 0
+    assert f(A, X, Z, W, 1 << 25, 2, 8, 16, 16, 16, 1e-6, F32) == -2  # tokens * heads < 2^26
 
 
 def test_swiglu_validation():
@@ -150,6 +154,8 @@ def test_qk_norm_rope_validation():
     assert f(q=KI) == -5  # q output on the k input
     assert f(k=Q + 32) == -5  # the two outputs overlap
     assert f(tokens=0) == 0
+    # q rows + k rows < 2^26 (up to a wavefront per row, fewer than 2^32 work-items)
+    assert f(tokens=1 << 24, kv=2, ks=(32, 16, 32, 16)) == -2
 
 
 def test_delta_scan_validation():
