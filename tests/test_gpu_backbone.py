@@ -217,6 +217,49 @@ def test_full_depth_qwen35_backbone(dtype):
     assert err32 <= max(1e-2, 1.25 * drift)
 
 
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_full_size_forward_causal_prefix(dtype):
+    """The benchmark workload at full size -- the 24-layer Qwen3.5-0.8B-like
+    backbone over 8 sequences of 2048 tokens -- checked through properties that
+    hold at any size: attention and DeltaNet are causal, so the first 64
+    positions of each sequence depend only on its first 64 tokens and must match
+    the oracle's forward of those 64 tokens (fp32 within 1e-5; bf16 against the
+    full-depth bar); and two forwards are bitwise identical."""
+    from qdc_amd import backbone
+    from qdc_amd.config import qwen35_08b_config
+    from qdc_amd.weights import random_weights
+    cfg = qwen35_08b_config()
+    weights = random_weights(cfg, seed=31)
+    if dtype == torch.bfloat16:
+        weights = bf16_weights(weights)
+    model = model_for(weights, cfg, dtype)
+    B, S, P = 8, 2048, 64
+    ids = np.random.default_rng(32).integers(0, cfg.vocab, size=(B, S))
+    d_ids = torch.from_numpy(ids.astype(np.int32)).cuda()
+    first = backbone.batch_backbone_hidden(model, d_ids, None)
+    again = backbone.batch_backbone_hidden(model, d_ids, None)
+    assert torch.equal(first, again)
+    prefixes = first[:, :P].float().cpu().numpy()
+    del model, first, again
+    torch.cuda.empty_cache()
+    assert np.isfinite(prefixes).all()
+    for r in (0, B - 1):
+        full = np.ones(P, np.int64)
+        exp32 = forward.backbone_hidden(weights, cfg.as_dict(), ids[r, :P], full)
+        err32 = normwise(prefixes[r], exp32)
+        if dtype == torch.float32:
+            print(f"full-size fp32, sequence {r}: first {P} positions vs oracle {err32:.2e}",
+                  flush=True)
+            assert err32 <= 1e-5
+            continue
+        drift = normwise(forward.backbone_hidden(weights, cfg.as_dict(), ids[r, :P], full,
+                                                 bf16=True), exp32)
+        print(f"full-size bf16, sequence {r}: first {P} positions vs fp32 oracle {err32:.2e} "
+              f"(bf16-storage oracle drift {drift:.2e})", flush=True)
+        assert err32 <= max(1e-2, 1.25 * drift)
+
+
 def test_bf16_checkpoint_directory(native_fixture, tmp_path):
     """QwenBackbone(dir) on a BF16 safetensors checkpoint: loaded onto the GPU in
     bf16 (no widening) and packed there; the forward equals the in-memory build of
