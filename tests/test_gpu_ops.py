@@ -344,6 +344,36 @@ def test_delta_scan(out_dtype, B, S, KH, H, kd, vd, dscale):
     report(f"delta scan {B}x{S} kh{KH} h{H} kd{kd} vd{vd} decay*{dscale}", got, exp, out_dtype)
 
 
+@pytest.mark.parametrize("B,S,KH,H,kd,vd", [(2, 50, 2, 4, 128, 128), (1, 300, 1, 1, 64, 32)])
+def test_delta_scan_chunked_matches_recurrent(B, S, KH, H, kd, vd):
+    """The two forms of the recurrence agree, as the reference checks its chunked
+    and recurrent DeltaNet paths (test/backbone.jl:162-185): the same values go
+    through the matrix-core chunked kernel (aligned inputs) and the token
+    recurrence (q shifted by one element, so not 16-byte aligned)."""
+    from oracle import forward
+    from qdc_amd import ops
+    rng = np.random.default_rng(33)
+    q = rng.standard_normal((B, S, KH, kd), dtype=np.float32)
+    k = rng.standard_normal((B, S, KH, kd), dtype=np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True) * np.float32(np.sqrt(kd))
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((B, S, H, vd), dtype=np.float32)
+    beta = rng.random((B, S, H), dtype=np.float32)
+    decay = -rng.random((B, S, H), dtype=np.float32) * np.float32(2.0)
+    args = [dev(a, torch.float32) for a in (q, k, v, beta, decay)]
+    chunked = back(ops.delta_scan(*args))
+    shifted = torch.empty(q.size + 1, dtype=torch.float32, device=DEV)
+    shifted[1:] = args[0].reshape(-1)
+    q_off = shifted[1:].view(q.shape)
+    assert q_off.data_ptr() % 16 != 0
+    recurrent = back(ops.delta_scan(q_off, *args[1:]))
+    exp = np.stack([forward.delta_recurrence(q[b], k[b], v[b], beta[b], decay[b])
+                    for b in range(B)])
+    report(f"chunked {B}x{S} kd{kd}", chunked, exp, torch.float32)
+    report(f"recurrent {B}x{S} kd{kd}", recurrent, exp, torch.float32)
+    assert normwise(chunked, recurrent) <= 2e-6
+
+
 # ------------------------------------------------ DeltaNet prologue ----------
 # (B, S, KH, kd, H, vd, taps, pad): pad > 0 widens the row stride by pad elements
 PROLOGUE_CASES = [
