@@ -134,21 +134,24 @@ __global__ __launch_bounds__(kBlock) void rms_rows_general(
     const int64_t xo = (int64_t)t * map.x_tok + (int64_t)h * map.x_head;
     const int64_t zo = (int64_t)t * map.z_tok + (int64_t)h * map.z_head;
     const int64_t oo = (int64_t)t * map.o_tok + (int64_t)h * map.o_head;
+    // The first pass only reads; the second recomputes x + mixed in fp32 (the
+    // normalised output uses the unrounded sum, as the fast kernel does) and
+    // then writes.  Element i is read before it is written, and only by this
+    // lane, so the residual or the output may overwrite x or mixed in place.
     float ss = 0.0f;
+    for (int64_t i = lane; i < width; i += kWave) {
+        float v = to_f32(x[xo + i]);
+        if constexpr (M == Mode::kResidual) v = v + to_f32(mixed[xo + i]);
+        ss += v * v;
+    }
+    ss = group_sum<kWave>(ss);
+    const float s = rms_scale(ss, (float)width, eps);
     for (int64_t i = lane; i < width; i += kWave) {
         float v = to_f32(x[xo + i]);
         if constexpr (M == Mode::kResidual) {
             v = v + to_f32(mixed[xo + i]);
             res_out[oo + i] = from_f32<TX>(v);
         }
-        ss += v * v;
-    }
-    ss = group_sum<kWave>(ss);
-    const float s = rms_scale(ss, (float)width, eps);
-    for (int64_t i = lane; i < width; i += kWave) {
-        // the residual may overwrite x or mixed in place: read back what this
-        // lane stored in the first pass
-        const float v = M == Mode::kResidual ? to_f32(res_out[oo + i]) : to_f32(x[xo + i]);
         const float wv = to_f32(w[i]);
         float o;
         if constexpr (M == Mode::kGated) {

@@ -316,6 +316,75 @@ def test_residual_rmsnorm_fp32_stream(mixed_dtype, out_dtype, rows, width):
     report(f"residual f32+bf16 -> {out_dtype} {rows}x{width}", back(out), exp_out, out_dtype)
 
 
+# ------------------------------------------- fast and general kernels ------
+def _shifted(t):
+    """The same values starting one element past a 16-byte boundary (the
+    general kernels take them)."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    buf[1:] = t.reshape(-1)
+    out = buf[1:].view(t.shape)
+    assert out.data_ptr() % 16 != 0
+    return out
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("op", ["rms", "residual", "gated", "qk", "swiglu", "gather"])
+def test_fast_and_general_kernels_agree(dtype, op):
+    """Each in-scope op at its Qwen3.5-0.8B-like shape through both of its
+    kernels -- aligned inputs take the fast kernel, the same values one element
+    off a 16-byte boundary the general one -- as the reference checks each CPU
+    policy against the generic path (test/backbone.jl:36-75): both within the
+    op's bar of the oracle and close to each other (the gather bit for bit)."""
+    from qdc_amd import ops
+    if op == "rms":
+        x, w = host((8192, 1024), 51, 1.0, dtype), host((1024,), 52, 0.02, dtype)
+        run = lambda xt: ops.native_rms(xt, dev(w, dtype), 1e-6)  # noqa: E731
+        exp = O.rms(x, w, 1e-6)
+    elif op == "residual":
+        x, m = host((8192, 1024), 53, 1.0, dtype), host((8192, 1024), 54, 1.0, dtype)
+        w = host((1024,), 55, 0.02, dtype)
+        run = lambda xt: ops.native_residual_rms(xt, dev(m, dtype), dev(w, dtype), 1e-6)[1]  # noqa: E731
+        exp = O.residual_rms(x, m, w, 1e-6)[1]
+    elif op == "gated":
+        x, z = host((2048, 16, 128), 56, 1.0, dtype), host((2048, 16, 128), 57, 1.0, dtype)
+        w = host((128,), 58, 1.0, dtype)
+        run = lambda xt: ops.native_gated_rms(xt, dev(z, dtype), dev(w, dtype), 1e-6)  # noqa: E731
+        exp = O.gated_rms(x, z, w, 1e-6)
+    elif op == "qk":
+        T, H, KV, hd, rd, seq = 4096, 8, 2, 256, 64, 2048
+        x, kx = host((T, H, hd), 59, 1.0, dtype), host((T, KV, hd), 60, 1.0, dtype)
+        qn, kn = host((hd,), 61, 0.02, dtype), host((hd,), 62, 0.02, dtype)
+        tables = ops.rope_tables(seq, rd, 1e7, DEV)
+        kt = dev(kx, dtype)
+
+        def run(xt):
+            qo, ko = ops.prepare_heads(xt, kt, dev(qn, dtype), dev(kn, dtype), tables, rd, 1e-6,
+                                       seq_len=seq)
+            return torch.cat([qo.reshape(-1), ko.reshape(-1)])
+        cos, sin = O.rope_tables(seq, rd, 1e7)
+        exp = np.concatenate([O.qk_norm_rope(x, qn, cos, sin, rd, 1e-6, seq).reshape(-1),
+                              O.qk_norm_rope(kx, kn, cos, sin, rd, 1e-6, seq).reshape(-1)])
+    elif op == "swiglu":
+        x, u = host((4096, 3584), 63, 1.0, dtype), host((4096, 3584), 64, 1.0, dtype)
+        run = lambda xt: ops.native_mlp_gate(xt, dev(u, dtype))  # noqa: E731
+        exp = O.swiglu(x, u)
+    else:  # gather: the table is the aligned input; shift the output instead
+        table = host((4096, 1024), 65, 0.02, dtype)
+        ids = np.random.default_rng(66).integers(0, 4096, size=2048)
+        tt = dev(table, dtype)
+        fast = back(ops.native_gather(tt, ids))
+        general = _shifted(torch.zeros((2048, 1024), dtype=dtype, device=DEV))
+        ops.native_gather(tt, ids, out=general)
+        exp = table[ids]
+        assert np.array_equal(fast, exp) and np.array_equal(back(general), exp)
+        return
+    xt = dev(x, dtype)
+    fast, general = back(run(xt)), back(run(_shifted(xt)))
+    report(f"{op} fast kernel", fast, exp, dtype)
+    report(f"{op} general kernel", general, exp, dtype)
+    assert normwise(fast, general) <= (1e-6 if dtype == torch.float32 else 2e-3)
+
+
 # ------------------------------------------------ DeltaNet recurrence --------
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,S,KH,H,kd,vd,dscale", [
