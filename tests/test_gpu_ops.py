@@ -328,15 +328,50 @@ def _shifted(t):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("op", ["rms", "residual", "gated", "qk", "swiglu", "gather"])
+@pytest.mark.parametrize("op", ["rms", "residual", "gated", "qk", "swiglu", "gather",
+                                "prologue", "softmax", "gate"])
 def test_fast_and_general_kernels_agree(dtype, op):
-    """Each in-scope op at its Qwen3.5-0.8B-like shape through both of its
-    kernels -- aligned inputs take the fast kernel, the same values one element
-    off a 16-byte boundary the general one -- as the reference checks each CPU
-    policy against the generic path (test/backbone.jl:36-75): both within the
-    op's bar of the oracle and close to each other (the gather bit for bit)."""
+    """Each op at its Qwen3.5-0.8B-like shape through both of its kernels --
+    aligned inputs take the fast kernel, the same values one element off a
+    16-byte boundary the general one -- as the reference checks each CPU policy
+    against the generic path (test/backbone.jl:36-75): both within the op's bar
+    of the oracle and close to each other (the gather bit for bit)."""
+    from oracle import forward
     from qdc_amd import ops
-    if op == "rms":
+    bar = dtype  # tolerance class of the outputs
+    if op == "prologue":  # bf16 or fp32 projection -> fp32 q, k, v
+        B, S, KH, kd, H, vd = 2, 1024, 16, 128, 16, 128
+        kw, vw = KH * kd, H * vd
+        cq = 2 * kw + vw
+        width = cq + vw + 2 * H
+        x = host((B * S, width), 67, 1.0, dtype)
+        conv = host((cq, 4), 68, 0.5)
+        a_decay, dt_bias = -np.exp(host((H,), 69, 0.5)), host((H,), 70, 1.0)
+        dconv, da, dd = (dev(t, torch.float32) for t in (conv, a_decay, dt_bias))
+
+        def run(xt):
+            parts = ops.delta_prologue(xt, dconv, da, dd, S, KH, kd, H, vd)
+            return torch.cat([t.reshape(-1) for t in parts[:3]])
+        per = [forward.delta_prologue(r[:, :cq], conv, r[:, cq + vw:cq + vw + H],
+                                      r[:, cq + vw + H:width], a_decay, dt_bias, KH, kd, H, vd)
+               for r in (x[b * S:(b + 1) * S] for b in range(B))]
+        exp = np.concatenate([np.concatenate([p[i] for p in per]).reshape(-1) for i in range(3)])
+        bar = torch.float32
+    elif op == "softmax":
+        x, mask = _softmax_inputs((1, 8, 2048, 2048, 0, "rand"))
+        scale = float(1.0 / np.sqrt(np.float32(256)))
+        dmask = dev(mask, torch.int32)
+        run = lambda xt: ops.attention_softmax(xt, dmask, scale, out_dtype=dtype)  # noqa: E731
+        exp = forward.attention_softmax(x, mask, np.float32(scale))
+        x = x.astype(np.float32)
+    elif op == "gate":
+        B, S, H, hd = 1, 2048, 8, 256
+        x = host((B, H, S, hd), 71, 1.0)
+        qgate = host((B * S, H, 2 * hd), 72, 2.0, dtype)
+        gv = dev(qgate, dtype)[:, :, hd:]
+        run = lambda xt: ops.attention_gate(xt, gv, out_dtype=dtype)  # noqa: E731
+        exp = forward.attention_gate(x, qgate[:, :, hd:])
+    elif op == "rms":
         x, w = host((8192, 1024), 51, 1.0, dtype), host((1024,), 52, 0.02, dtype)
         run = lambda xt: ops.native_rms(xt, dev(w, dtype), 1e-6)  # noqa: E731
         exp = O.rms(x, w, 1e-6)
@@ -378,11 +413,11 @@ def test_fast_and_general_kernels_agree(dtype, op):
         exp = table[ids]
         assert np.array_equal(fast, exp) and np.array_equal(back(general), exp)
         return
-    xt = dev(x, dtype)
+    xt = dev(x, torch.float32 if op in ("softmax", "gate") else dtype)
     fast, general = back(run(xt)), back(run(_shifted(xt)))
-    report(f"{op} fast kernel", fast, exp, dtype)
-    report(f"{op} general kernel", general, exp, dtype)
-    assert normwise(fast, general) <= (1e-6 if dtype == torch.float32 else 2e-3)
+    report(f"{op} fast kernel", fast, exp, bar)
+    report(f"{op} general kernel", general, exp, bar)
+    assert normwise(fast, general) <= (1e-6 if bar == torch.float32 else 2e-3)
 
 
 # ------------------------------------------------ DeltaNet recurrence --------
