@@ -420,6 +420,69 @@ def test_fast_and_general_kernels_agree(dtype, op):
     assert normwise(fast, general) <= (1e-6 if bar == torch.float32 else 2e-3)
 
 
+def test_graph_replays_match_eager():
+    """A chain of the library's kernels (gather, RMSNorm, q/k norm + RoPE,
+    SwiGLU, gated norm, residual norm, DeltaNet prologue and scan, softmax, gate
+    merge) captured once in a HIP graph and replayed three times, with eager work
+    on other buffers in between: every replay equals the eager run bit for bit
+    (the kernels clear nothing with memset and keep no state between calls)."""
+    from qdc_amd import ops
+    dt = torch.bfloat16
+    r = lambda shape, seed, scale=1.0: dev(host(shape, seed, scale, dt), dt)  # noqa: E731
+    T, hidden, H, KV, hd, rd = 256, 1024, 8, 2, 256, 64
+    table, ids = r((512, hidden), 81, 0.02), torch.randint(0, 512, (T,), dtype=torch.int32,
+                                                             device=DEV)
+    w = r((hidden,), 82, 0.02)
+    qg, kx = r((T, H, 2 * hd), 83), r((T, KV, hd), 84)
+    qn, kn = r((hd,), 85, 0.02), r((hd,), 86, 0.02)
+    tables = ops.rope_tables(T, rd, 1e7, DEV)
+    gu = r((T, 2 * 3584), 87)
+    gx, gz, gw = r((T, 16, 128), 88), r((T, 16, 128), 89), r((128,), 90)
+    mixed = r((T, hidden), 91)
+    KH, kd, VH, vd = 16, 128, 16, 128
+    cq = 2 * KH * kd + VH * vd
+    proj = r((T, cq + VH * vd + 2 * VH), 92)
+    conv = dev(host((cq, 4), 93, 0.5), torch.float32)
+    a_dec = dev(-np.exp(host((VH,), 94, 0.5)), torch.float32)
+    dt_b = dev(host((VH,), 95, 1.0), torch.float32)
+    scores = dev(host((1, H, T, T), 96, 4.0), torch.float32)
+    values = dev(host((1, H, T, hd), 97, 1.0), torch.float32)
+
+    def chain():
+        h = ops.native_gather(table, ids, out_dtype=torch.float32)
+        n = ops.native_rms(h, w.float(), 1e-6)
+        qo, ko = ops.prepare_heads(qg[:, :, :hd], kx, qn, kn, tables, rd, 1e-6, seq_len=T)
+        a = ops.native_mlp_gate(gu[:, :3584], gu[:, 3584:])
+        g = ops.native_gated_rms(gx, gz, gw, 1e-6)
+        res, nr = ops.native_residual_rms(h, mixed, w, 1e-6)
+        q, k, v, beta, decay = ops.delta_prologue(proj, conv, a_dec, dt_b, T, KH, kd, VH, vd)
+        o = ops.delta_scan(q.view(1, T, KH, kd), k.view(1, T, KH, kd), v.view(1, T, VH, vd),
+                           beta.view(1, T, VH), decay.view(1, T, VH), dt)
+        p = ops.attention_softmax(scores, None, 0.0625, out_dtype=dt)
+        m = ops.attention_gate(values, qg[:, :, hd:], out_dtype=dt)
+        return [n, qo, ko, a, g, res, nr, o, p, m]
+
+    eager = [t.clone() for t in chain()]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        chain()  # warm up on the capture stream
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            outs = chain()
+    for rep in range(3):
+        for t in outs:
+            t.fill_(float("nan"))  # a replay must rewrite every output
+        graph.replay()
+        torch.cuda.synchronize()
+        other = chain()  # eager work between replays, on freshly allocated outputs
+        torch.cuda.synchronize()
+        for i, (got, exp) in enumerate(zip(outs, eager)):
+            assert torch.equal(got, exp), (rep, i)
+            assert torch.equal(other[i], exp), (rep, i)
+
+
 # ------------------------------------------------ DeltaNet recurrence --------
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,S,KH,H,kd,vd,dscale", [
