@@ -1,7 +1,8 @@
 /*
  * qdc_oracle.c -- CPU restatement of the reference CPU path for the fused row
- * kernels.  TEST INFRASTRUCTURE ONLY (see qdc_oracle.h): the checker for the
- * HIP library and the timed CPU baseline, never part of the product path.
+ * kernels.  TEST INFRASTRUCTURE ONLY (see qdc_oracle.h): the reference the HIP
+ * library is compared with and the timed CPU baseline, never part of the
+ * product path.
  *
  * Built with -ffp-contract=off so that every multiply and add rounds on its
  * own, as in the reference's Julia code (no FMA contraction there).  Row sums

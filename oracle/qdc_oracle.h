@@ -4,7 +4,7 @@
  * residual + RMSNorm, per-head q/k RMSNorm + partial RoPE, gated RMSNorm,
  * SwiGLU) and the bf16 <-> fp32 format.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker the GPU kernels are
+ * TEST INFRASTRUCTURE ONLY.  This library is what the GPU kernels are
  * compared against and the timed CPU baseline.  Only tests/, the smoke() entry
  * and bench.py's cpu_baseline leg may load it.  The product path (the HIP
  * library) never links or calls it.

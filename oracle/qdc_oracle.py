@@ -1,7 +1,7 @@
 """numpy front end of the CPU oracle (``oracle/liboracle.so``).
 
 TEST INFRASTRUCTURE ONLY.  These functions restate the reference's CPU path for
-the fused row kernels and are the checker the HIP library is compared with; only
+the fused row kernels and are what the HIP library is compared with; only
 ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
 call them.  Nothing in the product package imports this module.
 
