@@ -108,6 +108,32 @@ int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x, const voi
                              hipStream_t stream);
 
 /*
+ * qdc_rmsnorm and qdc_residual_rmsnorm with the DeltaNet input mask fused into
+ * the store: normalised row r is multiplied by (float)token_mask[r] in fp32
+ * before it is rounded to out_dtype; the residual output is not masked.
+ * token_mask is a device int32 vector of `rows` entries, 0 or 1 (the prepared
+ * mask of native_prepare_mask, ext/amdgpu_workspace.jl:151-155, validated on
+ * the host like the ids).  Replaces the separate `masked .= x .* mask` pass at
+ * the head of delta_attention (ext/amdgpu_delta.jl:130-133; generic
+ * src/backbone.jl:286): the norm producing a DeltaNet layer's input writes the
+ * masked rows directly, as the reference's fused masked normalisation does
+ * (residual_input_rms! and the first-layer fused_normalization,
+ * ext/metal_normalization.jl:369-432, with native_layer_outputs(...,
+ * Val(true)) skipping the multiply, src/backbone.jl:372-376).  Arguments and
+ * status otherwise as the unmasked entry points; token_mask may not overlap an
+ * output.
+ */
+int32_t qdc_rmsnorm_masked(void *out, const void *x, const void *weight,
+                           const int32_t *token_mask, int64_t rows, int64_t width, int64_t ld_x,
+                           int64_t ld_out, float eps, int32_t centered, int32_t x_dtype,
+                           int32_t out_dtype, hipStream_t stream);
+
+int32_t qdc_residual_rmsnorm_masked(void *residual, void *out, const void *x, const void *mixed,
+                                    const void *weight, const int32_t *token_mask, int64_t rows,
+                                    int64_t width, float eps, int32_t residual_dtype,
+                                    int32_t mixed_dtype, int32_t out_dtype, hipStream_t stream);
+
+/*
  * Per-head zero-centred RMSNorm fused with half-split partial RoPE, for the Q
  * heads and the K heads of full attention in one launch.
  * Replaces prepare_head_kernel! (ext/amdgpu_attention.jl:1-43, launches
@@ -215,7 +241,7 @@ int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta, float *dec
  * exp(value - max) / sum (fp32 or bf16, contiguous like scores; may equal
  * scores when fp32).  A row with no visible key gets 1/keys everywhere.
  * Replaces attention_softmax_kernel! (ext/amdgpu_attention.jl:61-88, launch
- * :150-156; generic mask and softmax src/backbone.jl:237-242, 252-254).
+ * :158-165; generic mask and softmax src/backbone.jl:237-242, 252-256).
  */
 int32_t qdc_attention_softmax(void *probs, int32_t probs_dtype, const float *scores,
                               const int32_t *mask, int64_t batch, int64_t heads,
@@ -227,8 +253,8 @@ int32_t qdc_attention_softmax(void *probs, int32_t probs_dtype, const float *sco
  * sigmoid(gate[t*gate_tok + h*gate_head + r]) for t = b*seq + s; values fp32
  * [batch, heads, seq, head_dim] contiguous (the PV GEMM output), gate and out
  * in gate_dtype / out_dtype with the given token and head strides (elements).
- * Replaces merge_gate_kernel! (ext/amdgpu_attention.jl:90-106, launch :159-166;
- * generic src/backbone.jl:256-258).
+ * Replaces merge_gate_kernel! (ext/amdgpu_attention.jl:90-106, launch :168-176;
+ * generic src/backbone.jl:258-259).
  */
 int32_t qdc_attention_gate(void *out, int32_t out_dtype, const float *values, const void *gate,
                            int32_t gate_dtype, int64_t batch, int64_t seq, int64_t heads,

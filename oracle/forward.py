@@ -97,7 +97,7 @@ def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, 
     k = _store(ops.qk_norm_rope(kp, W[p + "self_attn.k_norm.weight"], cos, sin, cfg["rotary_dim"],
                                 cfg["eps"]), bf16)
     v = _store(_linear(x, W[p + "self_attn.v_proj.weight"]), bf16).reshape(T, KV, hd)
-    # AMDGPU form (ext/amdgpu_attention.jl:148-166): scores of every head, the
+    # AMDGPU form (ext/amdgpu_attention.jl:148-176): scores of every head, the
     # masked softmax with scale inv(sqrt(dim)), the PV product, the gate merge;
     # kv head of query head h is h // (H // KV) (src/backbone.jl:249-251)
     groups = H // KV

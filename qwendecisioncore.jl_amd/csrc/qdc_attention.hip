@@ -18,7 +18,7 @@
 // streams the row three times (max, sum, write).
 //
 // Gate merge (merge_gate_kernel!, ext/amdgpu_attention.jl:90-106; generic
-// src/backbone.jl:256-258): out[t, h*dim + r] = values[b, h, s, r] *
+// src/backbone.jl:258-259): out[t, h*dim + r] = values[b, h, s, r] *
 // sigmoid(gate[t, h, r]) with t = b*seq + s, reading the PV GEMM output in its
 // head-major layout and the gate straight out of the q||gate projection.
 #include <cfloat>

@@ -21,6 +21,11 @@
 //
 // General path (any width, stride or alignment): one wavefront per row, scalar
 // strided accesses, two passes over the row (the second from cache).
+//
+// Optional row mask (plain and residual modes): out row r is multiplied by
+// keep[r], an int32 0/1, in fp32 before the store, as the reference's masked
+// normalisation store does (ext/metal_normalization.jl:20-28).  The residual
+// output is never masked.
 #include <initializer_list>
 
 #include "qdc_common.hpp"
@@ -45,7 +50,8 @@ template <typename TX, typename TM, typename TO> constexpr int group_elems() {
 template <typename TX, typename TM, typename TO, int LPR, int CPL, Mode M, bool CENTERED>
 __global__ __launch_bounds__(kBlock) void rms_rows_fast(
     TO *out, TX *res_out, const TX *x, const TM *mixed, const TO *__restrict__ z,
-    const TO *__restrict__ w, int64_t rows, RowMap map, float width, float eps) {
+    const TO *__restrict__ w, const int32_t *__restrict__ keep, int64_t rows, RowMap map,
+    float width, float eps) {
     constexpr int V = group_elems<TX, TM, TO>();
     constexpr int RPB = kBlock / LPR;  // rows per workgroup
     const int lane = threadIdx.x % LPR;
@@ -81,6 +87,8 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
 #pragma unroll
         for (int c = 0; c < CPL; ++c) wr[c] = load_frag<TO, V>(w + (c * LPR + lane) * V);
     }
+    int32_t keep_row = 1;
+    if (active && keep) keep_row = keep[row];
 
     float v[CPL][V];
     float ss = 0.0f;
@@ -116,6 +124,10 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
 #pragma unroll
             for (int j = 0; j < V; ++j)
                 o[j] = (v[c][j] * s) * (CENTERED ? (1.0f + wv[j]) : wv[j]);
+            if (keep) {
+#pragma unroll
+                for (int j = 0; j < V; ++j) o[j] = o[j] * (float)keep_row;
+            }
         }
         store_frag(out + oo + (c * LPR + lane) * V, o);
     }
@@ -125,7 +137,8 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
 template <typename TX, typename TM, typename TO, Mode M, bool CENTERED>
 __global__ __launch_bounds__(kBlock) void rms_rows_general(
     TO *out, TX *res_out, const TX *x, const TM *mixed, const TO *__restrict__ z,
-    const TO *__restrict__ w, int64_t rows, RowMap map, int64_t width, float eps) {
+    const TO *__restrict__ w, const int32_t *__restrict__ keep, int64_t rows, RowMap map,
+    int64_t width, float eps) {
     const int lane = threadIdx.x % kWave;
     const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
     if (row >= rows) return;  // uniform per wavefront
@@ -138,6 +151,7 @@ __global__ __launch_bounds__(kBlock) void rms_rows_general(
     // normalised output uses the unrounded sum, as the fast kernel does) and
     // then writes.  Element i is read before it is written, and only by this
     // lane, so the residual or the output may overwrite x or mixed in place.
+    const float keep_row = keep ? (float)keep[row] : 1.0f;
     float ss = 0.0f;
     for (int64_t i = lane; i < width; i += kWave) {
         float v = to_f32(x[xo + i]);
@@ -158,6 +172,7 @@ __global__ __launch_bounds__(kBlock) void rms_rows_general(
             o = ((v * s) * wv) * silu(to_f32(z[zo + i]));
         } else {
             o = (v * s) * (CENTERED ? (1.0f + wv) : wv);
+            if (keep) o = o * keep_row;
         }
         out[oo + i] = from_f32<TO>(o);
     }
@@ -170,6 +185,7 @@ struct Args {
     RowMap map;
     float eps;
     bool fast;
+    const int32_t *keep = nullptr;  // per-row output mask (plain and residual modes)
 };
 
 template <typename TX, typename TM, typename TO, int LPR, int CPL, Mode M, bool C>
@@ -177,8 +193,8 @@ int32_t launch_fast(const Args &a, hipStream_t stream) {
     const int64_t blocks = ceil_div(a.rows, kBlock / LPR);
     hipLaunchKernelGGL((rms_rows_fast<TX, TM, TO, LPR, CPL, M, C>), dim3((uint32_t)blocks),
                        dim3(kBlock), 0, stream, (TO *)a.out, (TX *)a.res, (const TX *)a.x,
-                       (const TM *)a.mixed, (const TO *)a.z, (const TO *)a.w, a.rows, a.map,
-                       (float)a.width, a.eps);
+                       (const TM *)a.mixed, (const TO *)a.z, (const TO *)a.w, a.keep, a.rows,
+                       a.map, (float)a.width, a.eps);
     return launch_status();
 }
 
@@ -226,7 +242,7 @@ int32_t run(const Args &a, hipStream_t stream) {
     const int64_t blocks = ceil_div(a.rows, kBlock / kWave);
     hipLaunchKernelGGL((rms_rows_general<TX, TM, TO, M, C>), dim3((uint32_t)blocks), dim3(kBlock),
                        0, stream, (TO *)a.out, (TX *)a.res, (const TX *)a.x, (const TM *)a.mixed,
-                       (const TO *)a.z, (const TO *)a.w, a.rows, a.map, a.width, a.eps);
+                       (const TO *)a.z, (const TO *)a.w, a.keep, a.rows, a.map, a.width, a.eps);
     return launch_status();
 }
 
@@ -240,20 +256,15 @@ bool all16(std::initializer_list<const void *> ptrs) {
     return true;
 }
 
-}  // namespace
-}  // namespace qdc
-
-using namespace qdc;
-
-extern "C" int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows,
-                               int64_t width, int64_t ld_x, int64_t ld_out, float eps,
-                               int32_t centered, int32_t x_dtype, int32_t out_dtype,
-                               hipStream_t stream) {
+// Shared by the plain and the masked entry points; `masked` requires keep.
+int32_t rmsnorm(void *out, const void *x, const void *weight, const int32_t *keep, bool masked,
+                int64_t rows, int64_t width, int64_t ld_x, int64_t ld_out, float eps,
+                int32_t centered, int32_t x_dtype, int32_t out_dtype, hipStream_t stream) {
     if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return QDC_ERR_DTYPE;
     if (x_dtype == QDC_BF16 && out_dtype == QDC_F32) return QDC_ERR_DTYPE;
     if (rows < 0 || width < 0 || rows >= kMaxRows) return QDC_ERR_SHAPE;
     if (rows == 0 || width == 0) return QDC_OK;
-    if (!out || !x || !weight) return QDC_ERR_NULL;
+    if (!out || !x || !weight || (masked && !keep)) return QDC_ERR_NULL;
     if (ld_x < width || ld_out < width) return QDC_ERR_SHAPE;
     const int64_t ex = elem_size(x_dtype), eo = elem_size(out_dtype);
     const int64_t span_x = ((rows - 1) * ld_x + width) * ex;
@@ -261,9 +272,12 @@ extern "C" int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int
     // in place: the same buffer, element type and stride
     if (out == x ? (ld_out != ld_x || ex != eo) : overlaps(out, span_o, x, span_x))
         return QDC_ERR_ALIAS;
-    const Args a{out, nullptr, x, nullptr, nullptr, weight, rows, width,
-                 RowMap{make_fastdiv(1), ld_x, 0, 0, 0, ld_out, 0}, eps,
-                 all16({out, x, weight}) && (ld_x * ex) % 16 == 0 && (ld_out * eo) % 16 == 0};
+    if (masked && overlaps(out, span_o, keep, rows * (int64_t)sizeof(int32_t)))
+        return QDC_ERR_ALIAS;
+    Args a{out, nullptr, x, nullptr, nullptr, weight, rows, width,
+           RowMap{make_fastdiv(1), ld_x, 0, 0, 0, ld_out, 0}, eps,
+           all16({out, x, weight}) && (ld_x * ex) % 16 == 0 && (ld_out * eo) % 16 == 0};
+    a.keep = masked ? keep : nullptr;
     if (centered) {
         if (x_dtype == QDC_BF16) return run<bf16_t, bf16_t, bf16_t, Mode::kPlain, true>(a, stream);
         if (out_dtype == QDC_BF16) return run<float, float, bf16_t, Mode::kPlain, true>(a, stream);
@@ -274,11 +288,11 @@ extern "C" int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int
     return run<float, float, float, Mode::kPlain, false>(a, stream);
 }
 
-extern "C" int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x,
-                                        const void *mixed, const void *weight, int64_t rows,
-                                        int64_t width, float eps, int32_t residual_dtype,
-                                        int32_t mixed_dtype, int32_t out_dtype,
-                                        hipStream_t stream) {
+// Shared by the plain and the masked entry points; `masked` requires keep.
+int32_t residual_rmsnorm(void *residual, void *out, const void *x, const void *mixed,
+                         const void *weight, const int32_t *keep, bool masked, int64_t rows,
+                         int64_t width, float eps, int32_t residual_dtype, int32_t mixed_dtype,
+                         int32_t out_dtype, hipStream_t stream) {
     if (!valid_dtype(residual_dtype) || !valid_dtype(mixed_dtype) || !valid_dtype(out_dtype))
         return QDC_ERR_DTYPE;
     const bool all_f32 =
@@ -290,7 +304,7 @@ extern "C" int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x
     if (!all_bf16 && !f32_stream) return QDC_ERR_DTYPE;
     if (rows < 0 || width < 0 || rows >= kMaxRows) return QDC_ERR_SHAPE;
     if (rows == 0 || width == 0) return QDC_OK;
-    if (!residual || !out || !x || !mixed || !weight) return QDC_ERR_NULL;
+    if (!residual || !out || !x || !mixed || !weight || (masked && !keep)) return QDC_ERR_NULL;
     const int64_t br = rows * width * elem_size(residual_dtype);
     const int64_t bm = rows * width * elem_size(mixed_dtype);
     const int64_t bo = rows * width * elem_size(out_dtype);
@@ -302,14 +316,58 @@ extern "C" int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x
     if (out == x ? out_dtype != residual_dtype : overlaps(out, bo, x, br)) return QDC_ERR_ALIAS;
     if (out == mixed ? out_dtype != mixed_dtype : overlaps(out, bo, mixed, bm))
         return QDC_ERR_ALIAS;
-    const Args a{out, residual, x, mixed, nullptr, weight, rows, width,
-                 RowMap{make_fastdiv(1), width, 0, 0, 0, width, 0}, eps,
-                 all16({residual, out, x, mixed, weight})};
+    const int64_t bk = rows * (int64_t)sizeof(int32_t);
+    if (masked && (overlaps(out, bo, keep, bk) || overlaps(residual, br, keep, bk)))
+        return QDC_ERR_ALIAS;
+    Args a{out, residual, x, mixed, nullptr, weight, rows, width,
+           RowMap{make_fastdiv(1), width, 0, 0, 0, width, 0}, eps,
+           all16({residual, out, x, mixed, weight})};
+    a.keep = masked ? keep : nullptr;
     if (all_f32) return run<float, float, float, Mode::kResidual, true>(a, stream);
     if (all_bf16) return run<bf16_t, bf16_t, bf16_t, Mode::kResidual, true>(a, stream);
     if (mixed_dtype == QDC_F32) return run<float, float, bf16_t, Mode::kResidual, true>(a, stream);
     if (out_dtype == QDC_BF16) return run<float, bf16_t, bf16_t, Mode::kResidual, true>(a, stream);
     return run<float, bf16_t, float, Mode::kResidual, true>(a, stream);
+}
+
+}  // namespace
+}  // namespace qdc
+
+using namespace qdc;
+
+extern "C" int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows,
+                               int64_t width, int64_t ld_x, int64_t ld_out, float eps,
+                               int32_t centered, int32_t x_dtype, int32_t out_dtype,
+                               hipStream_t stream) {
+    return rmsnorm(out, x, weight, nullptr, false, rows, width, ld_x, ld_out, eps, centered,
+                   x_dtype, out_dtype, stream);
+}
+
+extern "C" int32_t qdc_rmsnorm_masked(void *out, const void *x, const void *weight,
+                                      const int32_t *token_mask, int64_t rows, int64_t width,
+                                      int64_t ld_x, int64_t ld_out, float eps, int32_t centered,
+                                      int32_t x_dtype, int32_t out_dtype, hipStream_t stream) {
+    return rmsnorm(out, x, weight, token_mask, true, rows, width, ld_x, ld_out, eps, centered,
+                   x_dtype, out_dtype, stream);
+}
+
+extern "C" int32_t qdc_residual_rmsnorm(void *residual, void *out, const void *x,
+                                        const void *mixed, const void *weight, int64_t rows,
+                                        int64_t width, float eps, int32_t residual_dtype,
+                                        int32_t mixed_dtype, int32_t out_dtype,
+                                        hipStream_t stream) {
+    return residual_rmsnorm(residual, out, x, mixed, weight, nullptr, false, rows, width, eps,
+                            residual_dtype, mixed_dtype, out_dtype, stream);
+}
+
+extern "C" int32_t qdc_residual_rmsnorm_masked(void *residual, void *out, const void *x,
+                                               const void *mixed, const void *weight,
+                                               const int32_t *token_mask, int64_t rows,
+                                               int64_t width, float eps, int32_t residual_dtype,
+                                               int32_t mixed_dtype, int32_t out_dtype,
+                                               hipStream_t stream) {
+    return residual_rmsnorm(residual, out, x, mixed, weight, token_mask, true, rows, width, eps,
+                            residual_dtype, mixed_dtype, out_dtype, stream);
 }
 
 extern "C" int32_t qdc_gated_rmsnorm(void *out, const void *x, const void *z, const void *weight,

@@ -32,6 +32,10 @@ SIGNATURES = {
     "qdc_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _vp]),
     "qdc_residual_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _i32,
                                     _vp]),
+    "qdc_rmsnorm_masked": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _i32, _i32,
+                                  _i32, _vp]),
+    "qdc_residual_rmsnorm_masked": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32,
+                                           _i32, _i32, _vp]),
     "qdc_qk_norm_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 16
                          + [_f32, _i32, _vp]),
     "qdc_rope_tables": (_i32, [_vp, _vp, _i64, _i64, _f32]),

@@ -13,7 +13,8 @@ Mirrors the reference's public entry points and their validation:
 
 Per layer (``native_layer``, ``src/backbone.jl:363-388``) the fused kernels do
 the row work: the layer's input RMSNorm is fused with the previous layer's MLP
-residual add (``qdc_residual_rmsnorm``; the last one with the final norm),
+residual add (``qdc_residual_rmsnorm``; the last one with the final norm) and,
+before a DeltaNet layer, with its input mask (``qdc_residual_rmsnorm_masked``),
 post-attention residual + RMSNorm, q/k norm + partial RoPE read straight out of
 the packed projection, the attention masked softmax and output-gate merge, the
 DeltaNet prologue (convolution, SiLU, q/k L2 norm, gates), the gated-delta
@@ -146,26 +147,31 @@ class QwenBackbone:
         cfg = self.cfg
         # residual stream h in fp32 (a bf16 table widens exactly while gathered)
         h = ops.native_gather(self.embedding, ids.reshape(-1).contiguous(), out_dtype=torch.float32)
-        normed = ops.native_rms(h, self.layers[0]["input_norm"], cfg.eps)
-        maskf = None if mask is None else mask.to(torch.float32)
         mask32 = None if mask is None else mask.to(torch.int32).contiguous()
+        # Masked tokens are zeroed before the DeltaNet projections (src/backbone.jl:286):
+        # the norm producing a DeltaNet layer's input writes the masked rows itself.
+        keep = None if mask32 is None else mask32.view(-1)
+        delta_keep = lambda i: keep if self.layers[i]["kind"] != "full_attention" else None  # noqa: E731
+        normed = ops.native_rms(h, self.layers[0]["input_norm"], cfg.eps, token_mask=delta_keep(0))
         for i, layer in enumerate(self.layers):
             if layer["kind"] == "full_attention":
                 mixed = self._full_attention(layer, normed, mask32, B, S)
             else:
-                mixed = self._delta_attention(layer, normed, maskf, B, S)
+                mixed = self._delta_attention(layer, normed, B, S)
             residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps)
             gate_up = normed @ layer["gate_up"]
             inter = gate_up.shape[1] // 2
             act = ops.native_mlp_gate(gate_up[:, :inter], gate_up[:, inter:])
             down = self._mm32(act, layer["down"])
-            nxt = self.layers[i + 1]["input_norm"] if i + 1 < len(self.layers) else self.final_norm
+            last = i + 1 == len(self.layers)
+            nxt = self.final_norm if last else self.layers[i + 1]["input_norm"]
             # residual add of the MLP fused with the next RMSNorm
-            h, normed = ops.native_residual_rms(residual, down, nxt, cfg.eps)
+            h, normed = ops.native_residual_rms(residual, down, nxt, cfg.eps,
+                                                token_mask=None if last else delta_keep(i + 1))
         return normed
 
     def _full_attention(self, layer, x, mask32, B, S):
-        """``full_attention`` in the AMDGPU form (``ext/amdgpu_attention.jl:108-168``;
+        """``full_attention`` in the AMDGPU form (``ext/amdgpu_attention.jl:108-178``;
         generic ``src/backbone.jl:224-262``).  Q and K are normalised and rotated
         straight into head-major per-sequence layouts ``[B, H, S, hd]`` and
         ``[B, KV, S, hd]``: the G = H / KV query heads sharing a KV head are then one
@@ -204,17 +210,17 @@ class QwenBackbone:
             return torch.bmm(a, b)
         return torch.bmm(a, b, out_dtype=torch.float32)
 
-    def _delta_attention(self, layer, x, maskf, B, S):
+    def _delta_attention(self, layer, x, B, S):
         """Gated DeltaNet (``src/backbone.jl:284-345``; recurrent form
-        ``src/backbone_cpu.jl:680-759``)."""
+        ``src/backbone_cpu.jl:680-759``) on an input whose masked tokens the
+        producing norm has already zeroed (``native_layer_outputs(...,
+        Val(true))``, ``src/backbone.jl:372-376``)."""
         cfg = self.cfg
         kd, kh, vd, vh = cfg.key_dim, cfg.key_heads, cfg.value_dim, cfg.value_heads
         T = B * S
         kw, vw = kd * kh, vd * vh
         cq = 2 * kw + vw
-        # masked tokens are zeroed before the projections (src/backbone.jl:286)
-        masked = x if maskf is None else x * maskf.reshape(T, 1).to(x.dtype)
-        proj = masked @ layer["proj"]      # [T, cq + vw + 2*vh (+ zero padding)]
+        proj = x @ layer["proj"]           # [T, cq + vw + 2*vh (+ zero padding)]
         # conv + SiLU, q/k L2 norm and the beta/decay gates in one pass
         q, k, v, beta, decay = ops.delta_prologue(proj, layer["conv"], layer["a_decay"],
                                                   layer["dt_bias"], S, kh, kd, vh, vd)

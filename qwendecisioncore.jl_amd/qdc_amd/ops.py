@@ -116,12 +116,27 @@ def native_gather(embedding: torch.Tensor, ids, out: torch.Tensor | None = None,
 
 
 # ------------------------------------------------------------------ norms ---
+def _row_mask(token_mask: torch.Tensor | None, rows: int, like: torch.Tensor):
+    """Validate an optional device int32 row mask (one 0/1 entry per row)."""
+    if token_mask is None:
+        return None
+    _device(like, token_mask)
+    if (token_mask.dtype != torch.int32 or not token_mask.is_contiguous()
+            or token_mask.numel() != rows):
+        raise ValueError("token_mask must be a contiguous int32 vector of one entry per row")
+    return token_mask
+
+
 def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool = True,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None,
+               token_mask: torch.Tensor | None = None) -> torch.Tensor:
     """RMSNorm over the last axis: ``(x*s)*(1+w)`` (centred) or ``(x*s)*w``.
 
     The output takes the weight's dtype, so an fp32 ``x`` with a bf16 weight
-    gives a bf16 result (an fp32 residual stream feeding bf16 GEMMs)."""
+    gives a bf16 result (an fp32 residual stream feeding bf16 GEMMs).  With a
+    ``token_mask`` (device int32, one 0/1 entry per row) each output row is
+    multiplied by its entry before rounding: the DeltaNet input mask of
+    ``src/backbone.jl:286`` fused into the norm that produces that input."""
     _device(x, weight)
     if x.dtype not in _DTYPES or weight.dtype not in _DTYPES:
         raise ValueError("x and weight must be float32 or bfloat16")
@@ -133,19 +148,29 @@ def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool
     if out.shape != x.shape or out.dtype != weight.dtype:
         raise ValueError("out must have the shape of x and the dtype of weight")
     _, _, ld_out = _rows_view(out)
-    check(lib().qdc_rmsnorm(out.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, width, ld_x,
-                            ld_out, eps, int(bool(centered)), _DTYPES[x.dtype],
-                            _DTYPES[weight.dtype], _stream(x)), "native_rms")
+    keep = _row_mask(token_mask, rows, x)
+    if keep is None:
+        check(lib().qdc_rmsnorm(out.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, width,
+                                ld_x, ld_out, eps, int(bool(centered)), _DTYPES[x.dtype],
+                                _DTYPES[weight.dtype], _stream(x)), "native_rms")
+    else:
+        check(lib().qdc_rmsnorm_masked(out.data_ptr(), x.data_ptr(), weight.data_ptr(),
+                                       keep.data_ptr(), rows, width, ld_x, ld_out, eps,
+                                       int(bool(centered)), _DTYPES[x.dtype],
+                                       _DTYPES[weight.dtype], _stream(x)), "native_rms")
     return out
 
 
 def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tensor, eps: float,
                         residual: torch.Tensor | None = None,
-                        out: torch.Tensor | None = None):
+                        out: torch.Tensor | None = None,
+                        token_mask: torch.Tensor | None = None):
     """``residual = x + mixed``; returns ``(residual, rms(residual))`` in one pass.
 
     ``residual`` has x's dtype, the normalised output the weight's dtype;
-    ``mixed`` may be bf16 while x is fp32 (fp32 residual stream)."""
+    ``mixed`` may be bf16 while x is fp32 (fp32 residual stream).  A
+    ``token_mask`` masks the normalised rows as in ``native_rms``; the residual
+    is never masked."""
     _device(x, mixed, weight)
     for t in (x, mixed, weight):
         if t.dtype not in _DTYPES:
@@ -162,10 +187,19 @@ def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tens
         raise ValueError("residual must be a contiguous tensor like x")
     if out.shape != x.shape or not out.is_contiguous() or out.dtype != weight.dtype:
         raise ValueError("out must be contiguous, shaped like x, of the weight's dtype")
-    check(lib().qdc_residual_rmsnorm(residual.data_ptr(), out.data_ptr(), x.data_ptr(),
-                                     mixed.data_ptr(), weight.data_ptr(), rows, width, eps,
-                                     _DTYPES[x.dtype], _DTYPES[mixed.dtype],
-                                     _DTYPES[weight.dtype], _stream(x)), "native_residual_rms")
+    keep = _row_mask(token_mask, rows, x)
+    if keep is None:
+        check(lib().qdc_residual_rmsnorm(residual.data_ptr(), out.data_ptr(), x.data_ptr(),
+                                         mixed.data_ptr(), weight.data_ptr(), rows, width, eps,
+                                         _DTYPES[x.dtype], _DTYPES[mixed.dtype],
+                                         _DTYPES[weight.dtype], _stream(x)), "native_residual_rms")
+    else:
+        check(lib().qdc_residual_rmsnorm_masked(residual.data_ptr(), out.data_ptr(), x.data_ptr(),
+                                                mixed.data_ptr(), weight.data_ptr(),
+                                                keep.data_ptr(), rows, width, eps,
+                                                _DTYPES[x.dtype], _DTYPES[mixed.dtype],
+                                                _DTYPES[weight.dtype], _stream(x)),
+              "native_residual_rms")
     return residual, out
 
 

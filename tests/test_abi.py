@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 14, names
+    assert len(names) == 16, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -96,6 +96,27 @@ def test_residual_validation():
     assert f(A, B, C, B, W, 4, 8, 1e-6, F32, BF16, F32) == -5  # out on mixed of another type
     assert f(A, B, C, D, W, 0, 8, 1e-6, F32, F32, F32) == 0
     assert f(A, B, C, D, W, 1 << 26, 8, 1e-6, F32, F32, F32) == -2  # rows < 2^26
+
+
+def test_masked_norm_validation():
+    """The masked entry points validate like the unmasked ones, require the
+    mask, and refuse a mask that overlaps an output."""
+    lib = _lib.lib()
+    rms = lambda *a: lib.qdc_rmsnorm_masked(*a, None)  # noqa: E731
+    K = FAKE * 8
+    assert rms(FAKE, FAKE, FAKE, K, 4, 8, 8, 8, 1e-6, 1, 7, F32) == -3
+    assert rms(FAKE, FAKE, FAKE, None, 4, 8, 8, 8, 1e-6, 1, F32, F32) == -1  # mask required
+    assert rms(None, None, None, None, 0, 8, 8, 8, 1e-6, 1, F32, F32) == 0  # nothing to do
+    assert rms(FAKE, FAKE * 2, FAKE * 3, FAKE + 16, 4, 8, 8, 8, 1e-6, 1, F32, F32) == -5
+    assert rms(FAKE, FAKE * 2, FAKE * 3, K, 1 << 26, 8, 8, 8, 1e-6, 1, F32, F32) == -2
+    f = lambda *a: lib.qdc_residual_rmsnorm_masked(*a, None)  # noqa: E731
+    A, B, C, D, W = FAKE, FAKE * 2, FAKE * 3, FAKE * 4, FAKE * 5
+    assert f(A, B, C, D, W, None, 4, 8, 1e-6, F32, F32, F32) == -1  # mask required
+    assert f(A, B, C, D, W, K, 4, 8, 1e-6, BF16, F32, F32) == -3
+    assert f(A, B, C, D, W, B + 8, 4, 8, 1e-6, F32, F32, F32) == -5  # mask inside out
+    assert f(A, B, C, D, W, A + 8, 4, 8, 1e-6, F32, F32, F32) == -5  # mask inside residual
+    assert f(A, B, C, D, W, None, 0, 8, 1e-6, F32, F32, F32) == 0
+    assert f(A, B, C, D, W, K, 1 << 26, 8, 1e-6, F32, F32, F32) == -2
 
 
 def test_gated_validation():

@@ -316,6 +316,61 @@ def test_residual_rmsnorm_fp32_stream(mixed_dtype, out_dtype, rows, width):
     report(f"residual f32+bf16 -> {out_dtype} {rows}x{width}", back(out), exp_out, out_dtype)
 
 
+# ------------------------------------------------- DeltaNet input mask ------
+def _same_bits_or_nan(a, b):
+    """Julia isequal on fp32 arrays: NaN equals NaN, -0 differs from +0."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | ((a.view(np.uint32) == b.view(np.uint32)) & ~np.isnan(a))))
+
+
+@pytest.mark.parametrize("x_dtype,out_dtype", [(torch.float32, torch.float32),
+                                                (torch.bfloat16, torch.bfloat16),
+                                                (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("rows,width", [(16384, 1024), (65, 256), (33, 1000), (3, 7)])
+def test_masked_norms(x_dtype, out_dtype, rows, width):
+    """The DeltaNet input mask (src/backbone.jl:286) fused into the norms that
+    produce that input.  Each masked row is the unmasked kernel's row times its
+    0/1 entry, bit for bit (-0, and NaN from a masked inf, included); the
+    residual output is not masked; and the finite rows match the oracle's norm
+    followed by the reference's ``x .* mask``.  Widths 1000 and 7 take the
+    general kernels."""
+    from qdc_amd import ops
+    keep = (np.random.default_rng(40).random(rows) < 0.7).astype(np.int32)
+    keep[0] = 0
+    keep[-1] = 1
+    x = host((rows, width), 41, 1.0, x_dtype)
+    m = host((rows, width), 42, 1.0, out_dtype)
+    w = host((width,), 43, 0.02, out_dtype)
+    special = 1 if rows > 2 else None
+    if special is not None:  # masked row holding an inf: 0 * inf = NaN, as in the reference
+        keep[special] = 0
+        x[special, 0] = np.inf
+    finite = np.ones(rows, bool)
+    if special is not None:
+        finite[special] = False
+    km = torch.from_numpy(keep).to(DEV)
+    xt, mt, wt = dev(x, x_dtype), dev(m, out_dtype), dev(w, out_dtype)
+    with np.errstate(all="ignore"):
+        plain = back(ops.native_rms(xt, wt, 1e-6))
+        masked = back(ops.native_rms(xt, wt, 1e-6, token_mask=km))
+        assert _same_bits_or_nan(masked, plain * keep[:, None].astype(np.float32))
+        exp = O.rms(x, w, 1e-6) * keep[:, None].astype(np.float32)
+        report(f"masked rms {rows}x{width} {x_dtype}->{out_dtype}", masked[finite], exp[finite],
+               out_dtype)
+        res0, out0 = ops.native_residual_rms(xt, mt, wt, 1e-6)
+        res1, out1 = ops.native_residual_rms(xt, mt, wt, 1e-6, token_mask=km)
+        assert _same_bits_or_nan(back(res1), back(res0))
+        assert _same_bits_or_nan(back(out1), back(out0) * keep[:, None].astype(np.float32))
+        exp_res, exp_out = O.residual_rms(x, m, w, 1e-6)
+        report(f"masked residual-norm {rows}x{width}", back(out1)[finite],
+               (exp_out * keep[:, None].astype(np.float32))[finite], out_dtype)
+    with pytest.raises(ValueError):
+        ops.native_rms(xt, wt, 1e-6, token_mask=km[:-1])
+    with pytest.raises(ValueError):
+        ops.native_rms(xt, wt, 1e-6, token_mask=km.to(torch.int64))
+
+
 # ------------------------------------------- fast and general kernels ------
 def _shifted(t):
     """The same values starting one element past a 16-byte boundary (the
@@ -590,17 +645,10 @@ def test_delta_prologue(dtype, case):
         report(f"prologue {name} {case} {dtype}", g, e, torch.float32)
 
 
-def _same_bits_or_nan(a, b):
-    """Julia isequal on fp32 arrays: NaN equals NaN, -0 differs from +0."""
-    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
-    nan = np.isnan(a) & np.isnan(b)
-    return bool(np.all(nan | ((a.view(np.uint32) == b.view(np.uint32)) & ~np.isnan(a))))
-
-
 @pytest.mark.parametrize("KH,kd,H,vd,pad", [(1, 8, 1, 8, 2),    # fast kernel
                                             (1, 6, 1, 6, 0)])   # general kernel
 def test_delta_prologue_special_values(KH, kd, H, vd, pad):
-    """The q/k normalisation special values of test/backbone.jl:303-312 (0, -0,
+    """The q/k normalisation special values of test/backbone.jl:304-312 (0, -0,
     NaN, Inf, floatmax and the smallest denormal) through the prologue: every
     token its own sequence and the convolution the current-row tap, so each head
     sees silu(x) with x the special value (2^-148 becomes 2^-149)."""
