@@ -90,7 +90,12 @@ def masks(n, rng):
     prefix[: n // 3] = 0
     holes = np.ones(n, np.int64)
     holes[: n - 1:3] = 0
-    return {"ones": np.ones(n, np.int64), "prefix": prefix, "holes": holes}
+    last = np.zeros(n, np.int64)
+    last[-1] = 1
+    # every token masked is valid input (check_sequence asks only for 0/1): DeltaNet
+    # inputs all zero, attention rows with no visible key uniform over the keys
+    return {"ones": np.ones(n, np.int64), "prefix": prefix, "holes": holes, "last": last,
+            "zeros": np.zeros(n, np.int64)}
 
 
 @pytest.mark.parametrize("n", [1, 9, 64, 65, 128])
