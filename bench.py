@@ -175,10 +175,11 @@ def build_kernels(dev):
         "bfloat16", group="next"))
 
     # DeltaNet prologue of one layer: 16384 tokens, 16 key/value heads of 128,
-    # packed projection [qkv | z | a | b] in bf16 (z is not read), fp32 outputs.
+    # packed projection [qkv | z | a | b] in bf16 (z is not read), fp32 outputs;
+    # rows padded to a multiple of 256 columns as the backbone packs the weight.
     Tp, hp, dp = 16384, 16, 128
     cqp = 3 * hp * dp
-    widthp = cqp + hp * dp + 2 * hp
+    widthp = -(-(cqp + hp * dp + 2 * hp) // 256) * 256
     convp = randn((cqp, 4), f32, 0.5)
     a_dec = -torch.exp(randn((hp,), f32, 0.5))
     dtb = randn((hp,), f32)

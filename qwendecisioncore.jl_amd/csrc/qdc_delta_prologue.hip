@@ -12,7 +12,7 @@
 // gates src/backbone.jl:293-296; AMDGPU causal_depthwise_kernel! /
 // qk_normalize_kernel! and the beta/decay broadcasts, ext/amdgpu_delta.jl:1-33, 83-113, 154-159.
 //
-// Fast path: a thread owns 4 consecutive channels for a tile of 32 (bf16) or 16
+// Fast path: a thread owns 4 consecutive channels for a tile of 40 (bf16) or 16
 // (fp32) consecutive tokens, loads the tile's rows and the K-1 halo rows before
 // it in one go, then slides a K-tap window down the tile, so each projection row
 // is read once from HBM (the halo comes from L2) and each output chunk is one
@@ -57,7 +57,9 @@ __device__ __forceinline__ float softplus_f(float x) {
 // and exactly one 16-byte fp32 output chunk, so every load and store
 // instruction of a wavefront covers whole cache lines.  Tokens per thread: the
 // tile's rows plus the kTaps-1 halo rows are all loaded before the first is used.
-template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 32 : 16; }
+// bf16 tiles of 40 tokens measured ~4% faster than 32 or 64 at the 0.8B shapes
+// (more rows in flight per wavefront against occupancy 3 instead of 4).
+template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 40 : 16; }
 
 template <typename T> struct Raw4;  // 4 channels of one projection row
 template <> struct Raw4<bf16_t> {
