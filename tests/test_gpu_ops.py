@@ -324,6 +324,54 @@ def _same_bits_or_nan(a, b):
     return bool(np.all(nan | ((a.view(np.uint32) == b.view(np.uint32)) & ~np.isnan(a))))
 
 
+def _exact_rows(width):
+    """Rows whose sum of squares is exact in any summation order, so the
+    normalised values are fixed bit for bit: zeros; 1e20 (the sum overflows to
+    inf, scale 0); an inf (NaN there, zeros elsewhere); a NaN (all NaN); fp32
+    denormals 2^-130 (squares underflow to 0: a flush-to-zero would show);
+    2^-60 (squares 2^-120, exact partial sums); 3.0 and alternating +-1.5.
+    All values are bf16-representable."""
+    rows = [np.zeros(width), np.full(width, 1e20)]
+    r = np.full(width, 3.0)
+    r[width // 2] = np.inf
+    rows.append(r)
+    r = np.full(width, 2.0)
+    r[0] = np.nan
+    rows.append(r)
+    rows += [np.full(width, 2.0 ** -130), np.full(width, 2.0 ** -60), np.full(width, 3.0),
+             np.where(np.arange(width) % 2 == 0, 1.5, -1.5)]
+    return O.round_bf16(np.array(rows, dtype=np.float32))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("width", [1024, 1000, 7])
+def test_norm_special_rows_bit_exact(dtype, width):
+    """Zero, overflowing, inf, NaN, denormal and exactly-summable rows through
+    the plain, residual and gated norms: bit for bit (NaN-aware) equal to the
+    oracle, on the fast kernels (width 1024) and the general ones (1000, 7).
+    The gate z is 0, +100 or -100, where silu is exactly 0, z and -0."""
+    from qdc_amd import ops
+    x = _exact_rows(width)
+    w = host((width,), 45, 0.02, dtype)
+    # a bf16 output is the fp32 result rounded once to nearest even
+    rnd = O.round_bf16 if dtype == torch.bfloat16 else (lambda e: e)
+    with np.errstate(all="ignore"):
+        got = back(ops.native_rms(dev(x, dtype), dev(w, dtype), 1e-6))
+        assert _same_bits_or_nan(got, rnd(O.rms(x, w, 1e-6))), "rms"
+        got = back(ops.native_rms(dev(x, dtype), dev(w, dtype), 1e-6, centered=False))
+        assert _same_bits_or_nan(got, rnd(O.rms(x, w, 1e-6, False))), "rms not centred"
+        zero = np.zeros_like(x)
+        res, out = ops.native_residual_rms(dev(x, dtype), dev(zero, dtype), dev(w, dtype), 1e-6)
+        exp_res, exp_out = O.residual_rms(x, zero, w, 1e-6)
+        assert _same_bits_or_nan(back(res), exp_res), "residual"
+        assert _same_bits_or_nan(back(out), rnd(exp_out)), "residual norm"
+        z = np.resize(np.array([0.0, 100.0, -100.0], np.float32), x.shape)
+        got = back(ops.native_gated_rms(dev(x, dtype).view(len(x), 1, width),
+                                        dev(z, dtype).view(len(x), 1, width), dev(w, dtype), 1e-6))
+        exp = O.gated_rms(x.reshape(len(x), 1, width), z.reshape(len(x), 1, width), w, 1e-6)
+        assert _same_bits_or_nan(got.reshape(x.shape), rnd(exp.reshape(x.shape))), "gated"
+
+
 @pytest.mark.parametrize("x_dtype,out_dtype", [(torch.float32, torch.float32),
                                                 (torch.bfloat16, torch.bfloat16),
                                                 (torch.float32, torch.bfloat16)])
