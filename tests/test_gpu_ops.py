@@ -372,6 +372,29 @@ def test_norm_special_rows_bit_exact(dtype, width):
         assert _same_bits_or_nan(got.reshape(x.shape), rnd(exp.reshape(x.shape))), "gated"
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("hd,rd", [(256, 64), (96, 24)])
+def test_qk_norm_rope_special_rows_bit_exact(dtype, hd, rd):
+    """The same exactly-summable and special rows as q and k heads (one token
+    each, positions 0..7): normalisation and rotation use the oracle's
+    operation order and its bit-equal tables, so q and k agree bit for bit
+    (fast kernel at head_dim 256, general kernel at 96)."""
+    from qdc_amd import ops
+    x = _exact_rows(hd)
+    T = len(x)
+    qn = host((hd,), 46, 0.02, dtype)
+    kn = host((hd,), 47, 0.02, dtype)
+    tables = ops.rope_tables(T, rd, 1e7, DEV)
+    cos, sin = O.rope_tables(T, rd, 1e7)
+    rnd = O.round_bf16 if dtype == torch.bfloat16 else (lambda e: e)
+    xs = x.reshape(T, 1, hd)
+    with np.errstate(all="ignore"):
+        qo, ko = ops.prepare_heads(dev(xs, dtype), dev(xs, dtype), dev(qn, dtype), dev(kn, dtype),
+                                   tables, rd, 1e-6, seq_len=T)
+        assert _same_bits_or_nan(back(qo), rnd(O.qk_norm_rope(xs, qn, cos, sin, rd, 1e-6, T))), "q"
+        assert _same_bits_or_nan(back(ko), rnd(O.qk_norm_rope(xs, kn, cos, sin, rd, 1e-6, T))), "k"
+
+
 @pytest.mark.parametrize("x_dtype,out_dtype", [(torch.float32, torch.float32),
                                                 (torch.bfloat16, torch.bfloat16),
                                                 (torch.float32, torch.bfloat16)])
