@@ -28,7 +28,6 @@ namespace qdc {
 namespace {
 
 constexpr int kTaps = 4;    // fast-path convolution width (the Qwen3.5 default)
-constexpr uint32_t kXcds = 8;  // accelerator complex dies of an MI355X
 
 struct Prologue {
     const void *proj;
@@ -82,21 +81,11 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     using Raw = typename Raw4<T>::type;
     constexpr int kTileT = tile_for<T>();
     constexpr int kRows = kTileT + kTaps - 1;  // rows t0-3 .. t0+tile-1
-    // One-dimensional grid of tiles x channel blocks (the last block of a tile
-    // computes the gates).  Workgroups are dealt round-robin to the 8 XCDs (each
-    // with its own L2): XCD z gets a contiguous run of tiles and, for each tile,
-    // all its channel blocks in a row, so whole projection rows are read together
-    // and a tile's halo rows were just read by the previous tile on the same XCD.
-    const uint32_t nblk = a.blocks_per_tile, tiles = gridDim.x / nblk;
-    uint32_t tile, cblk;
-    if (tiles % kXcds == 0) {
-        const uint32_t z = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
-        tile = z * (tiles / kXcds) + k / nblk;
-        cblk = k % nblk;
-    } else {
-        tile = blockIdx.x / nblk;
-        cblk = blockIdx.x % nblk;
-    }
+    // One-dimensional grid of tiles x channel blocks in plain order (the last
+    // block of a tile computes the gates).  Dealing each XCD a contiguous run of
+    // tiles, so halo rows hit the same L2, measured 0-2% slower on MI355X.
+    const uint32_t nblk = a.blocks_per_tile;
+    const uint32_t tile = blockIdx.x / nblk, cblk = blockIdx.x % nblk;
     const int64_t t0 = (int64_t)tile * kTileT;
     if (cblk == nblk - 1) {  // the gates block of this tile
         for (int i = threadIdx.x; i < kTileT * a.vh; i += kBlock) {
