@@ -9,11 +9,26 @@
  * of squares use 16 independent fp32 partial sums combined pairwise, the
  * reassociation Julia's `sum(abs2, v)` / `@simd` applies; the result differs
  * from a sequential sum only in the last bits.
+ *
+ * Threads (qdco_set_threads, default 1): rows are independent, so an OpenMP
+ * loop over rows gives the same bits at any thread count; the timed CPU
+ * baseline uses it for an all-cores figure.  SwiGLU over contiguous rows
+ * restates the reference's own split instead: min(threads, cld(n, 65536))
+ * workers, worker w taking the 256-element blocks w, w + workers, ...
+ * (ext/QwenDecisionCoreLoopVectorizationExt.jl:194-205).
  */
 #include "qdc_oracle.h"
 
 #include <math.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 1;
+
+void qdco_set_threads(int threads) { g_threads = threads < 1 ? 1 : threads; }
+int qdco_threads(void) { return g_threads; }
 
 /* src/safetensors.jl:28-30 */
 float qdco_bf16_to_f32(uint16_t bits) {
@@ -45,6 +60,7 @@ int qdco_gather(void *out, const void *table, int64_t elem_bytes, const int32_t 
     for (int64_t t = 0; t < n_ids; ++t)
         if (ids[t] < 0 || (int64_t)ids[t] >= vocab) return -1;
     const int64_t row_bytes = hidden * elem_bytes;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t t = 0; t < n_ids; ++t)
         memcpy((char *)out + t * row_bytes, (const char *)table + (int64_t)ids[t] * row_bytes,
                (size_t)row_bytes);
@@ -71,6 +87,7 @@ static float rms_scale(const float *row, int64_t width, float eps) {
 /* cpu_rms! src/backbone_cpu.jl:333-350 (centred) and cpu_delta_rms! :352-362. */
 void qdco_rms(float *out, int64_t ld_out, const float *x, int64_t ld_x, const float *w,
               int64_t rows, int64_t width, float eps, int centered) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t r = 0; r < rows; ++r) {
         const float *in = x + r * ld_x;
         float *dst = out + r * ld_out;
@@ -85,6 +102,7 @@ void qdco_rms(float *out, int64_t ld_out, const float *x, int64_t ld_x, const fl
 /* src/backbone.jl:347-350; src/backbone_cpu.jl:321-328. */
 void qdco_residual_rms(float *residual, float *out, const float *x, const float *mixed,
                        const float *w, int64_t rows, int64_t width, float eps) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t r = 0; r < rows; ++r) {
         float *res = residual + r * width;
         for (int64_t i = 0; i < width; ++i) res[i] = x[r * width + i] + mixed[r * width + i];
@@ -116,6 +134,7 @@ void qdco_qk_norm_rope(float *out, int64_t out_tok, int64_t out_head, const floa
                        const float *sines, int64_t tokens, int64_t heads, int64_t dim,
                        int64_t rotary_dim, int64_t seq_len, int64_t pos_offset, float eps) {
     const int64_t half = rotary_dim / 2;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t t = 0; t < tokens; ++t) {
         const int64_t pos = pos_offset + t % seq_len;
         const float *c = cosines + pos * half;
@@ -141,6 +160,7 @@ static float silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
 void qdco_gated_rms(float *out, int64_t out_tok, const float *x, int64_t x_tok, const float *z,
                     int64_t z_tok, const float *w, int64_t tokens, int64_t heads, int64_t width,
                     float eps) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t t = 0; t < tokens; ++t)
         for (int64_t h = 0; h < heads; ++h) {
             const float *src = x + t * x_tok + h * width;
@@ -153,8 +173,31 @@ void qdco_gated_rms(float *out, int64_t out_tok, const float *x, int64_t x_tok, 
 }
 
 /* ext/QwenDecisionCoreLoopVectorizationExt.jl:189-215 / :104-127 / :144-160. */
+static void swiglu_range(float *out, const float *gate, const float *up, int64_t lo, int64_t hi) {
+    for (int64_t i = lo; i < hi; ++i) {
+        const float x = gate[i];
+        out[i] = (x * (1.0f / (1.0f + expf(-x)))) * up[i];
+    }
+}
+
 void qdco_swiglu(float *out, int64_t ld_out, const float *gate, int64_t ld_gate, const float *up,
                  int64_t ld_up, int64_t tokens, int64_t width) {
+    const int64_t n = tokens * width;
+    const int64_t blocks_needed = (n + 65535) / 65536;
+    const int workers = (int)(g_threads < blocks_needed ? g_threads : blocks_needed);
+    if (workers > 1 && ld_out == width && ld_gate == width && ld_up == width) {
+#pragma omp parallel num_threads(workers)
+        {
+#ifdef _OPENMP
+            const int64_t w = omp_get_thread_num(), nw = omp_get_num_threads();
+#else
+            const int64_t w = 0, nw = 1;
+#endif
+            for (int64_t b = 256 * w; b < n; b += 256 * nw)
+                swiglu_range(out, gate, up, b, b + 256 < n ? b + 256 : n);
+        }
+        return;
+    }
     for (int64_t t = 0; t < tokens; ++t) {
         const float *g = gate + t * ld_gate;
         const float *u = up + t * ld_up;

@@ -23,6 +23,11 @@
 extern "C" {
 #endif
 
+/* Threads for the row loops (default 1).  Rows are independent, so the
+ * results do not depend on the count; used for the all-cores CPU figure. */
+void qdco_set_threads(int threads);
+int qdco_threads(void);
+
 /* bf16 widen: bits << 16.  src/safetensors.jl:28-30 */
 float qdco_bf16_to_f32(uint16_t bits);
 /* bf16 narrow, RNE on the 16 dropped bits.  src/safetensors.jl:37-42 */

@@ -47,8 +47,19 @@ def _load():
     lib.qdco_gated_rms.argtypes = [_f32p, _i64, _f32p, _i64, _f32p, _i64, _f32p, _i64, _i64, _i64,
                                    ctypes.c_float]
     lib.qdco_swiglu.argtypes = [_f32p, _i64, _f32p, _i64, _f32p, _i64, _i64, _i64]
+    lib.qdco_set_threads.argtypes = [ctypes.c_int]
+    lib.qdco_threads.restype = ctypes.c_int
     _lib = lib
     return lib
+
+
+def set_threads(threads: int) -> int:
+    """Threads for the C row loops (1 by default; results do not depend on it).
+    Returns the previous count."""
+    lib = _load()
+    previous = lib.qdco_threads()
+    lib.qdco_set_threads(int(threads))
+    return previous
 
 
 def _p(a, t=_f32p):
