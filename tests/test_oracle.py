@@ -345,3 +345,35 @@ def test_attention_gate_against_scipy():
             for h in range(H):
                 exp = values[b, h, s] * expit(gate[b * S + s, h].astype(np.float64))
                 assert np.abs(got[b * S + s, h * hd:(h + 1) * hd] - exp).max() < 1e-6
+
+
+def test_threaded_oracle_is_bit_identical():
+    """The oracle's OpenMP row loops (used for the all-cores CPU figure) give
+    the single-thread bits; SwiGLU over more than 65536 elements takes the
+    reference's interleaved 256-element block split, with a ragged last block."""
+    rng = np.random.default_rng(9)
+    g = rng.standard_normal((301, 700), dtype=np.float32) * np.float32(4)
+    u = rng.standard_normal((301, 700), dtype=np.float32)
+    x = rng.standard_normal((257, 96), dtype=np.float32)
+    w = rng.standard_normal(96, dtype=np.float32) * np.float32(0.02)
+    q = rng.standard_normal((33, 3, 96), dtype=np.float32)
+    cos, sin = O.rope_tables(33, 32, 1e4)
+    z = rng.standard_normal((41, 4, 96), dtype=np.float32)
+    table = rng.standard_normal((500, 96), dtype=np.float32)
+    ids = rng.integers(0, 500, size=77)
+
+    def run():
+        return [O.swiglu(g, u), O.rms(x, w, 1e-6), O.rms(x, w, 1e-6, False),
+                *O.residual_rms(x, x[::-1].copy(), w, 1e-6),
+                O.qk_norm_rope(q, w, cos, sin, 32, 1e-6, 11),
+                O.gated_rms(z, z[::-1].copy(), w, 1e-6), O.gather(table, ids)]
+
+    assert g.size > 65536 and g.size % 256
+    single = run()
+    previous = O.set_threads(4)
+    try:
+        threaded = run()
+    finally:
+        O.set_threads(previous)
+    for a, b in zip(single, threaded):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
