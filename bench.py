@@ -39,6 +39,9 @@ reference CPU path, fp32 arithmetic as in the reference) on a quarter of each
 kernel's rows, repeated to at least 10 s, on this machine's host cores, then
 the same mix on every host core the process may use (OpenMP over rows,
 `all_cores`, at least 5 s) as an upper bound for a threaded CPU path.
+With the end-to-end run, `backbone.cpu` times the oracle's backbone_hidden of
+one 2048-token sequence of the same backbone in fp32 on the host (the
+reference runs one sequence per call) and `backbone.speedup_vs_cpu` compares.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
 """
@@ -449,6 +452,31 @@ def e2e_benchmark(dev, steps=3, warmup=1):
             "steps": steps, "warmup": warmup}
 
 
+def cpu_backbone(n_tokens=None):
+    """The oracle's backbone_hidden of one sequence of E2E_SEQ tokens (the
+    reference runs one sequence per call) on the host: the same random-init
+    0.8B-like backbone in fp32 (numpy GEMMs on the host BLAS threads, the
+    oracle's row ops on one thread, as the reference CPU path with Julia's
+    default single thread).  Weights are drawn on the host (seed 0)."""
+    import numpy as np
+    from oracle import forward
+    from qdc_amd.config import qwen35_08b_config
+    from qdc_amd.weights import random_weights
+    n = n_tokens or E2E_SEQ
+    cfg = qwen35_08b_config()
+    weights = random_weights(cfg, seed=0)
+    ids = np.random.default_rng(2).integers(0, cfg.vocab, size=n)
+    t0 = time.perf_counter()
+    hidden = forward.backbone_hidden(weights, cfg.as_dict(), ids, np.ones(n, np.int64))
+    secs = time.perf_counter() - t0
+    if not np.isfinite(hidden).all():
+        raise RuntimeError("non-finite oracle backbone output")
+    return {"tokens_per_s": round(n / secs, 1), "seconds": round(secs, 2),
+            "sample": (f"oracle backbone_hidden, fp32, one sequence of {n} tokens, numpy GEMMs "
+                       f"on the host BLAS threads, row ops on 1 thread, on '{cpu_model()}' "
+                       f"({len(os.sched_getaffinity(0))} cores usable)")}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -618,6 +646,10 @@ def main():
         line["backbone"] = e2e_benchmark(dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        if "backbone" in line:
+            line["backbone"]["cpu"] = cpu_backbone()
+            line["backbone"]["speedup_vs_cpu"] = round(
+                line["backbone"]["tokens_per_s"] / line["backbone"]["cpu"]["tokens_per_s"], 1)
     print(json.dumps(line), flush=True)
 
 
