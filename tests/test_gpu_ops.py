@@ -546,33 +546,32 @@ def test_fast_and_general_kernels_agree(dtype, op):
     assert normwise(fast, general) <= (1e-6 if bar == torch.float32 else 2e-3)
 
 
-def test_graph_replays_match_eager():
-    """A chain of the library's kernels (gather, RMSNorm, q/k norm + RoPE,
-    SwiGLU, gated norm, residual norm, DeltaNet prologue and scan, softmax, gate
-    merge) captured once in a HIP graph and replayed three times, with eager work
-    on other buffers in between: every replay equals the eager run bit for bit
-    (the kernels clear nothing with memset and keep no state between calls)."""
+def _kernel_chain(seed):
+    """Inputs drawn from seeds seed .. seed+16 and a closure running a chain of
+    the library's kernels on them (gather, RMSNorm, q/k norm + RoPE, SwiGLU,
+    gated norm, residual norm, DeltaNet prologue and scan, softmax, gate merge);
+    it allocates its outputs on the current stream."""
     from qdc_amd import ops
     dt = torch.bfloat16
-    r = lambda shape, seed, scale=1.0: dev(host(shape, seed, scale, dt), dt)  # noqa: E731
+    r = lambda shape, k, scale=1.0: dev(host(shape, seed + k, scale, dt), dt)  # noqa: E731
     T, hidden, H, KV, hd, rd = 256, 1024, 8, 2, 256, 64
-    table, ids = r((512, hidden), 81, 0.02), torch.randint(0, 512, (T,), dtype=torch.int32,
-                                                             device=DEV)
-    w = r((hidden,), 82, 0.02)
-    qg, kx = r((T, H, 2 * hd), 83), r((T, KV, hd), 84)
-    qn, kn = r((hd,), 85, 0.02), r((hd,), 86, 0.02)
+    table = r((512, hidden), 0, 0.02)
+    ids = torch.from_numpy(np.random.default_rng(seed).integers(0, 512, T).astype(np.int32)).to(DEV)
+    w = r((hidden,), 1, 0.02)
+    qg, kx = r((T, H, 2 * hd), 2), r((T, KV, hd), 3)
+    qn, kn = r((hd,), 4, 0.02), r((hd,), 5, 0.02)
     tables = ops.rope_tables(T, rd, 1e7, DEV)
-    gu = r((T, 2 * 3584), 87)
-    gx, gz, gw = r((T, 16, 128), 88), r((T, 16, 128), 89), r((128,), 90)
-    mixed = r((T, hidden), 91)
+    gu = r((T, 2 * 3584), 6)
+    gx, gz, gw = r((T, 16, 128), 7), r((T, 16, 128), 8), r((128,), 9)
+    mixed = r((T, hidden), 10)
     KH, kd, VH, vd = 16, 128, 16, 128
     cq = 2 * KH * kd + VH * vd
-    proj = r((T, cq + VH * vd + 2 * VH), 92)
-    conv = dev(host((cq, 4), 93, 0.5), torch.float32)
-    a_dec = dev(-np.exp(host((VH,), 94, 0.5)), torch.float32)
-    dt_b = dev(host((VH,), 95, 1.0), torch.float32)
-    scores = dev(host((1, H, T, T), 96, 4.0), torch.float32)
-    values = dev(host((1, H, T, hd), 97, 1.0), torch.float32)
+    proj = r((T, cq + VH * vd + 2 * VH), 11)
+    conv = dev(host((cq, 4), seed + 12, 0.5), torch.float32)
+    a_dec = dev(-np.exp(host((VH,), seed + 13, 0.5)), torch.float32)
+    dt_b = dev(host((VH,), seed + 14, 1.0), torch.float32)
+    scores = dev(host((1, H, T, T), seed + 15, 4.0), torch.float32)
+    values = dev(host((1, H, T, hd), seed + 16, 1.0), torch.float32)
 
     def chain():
         h = ops.native_gather(table, ids, out_dtype=torch.float32)
@@ -587,7 +586,15 @@ def test_graph_replays_match_eager():
         p = ops.attention_softmax(scores, None, 0.0625, out_dtype=dt)
         m = ops.attention_gate(values, qg[:, :, hd:], out_dtype=dt)
         return [n, qo, ko, a, g, res, nr, o, p, m]
+    return chain
 
+
+def test_graph_replays_match_eager():
+    """The kernel chain captured once in a HIP graph and replayed three times,
+    with eager work on other buffers in between: every replay equals the eager
+    run bit for bit (the kernels clear nothing with memset and keep no state
+    between calls)."""
+    chain = _kernel_chain(81)
     eager = [t.clone() for t in chain()]
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
@@ -607,6 +614,44 @@ def test_graph_replays_match_eager():
         for i, (got, exp) in enumerate(zip(outs, eager)):
             assert torch.equal(got, exp), (rep, i)
             assert torch.equal(other[i], exp), (rep, i)
+
+
+def _bits(t):
+    return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
+
+
+def test_concurrent_threads_on_own_streams_match_serial():
+    """Two host threads, each on its own stream, run the kernel chain ten times
+    on different inputs at the same time (the C calls release the GIL): every
+    result equals the serial run bit for bit.  The library keeps no mutable
+    state and launches only on the stream it is given."""
+    import threading
+    chains = [_kernel_chain(100), _kernel_chain(200)]
+    serial = [[t.clone() for t in c()] for c in chains]
+    torch.cuda.synchronize()
+    results, errors = [None, None], []
+
+    def worker(i):
+        try:
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                for _ in range(10):
+                    outs = chains[i]()
+                stream.synchronize()
+            results[i] = outs
+        except Exception as e:  # reported after the join
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i in range(2):
+        for j, (got, exp) in enumerate(zip(results[i], serial[i])):
+            assert torch.equal(_bits(got), _bits(exp)), (i, j)
 
 
 # ------------------------------------------------ DeltaNet recurrence --------
