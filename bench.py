@@ -25,6 +25,11 @@ DeltaNet layers (reported under "widened", not in `value`):
                        (chunked form on the fp32 matrix cores; reported in
                        TFLOP/s against the dense fp32 MFMA peak too)
 
+Beside each fused row kernel the run times the library's plain streaming copy
+(qdc_copy) of the same total bytes, half read and half written, in the same
+way: `copy_pct_peak` is what a single launch of that size reaches, and
+`pct_of_copy` the kernel's bandwidth as a share of it.
+
 Inputs are resident in HBM before timing.  Every kernel cycles through
 several input/output buffer sets totalling more than 512 MB, so the 256 MB
 last-level cache cannot serve repeated launches.  The K launches of each
@@ -272,6 +277,31 @@ def time_gpu(kernels, steps):
     for k, (a, b) in zip(kernels, marks):
         k.avg_ms = a.elapsed_time(b) / steps
     return start.elapsed_time(end)
+
+
+def copy_ceilings(dev, kernels, steps, warmup):
+    """For each kernel, the library's plain streaming copy (qdc_copy: one
+    16-byte chunk per thread, nontemporal) of the same total bytes, half read
+    and half written, graph-replayed over rotating buffers like the kernels:
+    what a single launch moving that many bytes reaches on this GPU."""
+    import torch
+    from qdc_amd import ops
+    copies = []
+    for k in kernels:
+        side = (k.algo_bytes // 2) // 16 * 16
+        copies.append(Kernel(
+            f"copy_{k.name}", "copy_chunks", 2 * side,
+            lambda i, side=side: (torch.empty(side, dtype=torch.uint8, device=dev),
+                                  torch.empty(side, dtype=torch.uint8, device=dev)),
+            lambda st: ops.device_copy(st[1], st[0]), [side], "u8"))
+    for i in range(warmup):
+        for c in copies:
+            c.run(i)
+    capture(copies, steps)
+    for c in copies:  # one untimed replay
+        c.graph.replay()
+    time_gpu(copies, steps)
+    return {k.name: c for k, c in zip(kernels, copies)}
 
 
 CALIB_BYTES = 512 << 20
@@ -604,6 +634,7 @@ def main():
         k.graph.replay()
     time_gpu(kernels, args.steps)
     hot = [k for k in kernels if k.group == "hot"] or kernels
+    ceilings = copy_ceilings(dev, hot, args.steps, args.warmup)
     hot_ms = sum(k.avg_ms for k in hot) * args.steps
     step_bytes = sum(k.algo_bytes for k in hot)
     value = step_bytes * args.steps / (hot_ms / 1e3) / 1e9
@@ -613,6 +644,12 @@ def main():
              "us": round(k.avg_ms * 1e3, 3),
              "gbs": round(k.algo_bytes / (k.avg_ms / 1e3) / 1e9, 1),
              "pct_peak": round(100 * k.algo_bytes / (k.avg_ms / 1e3) / 1e9 / PEAK_GBS, 1)}
+        c = ceilings.get(k.name)
+        if c is not None:  # the same bytes as one plain streaming copy launch
+            copy_gbs = c.algo_bytes / (c.avg_ms / 1e3) / 1e9
+            e.update(copy_us=round(c.avg_ms * 1e3, 3),
+                     copy_pct_peak=round(100 * copy_gbs / PEAK_GBS, 1),
+                     pct_of_copy=round(100 * e["gbs"] / copy_gbs, 1))
         if k.flops:
             tf = k.flops / (k.avg_ms / 1e3) / 1e12
             e.update(bound="mfma", tflops=round(tf, 2), mfma_f32_peak_tflops=MFMA_F32_PEAK_TF,

@@ -261,6 +261,15 @@ int32_t qdc_attention_gate(void *out, int32_t out_dtype, const float *values, co
                            int64_t head_dim, int64_t gate_tok, int64_t gate_head, int64_t out_tok,
                            hipStream_t stream);
 
+/*
+ * Plain device copy of `bytes` bytes (a multiple of 16; both pointers 16-byte
+ * aligned, QDC_ERR_SHAPE otherwise; no overlap), one 16-byte chunk per thread
+ * with nontemporal loads and stores.  No counterpart in the reference: it is
+ * the single-launch bandwidth ceiling that the benchmark measures beside each
+ * row kernel at the same byte count.
+ */
+int32_t qdc_copy(void *dst, const void *src, int64_t bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,7 @@ SIGNATURES = {
                                      _vp]),
     "qdc_attention_gate": (_i32, [_vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _vp]),
+    "qdc_copy": (_i32, [_vp, _vp, _i64, _vp]),
 }
 
 _lib = None

@@ -423,6 +423,20 @@ def attention_gate(values: torch.Tensor, gate: torch.Tensor, out_dtype=None,
     return out
 
 
+def device_copy(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """Plain copy of ``src``'s bytes into ``dst`` (both contiguous, same byte
+    count, a multiple of 16) with the library's streaming copy kernel: the
+    single-launch bandwidth ceiling the benchmark sets beside each row kernel."""
+    _device(dst, src)
+    if not dst.is_contiguous() or not src.is_contiguous():
+        raise ValueError("dst and src must be contiguous")
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("dst and src must hold the same number of bytes")
+    check(lib().qdc_copy(dst.data_ptr(), src.data_ptr(), nbytes, _stream(src)), "device_copy")
+    return dst
+
+
 def check_ids(ids: Sequence[int], vocab: int) -> None:
     """Host id check of ``check_sequence`` (``src/backbone.jl:417-418``)."""
     host = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))

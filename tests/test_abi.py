@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 16, names
+    assert len(names) == 17, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -293,3 +293,15 @@ def test_attention_gate_validation():
     assert ga(None, F32, None, None, F32, 0, 4, 2, 8, 32, 16, 16) == 0
     assert ga(FAKE + 65536 + 32, F32, FAKE + 65536, FAKE + 131072, F32, 1, 4, 2, 8, 32, 16,
               16) == -5
+
+
+def test_copy_validation():
+    lib = _lib.lib()
+    f = lambda *a: lib.qdc_copy(*a, None)  # noqa: E731
+    assert f(FAKE, FAKE * 2, 24) == -2           # not a multiple of 16
+    assert f(FAKE, FAKE * 2, -16) == -2
+    assert f(FAKE + 8, FAKE * 2, 32) == -2       # misaligned destination
+    assert f(None, FAKE, 32) == -1
+    assert f(None, None, 0) == 0
+    assert f(FAKE, FAKE + 16, 64) == -5          # overlapping
+    assert f(FAKE, FAKE * 2, 1 << 37) == -2      # 2^33 chunks: grid over 2^32 work-items

@@ -894,3 +894,18 @@ def test_qk_norm_rope_head_major_output():
            O.qk_norm_rope(qgate[:, :, :hd], qn, cos, sin, rd, 1e-6, seq), torch.float32)
     report("k head-major", back(k_hm).transpose(1, 0, 2),
            O.qk_norm_rope(k, kn, cos, sin, rd, 1e-6, seq), torch.float32)
+
+
+def test_device_copy():
+    """The streaming copy the benchmark uses as its per-size ceiling moves
+    every byte (sizes not a multiple of a workgroup's 4 KB included)."""
+    from qdc_amd import ops
+    for nbytes in (16, 4096 + 48, 33_554_432):
+        src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=DEV)
+        dst = torch.zeros_like(src)
+        ops.device_copy(dst, src)
+        torch.cuda.synchronize()
+        assert torch.equal(dst, src), nbytes
+    with pytest.raises(ValueError):
+        ops.device_copy(torch.empty(32, dtype=torch.uint8, device=DEV),
+                        torch.empty(24, dtype=torch.uint8, device=DEV))
