@@ -4,13 +4,18 @@
 //
 // Fast path (head_dim a power-of-two number >= 2 of 16-byte chunks, at most
 // 128, rotary_dim/2 a multiple of the chunk): a group of LPR = chunks/2 lanes
-// owns one (token, head) row, two 16-byte chunks per lane.  The chunks are
-// dealt so that each of the first half/chunk lanes holds a whole rotation pair
-// (element i of the first rotary half and its partner i + half), so the
-// rotation needs no lane exchange and only those lanes read cos/sin.  The row
-// is normalised in registers; every input byte is read from HBM once and every
-// output byte written once.  cos/sin come from small fp32 tables (L2-resident)
-// built on the host exactly as the reference CPU path builds them.
+// owns up to 4 consecutive heads of one token, two 16-byte chunks of each row
+// per lane, so the position's cos/sin and the norm weights are loaded once for
+// all of them.  When the rotary block fits in the first chunk of each lane
+// (2*hc <= LPR, hc = rotary_dim/2 / chunk a power of two), lane l holds chunks
+// l and l + LPR (whole cache lines per load) and swaps its rotary chunk with
+// lane l ^ hc, which holds the other half of the rotation pair; otherwise the
+// chunks are dealt so that each of the first hc lanes holds a whole rotation
+// pair (element i of the first rotary half and its partner i + half) and the
+// rotation needs no exchange.  Rows are normalised in registers; every input
+// byte is read from HBM once and every output byte written once.  cos/sin come
+// from small fp32 tables (L2-resident) built on the host exactly as the
+// reference CPU path builds them.
 //
 // General path (any shape/alignment): one wavefront per row; the normalised
 // rotary block is staged in LDS so in-place operation stays correct.
@@ -52,31 +57,37 @@ template <int LPR> __device__ __forceinline__ int pair_chunk(int lane, int slot,
     return slot == 0 ? lane + hc : lane + LPR;
 }
 
-template <typename T, int LPR>
-__global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
+// One side (Q or K) of the fast kernel, pair-dealt chunks.  A group of LPR
+// lanes owns RPG consecutive heads of one token (heads % RPG == 0), so the
+// cos/sin of the token's position and the norm weights are loaded once for RPG
+// rows and every lane keeps 2*RPG row chunks in flight.
+template <typename T, int LPR, int RPG>
+__device__ __forceinline__ void qk_side_paired(const QKArgs<T> &a, const Side<T> &sd, int64_t block) {
     constexpr int V = Elem<T>::kVec;
-    constexpr int RPB = kBlock / LPR;
-    const bool is_k = (int64_t)blockIdx.x >= a.q_blocks;
-    const Side<T> &sd = is_k ? a.k : a.q;
-    const int64_t block = is_k ? (int64_t)blockIdx.x - a.q_blocks : (int64_t)blockIdx.x;
+    constexpr int GPB = kBlock / LPR;  // lane groups per workgroup
     const int lane = threadIdx.x % LPR;
-    const int64_t row = block * RPB + threadIdx.x / LPR;
-    const bool active = row < sd.rows;
+    const int64_t row0 = (block * GPB + threadIdx.x / LPR) * RPG;
+    const bool active = row0 < sd.rows;
     const int hc = a.half / V;  // chunks per half of the rotary block
     const bool rotary = lane < hc;
     const int c0 = pair_chunk<LPR>(lane, 0, hc), c1 = pair_chunk<LPR>(lane, 1, hc);
 
-    // Every load first: both chunks of the row, their norm weights and (rotary
+    // Every load first: both chunks of each row, the norm weights and (rotary
     // lanes) the cos/sin of the position, so the latencies overlap.
-    uint32_t t = 0, h = 0;
-    u32x4 x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
+    uint32_t t = 0, h0 = 0;
+    u32x4 x0[RPG], x1[RPG];
     u32x4 cr[V / 4], sr[V / 4];
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) x0[r] = x1[r] = u32x4{0u, 0u, 0u, 0u};
     if (active) {
-        t = fastdiv((uint32_t)row, sd.heads);
-        h = (uint32_t)row - t * sd.heads.d;
-        const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head;
-        x0 = load_stream(src + c0 * V);
-        x1 = load_stream(src + c1 * V);
+        t = fastdiv((uint32_t)row0, sd.heads);
+        h0 = (uint32_t)row0 - t * sd.heads.d;
+        const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h0 * sd.in_head;
+#pragma unroll
+        for (int r = 0; r < RPG; ++r) {
+            x0[r] = load_stream(src + r * sd.in_head + c0 * V);
+            x1[r] = load_stream(src + r * sd.in_head + c1 * V);
+        }
         if (rotary) {
             const uint32_t tq = fastdiv(t, a.seq_len);
             const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
@@ -90,40 +101,164 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
     }
     const u32x4 w0 = load_raw(sd.w + c0 * V), w1 = load_raw(sd.w + c1 * V);
 
-    float v0[V], v1[V];
-    unpack(x0, v0);
-    unpack(x1, v1);
-    float ss = 0.0f;
+    float v0[RPG][V], v1[RPG][V], ss[RPG];
 #pragma unroll
-    for (int j = 0; j < V; ++j) ss += v0[j] * v0[j];
+    for (int r = 0; r < RPG; ++r) {
+        unpack(x0[r], v0[r]);
+        unpack(x1[r], v1[r]);
+        ss[r] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < V; ++j) ss += v1[j] * v1[j];
-    ss = group_sum<LPR>(ss);
+        for (int j = 0; j < V; ++j) ss[r] += v0[r][j] * v0[r][j];
+#pragma unroll
+        for (int j = 0; j < V; ++j) ss[r] += v1[r][j] * v1[r][j];
+    }
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) ss[r] = group_sum<LPR>(ss[r]);
     if (!active) return;
-    const float s = rms_scale(ss, (float)a.dim, a.eps);
     float wv0[V], wv1[V];
     unpack(w0, wv0);
     unpack(w1, wv1);
+    T *dst = sd.out + (int64_t)t * sd.out_tok + (int64_t)h0 * sd.out_head;
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-        v0[j] = (v0[j] * s) * (1.0f + wv0[j]);
-        v1[j] = (v1[j] * s) * (1.0f + wv1[j]);
+    for (int r = 0; r < RPG; ++r) {
+        const float s = rms_scale(ss[r], (float)a.dim, a.eps);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            v0[r][j] = (v0[r][j] * s) * (1.0f + wv0[j]);
+            v1[r][j] = (v1[r][j] * s) * (1.0f + wv1[j]);
+        }
+        if (rotary) {  // v0 = first-half element i, v1 = its partner i + half
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 4 * q + e;
+                    const float c = __uint_as_float(cr[q][e]), sn = __uint_as_float(sr[q][e]);
+                    const float a0 = v0[r][j], b0 = v1[r][j];
+                    v0[r][j] = a0 * c - b0 * sn;
+                    v1[r][j] = b0 * c + a0 * sn;
+                }
+        }
+        store_chunk(dst + r * sd.out_head + c0 * V, v0[r]);
+        store_chunk(dst + r * sd.out_head + c1 * V, v1[r]);
     }
-    if (rotary) {  // v0 = first-half element i, v1 = its partner i + half
+}
+
+// One side, contiguous chunks (2*hc <= LPR, hc a power of two): lane l holds
+// chunks l and l + LPR, so each load instruction of a lane group covers whole
+// lines.  The rotary chunks are all in slot 0 of lanes [0, 2*hc); lane l and
+// lane l ^ hc hold the two halves of a rotation pair and swap their raw
+// chunks; each normalises the partner's chunk exactly as the partner does
+// (same row scale, same weights) before rotating its own.
+template <typename T, int LPR, int RPG>
+__device__ __forceinline__ void qk_side_contig(const QKArgs<T> &a, const Side<T> &sd, int64_t block) {
+    constexpr int V = Elem<T>::kVec;
+    constexpr int GPB = kBlock / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int64_t row0 = (block * GPB + threadIdx.x / LPR) * RPG;
+    const bool active = row0 < sd.rows;
+    const int hc = a.half / V;
+    const bool rotary = lane < 2 * hc;
+    const bool first = lane < hc;  // holds element i of the pair (else i + half)
+    const int c0 = lane, c1 = lane + LPR;
+    const int pc = lane ^ hc;      // the partner's chunk (rotary lanes)
+
+    uint32_t t = 0, h0 = 0;
+    u32x4 x0[RPG], x1[RPG];
+    u32x4 cr[V / 4], sr[V / 4];
 #pragma unroll
-        for (int q = 0; q < V / 4; ++q)
+    for (int r = 0; r < RPG; ++r) x0[r] = x1[r] = u32x4{0u, 0u, 0u, 0u};
+    if (active) {
+        t = fastdiv((uint32_t)row0, sd.heads);
+        h0 = (uint32_t)row0 - t * sd.heads.d;
+        const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h0 * sd.in_head;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 4 * q + e;
-                const float c = __uint_as_float(cr[q][e]), sn = __uint_as_float(sr[q][e]);
-                const float a0 = v0[j], b0 = v1[j];
-                v0[j] = a0 * c - b0 * sn;
-                v1[j] = b0 * c + a0 * sn;
+        for (int r = 0; r < RPG; ++r) {
+            x0[r] = load_stream(src + r * sd.in_head + c0 * V);
+            x1[r] = load_stream(src + r * sd.in_head + c1 * V);
+        }
+        if (rotary) {
+            const uint32_t tq = fastdiv(t, a.seq_len);
+            const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
+            const int64_t i0 = pos * a.half + (lane & (hc - 1)) * V;
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q) {
+                cr[q] = load_raw(a.cos + i0 + 4 * q);
+                sr[q] = load_raw(a.sin + i0 + 4 * q);
             }
+        }
     }
-    T *dst = sd.out + (int64_t)t * sd.out_tok + (int64_t)h * sd.out_head;
-    store_chunk(dst + c0 * V, v0);
-    store_chunk(dst + c1 * V, v1);
+    const u32x4 w0 = load_raw(sd.w + c0 * V), w1 = load_raw(sd.w + c1 * V);
+    const u32x4 wp = load_raw(sd.w + (rotary ? pc : c0) * V);
+
+    // the partner's raw slot-0 chunk (lane ^ hc stays inside the lane group)
+    u32x4 xp[RPG];
+#pragma unroll
+    for (int r = 0; r < RPG; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xp[r][e] = (uint32_t)__shfl_xor((int)x0[r][e], hc, kWave);
+
+    float v0[RPG][V], v1[RPG][V], ss[RPG];
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) {
+        unpack(x0[r], v0[r]);
+        unpack(x1[r], v1[r]);
+        ss[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) ss[r] += v0[r][j] * v0[r][j];
+#pragma unroll
+        for (int j = 0; j < V; ++j) ss[r] += v1[r][j] * v1[r][j];
+    }
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) ss[r] = group_sum<LPR>(ss[r]);
+    if (!active) return;
+    float wv0[V], wv1[V], wvp[V];
+    unpack(w0, wv0);
+    unpack(w1, wv1);
+    unpack(wp, wvp);
+    T *dst = sd.out + (int64_t)t * sd.out_tok + (int64_t)h0 * sd.out_head;
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) {
+        const float s = rms_scale(ss[r], (float)a.dim, a.eps);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            v0[r][j] = (v0[r][j] * s) * (1.0f + wv0[j]);
+            v1[r][j] = (v1[r][j] * s) * (1.0f + wv1[j]);
+        }
+        if (rotary) {
+            float p[V];
+            unpack(xp[r], p);
+#pragma unroll
+            for (int j = 0; j < V; ++j) p[j] = (p[j] * s) * (1.0f + wvp[j]);
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 4 * q + e;
+                    const float c = __uint_as_float(cr[q][e]), sn = __uint_as_float(sr[q][e]);
+                    v0[r][j] = first ? v0[r][j] * c - p[j] * sn : v0[r][j] * c + p[j] * sn;
+                }
+        }
+        store_chunk(dst + r * sd.out_head + c0 * V, v0[r]);
+        store_chunk(dst + r * sd.out_head + c1 * V, v1[r]);
+    }
+}
+
+// Q rows take workgroups [0, q_blocks), K rows the rest (block-uniform branch).
+template <typename T, int LPR, int RPGQ, int RPGK>
+__global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
+    const int hc = a.half / Elem<T>::kVec;
+    if (2 * hc <= LPR && (hc & (hc - 1)) == 0) {
+        if ((int64_t)blockIdx.x < a.q_blocks)
+            qk_side_contig<T, LPR, RPGQ>(a, a.q, (int64_t)blockIdx.x);
+        else
+            qk_side_contig<T, LPR, RPGK>(a, a.k, (int64_t)blockIdx.x - a.q_blocks);
+        return;
+    }
+    if ((int64_t)blockIdx.x < a.q_blocks)
+        qk_side_paired<T, LPR, RPGQ>(a, a.q, (int64_t)blockIdx.x);
+    else
+        qk_side_paired<T, LPR, RPGK>(a, a.k, (int64_t)blockIdx.x - a.q_blocks);
 }
 
 constexpr int kMaxGeneralRotary = 1024;
@@ -179,34 +314,63 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_general(QKArgs<T> a) {
     }
 }
 
+// Heads of one token per lane group: the largest of 4, 2, 1 that divides the
+// side's head count (4 measured ~5% faster than 1 on the 8 + 2 heads of 256
+// in bf16; 8 was slower).
+constexpr int kMaxRowsPerGroup = 4;
+int rows_per_group(int64_t heads) {
+    int r = 1;
+    while (2 * r <= kMaxRowsPerGroup && heads % (2 * r) == 0) r *= 2;
+    return r;
+}
+
+template <typename T, int LPR, int RPGQ, int RPGK>
+int32_t launch_fast(QKArgs<T> a, hipStream_t stream) {
+    constexpr int64_t gpb = kBlock / LPR;
+    a.q_blocks = ceil_div(a.q.rows / RPGQ, gpb);
+    const int64_t blocks = a.q_blocks + ceil_div(a.k.rows / RPGK, gpb);
+    hipLaunchKernelGGL((qk_norm_rope_fast<T, LPR, RPGQ, RPGK>), dim3((uint32_t)blocks),
+                       dim3(kBlock), 0, stream, a);
+    return launch_status();
+}
+
+template <typename T, int LPR>
+int32_t launch_lpr(QKArgs<T> a, int64_t heads, int64_t kv_heads, hipStream_t stream) {
+    const int rq = rows_per_group(heads), rk = rows_per_group(kv_heads);
+#define QDC_QK_R(RQ, RK) \
+    if (rq == RQ && rk == RK) return launch_fast<T, LPR, RQ, RK>(a, stream);
+    QDC_QK_R(1, 1)
+    QDC_QK_R(2, 1)
+    QDC_QK_R(1, 2)
+    QDC_QK_R(2, 2)
+    QDC_QK_R(4, 1)
+    QDC_QK_R(4, 2)
+    QDC_QK_R(1, 4)
+    QDC_QK_R(2, 4)
+    QDC_QK_R(4, 4)
+#undef QDC_QK_R
+    return QDC_ERR_SHAPE;  // unreachable: rows_per_group stays within the instantiated set
+}
+
 template <typename T>
-int32_t launch(QKArgs<T> a, bool fast, hipStream_t stream) {
+int32_t launch(QKArgs<T> a, int64_t heads, int64_t kv_heads, bool fast, hipStream_t stream) {
     constexpr int V = Elem<T>::kVec;
     const int64_t chunks = a.dim / V;
     // two chunks per lane: LPR = chunks / 2 lanes per row, a power of two <= 64
     const int64_t lpr = chunks / 2;
     if (fast && a.dim % V == 0 && a.half % V == 0 && chunks >= 2 && chunks % 2 == 0 && lpr <= kWave &&
         (lpr & (lpr - 1)) == 0) {
-        const int64_t rpb = kBlock / lpr;
-        a.q_blocks = ceil_div(a.q.rows, rpb);
-        const int64_t blocks = a.q_blocks + ceil_div(a.k.rows, rpb);
-#define QDC_QK(LPR)                                                                          \
-    case LPR:                                                                                \
-        hipLaunchKernelGGL((qk_norm_rope_fast<T, LPR>), dim3((uint32_t)blocks), dim3(kBlock), 0, \
-                           stream, a);                                                       \
-        return launch_status();
         switch (lpr) {
-            QDC_QK(1)
-            QDC_QK(2)
-            QDC_QK(4)
-            QDC_QK(8)
-            QDC_QK(16)
-            QDC_QK(32)
-            QDC_QK(64)
+            case 1: return launch_lpr<T, 1>(a, heads, kv_heads, stream);
+            case 2: return launch_lpr<T, 2>(a, heads, kv_heads, stream);
+            case 4: return launch_lpr<T, 4>(a, heads, kv_heads, stream);
+            case 8: return launch_lpr<T, 8>(a, heads, kv_heads, stream);
+            case 16: return launch_lpr<T, 16>(a, heads, kv_heads, stream);
+            case 32: return launch_lpr<T, 32>(a, heads, kv_heads, stream);
+            case 64: return launch_lpr<T, 64>(a, heads, kv_heads, stream);
             default:
                 break;
         }
-#undef QDC_QK
     }
     // the general kernel stages the rotary block of each row in LDS
     if (2 * a.half > kMaxGeneralRotary) return QDC_ERR_SHAPE;
@@ -338,7 +502,7 @@ extern "C" int32_t qdc_qk_norm_rope(void *q_out, void *k_out, const void *q_in, 
         a.half = (int32_t)(rotary_dim / 2);
         a.dim = (int32_t)head_dim;
         a.eps = eps;
-        return launch<T>(a, fast, stream);
+        return launch<T>(a, heads, kv_heads, fast, stream);
     };
     if (dtype == QDC_BF16) return fill((bf16_t *)nullptr);
     return fill((float *)nullptr);
