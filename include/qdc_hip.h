@@ -142,6 +142,8 @@ int32_t qdc_residual_rmsnorm_masked(void *residual, void *out, const void *x, co
  *   Q row (t, h), h < heads:    in  q_in  + t*q_in_tok  + h*q_in_head
  *                               out q_out + t*q_out_tok + h*q_out_head
  *   K row (t, g), g < kv_heads: likewise with k_*.
+ * Rows of a tensor must not overlap (token-major, or head-major
+ * (dim, tokens, heads) as the reference AMDGPU layout).
  * q_in_head = 2*head_dim reads q straight out of the interleaved q||gate
  * projection (src/backbone.jl:226-227).  For i < rotary_dim/2 the pair
  * (i, i+rotary_dim/2) is rotated by the angle of position
@@ -158,6 +160,30 @@ int32_t qdc_qk_norm_rope(void *q_out, void *k_out, const void *q_in, const void 
                          int64_t table_len, int64_t q_in_tok, int64_t q_in_head, int64_t q_out_tok,
                          int64_t q_out_head, int64_t k_in_tok, int64_t k_in_head, int64_t k_out_tok,
                          int64_t k_out_head, float eps, int32_t dtype, hipStream_t stream);
+
+/*
+ * qdc_qk_norm_rope over a batch of sequences in one launch, each output with
+ * its own stride between sequences: token t = s*seq_len + i (sequence s,
+ * position pos_offset + i) writes
+ *   Q row (t, h):  q_out + s*q_out_seq + i*q_out_tok + h*q_out_head
+ * and likewise K.  Inputs are addressed as in qdc_qk_norm_rope.  With
+ * q_out_seq = H*seq_len*head_dim, q_out_tok = head_dim and
+ * q_out_head = seq_len*head_dim the output is head-major per sequence,
+ * [batch, heads, seq_len, head_dim], the layout of batched attention
+ * products; q_out_seq = seq_len*q_out_tok is qdc_qk_norm_rope.  The reference
+ * runs one sequence per call (ext/amdgpu_attention.jl:108-147, output
+ * (dim, tokens, heads)); this entry point does the same work for a batch in
+ * one launch.  Arguments, checks and status otherwise as qdc_qk_norm_rope.
+ */
+int32_t qdc_qk_norm_rope_batched(void *q_out, void *k_out, const void *q_in, const void *k_in,
+                                 const void *q_norm, const void *k_norm, const float *cos_table,
+                                 const float *sin_table, int64_t tokens, int64_t heads,
+                                 int64_t kv_heads, int64_t head_dim, int64_t rotary_dim,
+                                 int64_t seq_len, int64_t pos_offset, int64_t table_len,
+                                 int64_t q_in_tok, int64_t q_in_head, int64_t q_out_seq,
+                                 int64_t q_out_tok, int64_t q_out_head, int64_t k_in_tok,
+                                 int64_t k_in_head, int64_t k_out_seq, int64_t k_out_tok,
+                                 int64_t k_out_head, float eps, int32_t dtype, hipStream_t stream);
 
 /*
  * Host-side RoPE tables, fp32 [n_pos, rotary_dim/2] each, built the way the

@@ -33,6 +33,7 @@ template <typename T> struct Side {
     T *out;
     const T *w;
     int64_t in_tok, in_head, out_tok, out_head;
+    int64_t out_seq;  // output stride between sequences of seq_len tokens
     int64_t rows;  // tokens * heads of this side
     FastDiv heads;
 };
@@ -74,7 +75,7 @@ __device__ __forceinline__ void qk_side_paired(const QKArgs<T> &a, const Side<T>
 
     // Every load first: both chunks of each row, the norm weights and (rotary
     // lanes) the cos/sin of the position, so the latencies overlap.
-    uint32_t t = 0, h0 = 0;
+    uint32_t t = 0, h0 = 0, tq = 0;  // token, first head, sequence
     u32x4 x0[RPG], x1[RPG];
     u32x4 cr[V / 4], sr[V / 4];
 #pragma unroll
@@ -82,6 +83,7 @@ __device__ __forceinline__ void qk_side_paired(const QKArgs<T> &a, const Side<T>
     if (active) {
         t = fastdiv((uint32_t)row0, sd.heads);
         h0 = (uint32_t)row0 - t * sd.heads.d;
+        tq = fastdiv(t, a.seq_len);
         const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h0 * sd.in_head;
 #pragma unroll
         for (int r = 0; r < RPG; ++r) {
@@ -89,7 +91,6 @@ __device__ __forceinline__ void qk_side_paired(const QKArgs<T> &a, const Side<T>
             x1[r] = load_stream(src + r * sd.in_head + c1 * V);
         }
         if (rotary) {
-            const uint32_t tq = fastdiv(t, a.seq_len);
             const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
             const int64_t i0 = pos * a.half + lane * V;
 #pragma unroll
@@ -118,7 +119,8 @@ __device__ __forceinline__ void qk_side_paired(const QKArgs<T> &a, const Side<T>
     float wv0[V], wv1[V];
     unpack(w0, wv0);
     unpack(w1, wv1);
-    T *dst = sd.out + (int64_t)t * sd.out_tok + (int64_t)h0 * sd.out_head;
+    T *dst = sd.out + (int64_t)tq * sd.out_seq + (int64_t)(t - tq * a.seq_len.d) * sd.out_tok +
+             (int64_t)h0 * sd.out_head;
 #pragma unroll
     for (int r = 0; r < RPG; ++r) {
         const float s = rms_scale(ss[r], (float)a.dim, a.eps);
@@ -163,7 +165,7 @@ __device__ __forceinline__ void qk_side_contig(const QKArgs<T> &a, const Side<T>
     const int c0 = lane, c1 = lane + LPR;
     const int pc = lane ^ hc;      // the partner's chunk (rotary lanes)
 
-    uint32_t t = 0, h0 = 0;
+    uint32_t t = 0, h0 = 0, tq = 0;  // token, first head, sequence
     u32x4 x0[RPG], x1[RPG];
     u32x4 cr[V / 4], sr[V / 4];
 #pragma unroll
@@ -171,6 +173,7 @@ __device__ __forceinline__ void qk_side_contig(const QKArgs<T> &a, const Side<T>
     if (active) {
         t = fastdiv((uint32_t)row0, sd.heads);
         h0 = (uint32_t)row0 - t * sd.heads.d;
+        tq = fastdiv(t, a.seq_len);
         const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h0 * sd.in_head;
 #pragma unroll
         for (int r = 0; r < RPG; ++r) {
@@ -178,7 +181,6 @@ __device__ __forceinline__ void qk_side_contig(const QKArgs<T> &a, const Side<T>
             x1[r] = load_stream(src + r * sd.in_head + c1 * V);
         }
         if (rotary) {
-            const uint32_t tq = fastdiv(t, a.seq_len);
             const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
             const int64_t i0 = pos * a.half + (lane & (hc - 1)) * V;
 #pragma unroll
@@ -216,7 +218,8 @@ __device__ __forceinline__ void qk_side_contig(const QKArgs<T> &a, const Side<T>
     unpack(w0, wv0);
     unpack(w1, wv1);
     unpack(wp, wvp);
-    T *dst = sd.out + (int64_t)t * sd.out_tok + (int64_t)h0 * sd.out_head;
+    T *dst = sd.out + (int64_t)tq * sd.out_seq + (int64_t)(t - tq * a.seq_len.d) * sd.out_tok +
+             (int64_t)h0 * sd.out_head;
 #pragma unroll
     for (int r = 0; r < RPG; ++r) {
         const float s = rms_scale(ss[r], (float)a.dim, a.eps);
@@ -284,9 +287,10 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_general(QKArgs<T> a) {
         const uint32_t t = fastdiv((uint32_t)row, sd.heads);
         const uint32_t h = (uint32_t)row - t * sd.heads.d;
         in += (int64_t)t * sd.in_tok + (int64_t)h * sd.in_head;
-        out += (int64_t)t * sd.out_tok + (int64_t)h * sd.out_head;
         const uint32_t tq = fastdiv(t, a.seq_len);
-        pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
+        const uint32_t sq = t - tq * a.seq_len.d;  // token within its sequence
+        out += (int64_t)tq * sd.out_seq + (int64_t)sq * sd.out_tok + (int64_t)h * sd.out_head;
+        pos = a.pos_offset + (int64_t)sq;
         float ss = 0.0f;
         for (int i = lane; i < dim; i += kWave) {
             const float v = to_f32(in[i]);
@@ -382,10 +386,140 @@ int32_t launch(QKArgs<T> a, int64_t heads, int64_t kv_heads, bool fast, hipStrea
     return launch_status();
 }
 
-// Byte extent of a strided [tokens, heads, dim] view.
-int64_t span_bytes(int64_t tokens, int64_t heads, int64_t dim, int64_t tok, int64_t head,
+// A side's rows in memory: up to three (extent, stride) dimensions in
+// elements (sequence, token within the sequence, head) over rows of head_dim
+// contiguous elements.
+struct Layout {
+    int64_t n[3], stride[3];
+};
+
+// Rows never overlap: with the dimensions of extent > 1 sorted by stride, each
+// stride reaches past everything the smaller ones span.
+bool disjoint_rows(const Layout &l, int64_t head_dim) {
+    int order[3], m = 0;
+    for (int d = 0; d < 3; ++d) {
+        if (l.n[d] <= 1) continue;
+        if (l.stride[d] < 0) return false;
+        order[m++] = d;
+    }
+    std::sort(order, order + m, [&](int x, int y) { return l.stride[x] < l.stride[y]; });
+    int64_t span = head_dim;
+    for (int i = 0; i < m; ++i) {
+        const int d = order[i];
+        if (l.stride[d] < span) return false;
+        span += (l.n[d] - 1) * l.stride[d];
+    }
+    return true;
+}
+
+// Token t of `tokens` lies in sequence t / seq_len at position t % seq_len.
+Layout side_layout(int64_t tokens, int64_t seq_len, int64_t heads, int64_t seq_stride,
+                   int64_t tok, int64_t head) {
+    const int64_t n_seq = (tokens + seq_len - 1) / seq_len;
+    return Layout{{n_seq, std::min(tokens, seq_len), heads}, {seq_stride, tok, head}};
+}
+
+// Byte extent of a side: one past the last element any row touches.
+int64_t span_bytes(int64_t tokens, int64_t seq_len, const Layout &l, int64_t head_dim,
                    int64_t es) {
-    return ((tokens - 1) * tok + (heads - 1) * head + dim) * es;
+    const int64_t last = tokens - 1, tq = last / seq_len;
+    int64_t far = tq * l.stride[0] + (last - tq * seq_len) * l.stride[1];
+    if (tq > 0) far = std::max(far, (tq - 1) * l.stride[0] + (seq_len - 1) * l.stride[1]);
+    return (far + (l.n[2] - 1) * l.stride[2] + head_dim) * es;
+}
+
+int32_t qk_norm_rope(void *q_out, void *k_out, const void *q_in, const void *k_in,
+                     const void *q_norm, const void *k_norm, const float *cos_table,
+                     const float *sin_table, int64_t tokens, int64_t heads, int64_t kv_heads,
+                     int64_t head_dim, int64_t rotary_dim, int64_t seq_len, int64_t pos_offset,
+                     int64_t table_len, int64_t q_in_tok, int64_t q_in_head, int64_t q_out_seq,
+                     int64_t q_out_tok, int64_t q_out_head, int64_t k_in_tok, int64_t k_in_head,
+                     int64_t k_out_seq, int64_t k_out_tok, int64_t k_out_head, float eps,
+                     int32_t dtype, hipStream_t stream) {
+    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
+    if (tokens < 0 || heads < 0 || kv_heads < 0 || head_dim <= 0 || rotary_dim < 0 ||
+        rotary_dim % 2 || rotary_dim > head_dim || seq_len <= 0 || pos_offset < 0 ||
+        table_len < 0)
+        return QDC_ERR_SHAPE;
+    // up to a wavefront per (token, head) row in a grid of fewer than 2^32 work-items
+    if (head_dim > INT32_MAX || seq_len >= ((int64_t)1 << 31) ||
+        tokens * (heads + kv_heads) >= ((int64_t)1 << 26))
+        return QDC_ERR_SHAPE;
+    if (tokens == 0 || (heads == 0 && kv_heads == 0)) return QDC_OK;
+    if (heads > 0 && (!q_out || !q_in || !q_norm)) return QDC_ERR_NULL;
+    if (kv_heads > 0 && (!k_out || !k_in || !k_norm)) return QDC_ERR_NULL;
+    if (rotary_dim > 0) {
+        if (!cos_table || !sin_table) return QDC_ERR_NULL;
+        if (pos_offset + std::min(tokens, seq_len) > table_len) return QDC_ERR_RANGE;
+    }
+    const int64_t es = elem_size(dtype);
+    // Inputs are [tokens, heads] row grids; outputs may also split the tokens
+    // into sequences of seq_len with their own stride.  Rows of a tensor must
+    // not overlap (token-major, head-major (dim, tokens, heads) as the
+    // reference AMDGPU layout, or head-major per sequence).
+    const Layout qil{{1, tokens, heads}, {0, q_in_tok, q_in_head}};
+    const Layout kil{{1, tokens, kv_heads}, {0, k_in_tok, k_in_head}};
+    const Layout qol = side_layout(tokens, seq_len, heads, q_out_seq, q_out_tok, q_out_head);
+    const Layout kol = side_layout(tokens, seq_len, kv_heads, k_out_seq, k_out_tok, k_out_head);
+    if ((heads && (!disjoint_rows(qil, head_dim) || !disjoint_rows(qol, head_dim))) ||
+        (kv_heads && (!disjoint_rows(kil, head_dim) || !disjoint_rows(kol, head_dim))))
+        return QDC_ERR_SHAPE;
+    struct View {
+        const void *p;
+        int64_t bytes;
+        Layout l;
+    };
+    auto view = [&](const void *p, int64_t n_heads, int64_t seq, const Layout &l) {
+        return View{p, n_heads ? span_bytes(tokens, seq, l, head_dim, es) : 0, l};
+    };
+    // an input's rows are one sequence of all the tokens
+    const View qi = view(q_in, heads, tokens, qil), ki = view(k_in, kv_heads, tokens, kil);
+    const View qo = view(q_out, heads, seq_len, qol), ko = view(k_out, kv_heads, seq_len, kol);
+    // An output may coincide exactly with its own input (in place: same
+    // pointer, and every row at the same place); any other overlap between an
+    // output and an input or the other output is rejected.
+    auto same_rows = [&](const View &o, const View &i) {
+        const int64_t n_seq = o.l.n[0];
+        return o.p == i.p && o.l.stride[1] == i.l.stride[1] && o.l.stride[2] == i.l.stride[2] &&
+               (n_seq <= 1 || o.l.stride[0] == seq_len * i.l.stride[1]);
+    };
+    auto clash = [&](const View &o, const View &i, bool own) {
+        if (own && same_rows(o, i)) return false;
+        return overlaps(o.p, o.bytes, i.p, i.bytes);
+    };
+    if (clash(qo, qi, true) || clash(qo, ki, false) || clash(ko, ki, true) ||
+        clash(ko, qi, false) || overlaps(qo.p, qo.bytes, ko.p, ko.bytes))
+        return QDC_ERR_ALIAS;
+
+    const bool fast = aligned16(q_out) && aligned16(q_in) && aligned16(q_norm) &&
+                      aligned16(k_out) && aligned16(k_in) && aligned16(k_norm) &&
+                      aligned16(cos_table) && aligned16(sin_table) &&
+                      ((q_in_tok | q_in_head | q_out_seq | q_out_tok | q_out_head | k_in_tok |
+                        k_in_head | k_out_seq | k_out_tok | k_out_head) *
+                       es) % 16 == 0 &&
+                      (rotary_dim / 2) % 4 == 0;
+    if (!fast && rotary_dim > kMaxGeneralRotary) return QDC_ERR_SHAPE;
+
+    auto fill = [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        QKArgs<T> a{};
+        a.q = Side<T>{(const T *)q_in, (T *)q_out, (const T *)q_norm, q_in_tok, q_in_head,
+                      q_out_tok, q_out_head, q_out_seq, tokens * heads,
+                      make_fastdiv((uint32_t)std::max<int64_t>(heads, 1))};
+        a.k = Side<T>{(const T *)k_in, (T *)k_out, (const T *)k_norm, k_in_tok, k_in_head,
+                      k_out_tok, k_out_head, k_out_seq, tokens * kv_heads,
+                      make_fastdiv((uint32_t)std::max<int64_t>(kv_heads, 1))};
+        a.cos = cos_table;
+        a.sin = sin_table;
+        a.seq_len = make_fastdiv((uint32_t)seq_len);
+        a.pos_offset = pos_offset;
+        a.half = (int32_t)(rotary_dim / 2);
+        a.dim = (int32_t)head_dim;
+        a.eps = eps;
+        return launch<T>(a, heads, kv_heads, fast, stream);
+    };
+    if (dtype == QDC_BF16) return fill((bf16_t *)nullptr);
+    return fill((float *)nullptr);
 }
 
 }  // namespace
@@ -423,87 +557,25 @@ extern "C" int32_t qdc_qk_norm_rope(void *q_out, void *k_out, const void *q_in, 
                                     int64_t q_out_tok, int64_t q_out_head, int64_t k_in_tok,
                                     int64_t k_in_head, int64_t k_out_tok, int64_t k_out_head,
                                     float eps, int32_t dtype, hipStream_t stream) {
-    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
-    if (tokens < 0 || heads < 0 || kv_heads < 0 || head_dim <= 0 || rotary_dim < 0 ||
-        rotary_dim % 2 || rotary_dim > head_dim || seq_len <= 0 || pos_offset < 0 ||
-        table_len < 0)
-        return QDC_ERR_SHAPE;
-    // up to a wavefront per (token, head) row in a grid of fewer than 2^32 work-items
-    if (head_dim > INT32_MAX || seq_len >= ((int64_t)1 << 31) ||
-        tokens * (heads + kv_heads) >= ((int64_t)1 << 26))
-        return QDC_ERR_SHAPE;
-    if (tokens == 0 || (heads == 0 && kv_heads == 0)) return QDC_OK;
-    if (heads > 0 && (!q_out || !q_in || !q_norm)) return QDC_ERR_NULL;
-    if (kv_heads > 0 && (!k_out || !k_in || !k_norm)) return QDC_ERR_NULL;
-    if (rotary_dim > 0) {
-        if (!cos_table || !sin_table) return QDC_ERR_NULL;
-        if (pos_offset + std::min(tokens, seq_len) > table_len) return QDC_ERR_RANGE;
-    }
-    const int64_t es = elem_size(dtype);
-    // Strides must keep the rows of a side apart: token-major (head stride >=
-    // head_dim, token stride spanning the heads) or head-major (token stride >=
-    // head_dim, head stride spanning the tokens, the reference AMDGPU layout
-    // (dim, tokens, heads)).  A stride of a dimension of extent 1 is unused.
-    auto strides_ok = [&](int64_t n, int64_t tok, int64_t head) {
-        if (n == 0) return true;
-        const bool token_major = (n == 1 || head >= head_dim) &&
-                                 (tokens == 1 || tok >= (n - 1) * head + head_dim);
-        const bool head_major = (tokens == 1 || tok >= head_dim) &&
-                                (n == 1 || head >= (tokens - 1) * tok + head_dim);
-        return token_major || head_major;
-    };
-    if (!strides_ok(heads, q_in_tok, q_in_head) || !strides_ok(heads, q_out_tok, q_out_head) ||
-        !strides_ok(kv_heads, k_in_tok, k_in_head) || !strides_ok(kv_heads, k_out_tok, k_out_head))
-        return QDC_ERR_SHAPE;
-    struct View {
-        const void *p;
-        int64_t bytes, tok, head;
-    };
-    const View qi{q_in, heads ? span_bytes(tokens, heads, head_dim, q_in_tok, q_in_head, es) : 0,
-                  q_in_tok, q_in_head};
-    const View qo{q_out, heads ? span_bytes(tokens, heads, head_dim, q_out_tok, q_out_head, es) : 0,
-                  q_out_tok, q_out_head};
-    const View ki{k_in, kv_heads ? span_bytes(tokens, kv_heads, head_dim, k_in_tok, k_in_head, es) : 0,
-                  k_in_tok, k_in_head};
-    const View ko{k_out,
-                  kv_heads ? span_bytes(tokens, kv_heads, head_dim, k_out_tok, k_out_head, es) : 0,
-                  k_out_tok, k_out_head};
-    // An output may coincide exactly with its own input (in place); any other
-    // overlap between an output and an input or the other output is rejected.
-    auto clash = [](const View &o, const View &i, bool own) {
-        if (own && o.p == i.p && o.tok == i.tok && o.head == i.head) return false;
-        return overlaps(o.p, o.bytes, i.p, i.bytes);
-    };
-    if (clash(qo, qi, true) || clash(qo, ki, false) || clash(ko, ki, true) ||
-        clash(ko, qi, false) || overlaps(qo.p, qo.bytes, ko.p, ko.bytes))
-        return QDC_ERR_ALIAS;
+    // one grid of token rows: sequence s starts at token s*seq_len (a stride
+    // that is only used when tokens > seq_len)
+    const bool several = seq_len > 0 && tokens > seq_len;
+    return qk_norm_rope(q_out, k_out, q_in, k_in, q_norm, k_norm, cos_table, sin_table, tokens,
+                        heads, kv_heads, head_dim, rotary_dim, seq_len, pos_offset, table_len,
+                        q_in_tok, q_in_head, several ? seq_len * q_out_tok : 0, q_out_tok,
+                        q_out_head, k_in_tok, k_in_head, several ? seq_len * k_out_tok : 0,
+                        k_out_tok, k_out_head, eps, dtype, stream);
+}
 
-    const bool fast = aligned16(q_out) && aligned16(q_in) && aligned16(q_norm) &&
-                      aligned16(k_out) && aligned16(k_in) && aligned16(k_norm) &&
-                      aligned16(cos_table) && aligned16(sin_table) &&
-                      ((q_in_tok | q_in_head | q_out_tok | q_out_head | k_in_tok | k_in_head |
-                        k_out_tok | k_out_head) *
-                       es) % 16 == 0 &&
-                      (rotary_dim / 2) % 4 == 0;
-    if (!fast && rotary_dim > kMaxGeneralRotary) return QDC_ERR_SHAPE;
-
-    auto fill = [&](auto *tag) {
-        using T = std::remove_pointer_t<decltype(tag)>;
-        QKArgs<T> a{};
-        a.q = Side<T>{(const T *)q_in, (T *)q_out, (const T *)q_norm, q_in_tok, q_in_head,
-                      q_out_tok, q_out_head, tokens * heads, make_fastdiv((uint32_t)std::max<int64_t>(heads, 1))};
-        a.k = Side<T>{(const T *)k_in, (T *)k_out, (const T *)k_norm, k_in_tok, k_in_head,
-                      k_out_tok, k_out_head, tokens * kv_heads,
-                      make_fastdiv((uint32_t)std::max<int64_t>(kv_heads, 1))};
-        a.cos = cos_table;
-        a.sin = sin_table;
-        a.seq_len = make_fastdiv((uint32_t)seq_len);
-        a.pos_offset = pos_offset;
-        a.half = (int32_t)(rotary_dim / 2);
-        a.dim = (int32_t)head_dim;
-        a.eps = eps;
-        return launch<T>(a, heads, kv_heads, fast, stream);
-    };
-    if (dtype == QDC_BF16) return fill((bf16_t *)nullptr);
-    return fill((float *)nullptr);
+extern "C" int32_t qdc_qk_norm_rope_batched(
+    void *q_out, void *k_out, const void *q_in, const void *k_in, const void *q_norm,
+    const void *k_norm, const float *cos_table, const float *sin_table, int64_t tokens,
+    int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t rotary_dim, int64_t seq_len,
+    int64_t pos_offset, int64_t table_len, int64_t q_in_tok, int64_t q_in_head, int64_t q_out_seq,
+    int64_t q_out_tok, int64_t q_out_head, int64_t k_in_tok, int64_t k_in_head, int64_t k_out_seq,
+    int64_t k_out_tok, int64_t k_out_head, float eps, int32_t dtype, hipStream_t stream) {
+    return qk_norm_rope(q_out, k_out, q_in, k_in, q_norm, k_norm, cos_table, sin_table, tokens,
+                        heads, kv_heads, head_dim, rotary_dim, seq_len, pos_offset, table_len,
+                        q_in_tok, q_in_head, q_out_seq, q_out_tok, q_out_head, k_in_tok, k_in_head,
+                        k_out_seq, k_out_tok, k_out_head, eps, dtype, stream);
 }

@@ -189,11 +189,10 @@ class QwenBackbone:
         tables = self.rope_tables(S) if cfg.rotary_dim else None
         q = torch.empty((B, H, S, hd), dtype=dt, device=self.device)
         k = torch.empty((B, KV, S, hd), dtype=dt, device=self.device)
-        for b in range(B):
-            rows = slice(b * S, (b + 1) * S)
-            ops.prepare_heads(qgate[rows, :, :hd], k_in[rows], layer["q_norm"], layer["k_norm"],
-                              tables, cfg.rotary_dim, cfg.eps, seq_len=S,
-                              q_out=q[b].permute(1, 0, 2), k_out=k[b].permute(1, 0, 2))
+        # all sequences in one launch, written head-major per sequence
+        ops.prepare_heads(qgate[:, :, :hd], k_in, layer["q_norm"], layer["k_norm"], tables,
+                          cfg.rotary_dim, cfg.eps, seq_len=S, q_out=q.permute(0, 2, 1, 3),
+                          k_out=k.permute(0, 2, 1, 3))
         kt = k.transpose(-1, -2).contiguous().view(B * KV, hd, S)
         vh = v.view(B, S, KV, hd).permute(0, 2, 1, 3).contiguous().view(B * KV, S, hd)
         scores = self._bmm32(q.view(B * KV, G * S, hd), kt)          # [B*KV, G*S, S] fp32

@@ -249,39 +249,58 @@ def prepare_heads(q: torch.Tensor | None, k: torch.Tensor | None, q_norm, k_norm
     ``q`` ``[tokens, heads, head_dim]`` and ``k`` ``[tokens, kv_heads, head_dim]``
     are (possibly strided) views: ``qgate.view(T, H, 2*hd)[:, :, :hd]`` reads q
     straight out of the q||gate projection.  Token ``t`` uses position
-    ``pos_offset + t % seq_len``.  Returns ``(q_out, k_out)`` (contiguous unless
-    given)."""
+    ``pos_offset + t % seq_len``.  ``q_out``/``k_out`` are ``[tokens, heads,
+    head_dim]`` views, or ``[batch, seq_len, heads, head_dim]`` views splitting
+    the tokens into sequences (``x.permute(0, 2, 1, 3)`` of a ``[batch, heads,
+    seq_len, head_dim]`` tensor writes the head-major per-sequence layout of
+    batched attention products in the same single launch).  Returns
+    ``(q_out, k_out)`` (contiguous ``[tokens, heads, head_dim]`` unless given)."""
     ref = q if q is not None else k
     if ref is None:
         raise ValueError("q or k required")
     tokens, _, head_dim = ref.shape
     seq_len = max(tokens, 1) if seq_len is None else seq_len
     cos, sin = tables if rotary_dim else (None, None)
+    batched = any(o is not None and o.dim() == 4 for o in (q_out, k_out))
 
     def side(x, norm, out):
         if x is None:
-            return None, None, 0, (0, 0, 0, 0)
+            return None, None, 0, (0, 0, 0, 0, 0)
         _device(x, norm)
         if x.dim() != 3 or x.shape[0] != tokens or x.shape[2] != head_dim or x.stride(2) != 1:
             raise ValueError("q/k must be [tokens, heads, head_dim] with contiguous rows")
         if out is None:
             out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-        if out.shape != x.shape or out.stride(2) != 1:
-            raise ValueError("q_out/k_out must match q/k")
-        return x, out, x.shape[1], (x.stride(0), x.stride(1), out.stride(0), out.stride(1))
+        if out.dim() == 4:
+            n_seq = -(-tokens // seq_len)
+            if (out.shape[0] * out.shape[1] != tokens or out.shape[2:] != x.shape[1:]
+                    or out.stride(3) != 1 or (n_seq > 1 and out.shape[1] != seq_len)):
+                raise ValueError("a 4-D q_out/k_out must be [batch, seq_len, heads, head_dim]")
+            seq_stride, tok, head = out.stride(0), out.stride(1), out.stride(2)
+        else:
+            if out.shape != x.shape or out.stride(2) != 1:
+                raise ValueError("q_out/k_out must match q/k")
+            tok, head = out.stride(0), out.stride(1)
+            seq_stride = seq_len * tok if tokens > seq_len else 0
+        return x, out, x.shape[1], (x.stride(0), x.stride(1), seq_stride, tok, head)
 
     qi, qo, heads, qs = side(q, q_norm, q_out)
     ki, ko, kv_heads, ks = side(k, k_norm, k_out)
     code = _dtype_code(*[t for t in (qi, ki, q_norm if qi is not None else None,
                                      k_norm if ki is not None else None) if t is not None])
     ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
-    check(lib().qdc_qk_norm_rope(ptr(qo), ptr(ko), ptr(qi), ptr(ki),
-                                 ptr(q_norm if qi is not None else None),
-                                 ptr(k_norm if ki is not None else None),
-                                 ptr(cos) if rotary_dim else 0, ptr(sin) if rotary_dim else 0,
-                                 tokens, heads, kv_heads, head_dim, rotary_dim, seq_len,
-                                 pos_offset, cos.shape[0] if rotary_dim else 0, *qs, *ks, eps,
-                                 code, _stream(ref)), "prepare_heads")
+    head_args = (ptr(qo), ptr(ko), ptr(qi), ptr(ki), ptr(q_norm if qi is not None else None),
+                 ptr(k_norm if ki is not None else None),
+                 ptr(cos) if rotary_dim else 0, ptr(sin) if rotary_dim else 0,
+                 tokens, heads, kv_heads, head_dim, rotary_dim, seq_len,
+                 pos_offset, cos.shape[0] if rotary_dim else 0)
+    if batched:
+        check(lib().qdc_qk_norm_rope_batched(*head_args, *qs, *ks, eps, code, _stream(ref)),
+              "prepare_heads")
+    else:  # one grid of token rows: the reference-shaped entry point
+        flat = lambda s: (s[0], s[1], s[3], s[4])  # noqa: E731
+        check(lib().qdc_qk_norm_rope(*head_args, *flat(qs), *flat(ks), eps, code, _stream(ref)),
+              "prepare_heads")
     return qo, ko
 
 

@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 17, names
+    assert len(names) == 18, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -177,6 +177,35 @@ def test_qk_norm_rope_validation():
     assert f(tokens=0) == 0
     # q rows + k rows < 2^26 (up to a wavefront per row, fewer than 2^32 work-items)
     assert f(tokens=1 << 24, kv=2, ks=(32, 16, 32, 16)) == -2
+
+
+def test_qk_norm_rope_batched_validation():
+    """Output strides per sequence: rows of a tensor may not overlap, an
+    output may replace its input only row for row, and sequences laid out
+    head-major per sequence ([batch, heads, seq, head_dim]) are accepted."""
+    lib = _lib.lib()
+    Q, K, QI, KI, QN, KN, C, S = (FAKE * i for i in range(1, 9))
+    B, L, H, KV, hd = 3, 4, 2, 1, 16
+    # head-major per sequence: (seq, tok, head) strides
+    qhm, khm = (H * L * hd, hd, L * hd), (KV * L * hd, hd, L * hd)
+
+    def f(tokens=B * L, qs=(2 * H * hd, 2 * hd) + qhm, ks=(hd, hd) + khm, q=Q, k=K, qi=QI,
+          ki=KI, seq=L, dtype=F32):
+        return lib.qdc_qk_norm_rope_batched(q, k, qi, ki, QN, KN, C, S, tokens, H, KV, hd, 8, seq,
+                                            0, L, *qs, *ks, 1e-6, dtype, None)
+    # a grid that would launch is not called here: only rejected layouts
+    assert f(dtype=4) == -3
+    assert f(qs=(2 * H * hd, 2 * hd, H * L * hd - 1, hd, L * hd)) == -2  # sequences overlap
+    assert f(qs=(2 * H * hd, 2 * hd, H * L * hd, hd, hd)) == -2  # heads overlap tokens
+    assert f(ks=(hd, hd, 0, hd, L * hd)) == -2  # every sequence on the first
+    assert f(k=Q + 4 * (H * L * hd - 1)) == -5  # k output inside the q output
+    assert f(q=QI) == -5  # not the same rows as the input: rejected in place
+    assert f(tokens=0) == 0
+    # the flat entry point's checks agree with a sequence stride of seq_len * token stride
+    flat = lib.qdc_qk_norm_rope(Q, K, QI, KI, QN, KN, C, S, B * L, H, KV, hd, 8, L, 0, L,
+                                2 * H * hd, 2 * hd, hd, B * L * hd - 1, hd, hd, hd, hd,
+                                1e-6, F32, None)
+    assert flat == -2  # q heads overlap (head stride below the token span)
 
 
 def test_delta_scan_validation():

@@ -897,6 +897,41 @@ def test_qk_norm_rope_head_major_output():
            O.qk_norm_rope(k, kn, cos, sin, rd, 1e-6, seq), torch.float32)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,S,H,KV,hd,rd", [(8, 2048, 8, 2, 256, 64), (3, 37, 4, 1, 64, 16),
+                                            (2, 9, 2, 2, 128, 128), (3, 5, 3, 1, 96, 24)])
+def test_qk_norm_rope_batched_head_major(dtype, B, S, H, KV, hd, rd):
+    """All sequences of a batch in one launch, written head-major per sequence
+    ([B, H, S, hd], the layout of the batched attention products): each
+    sequence equals the one-sequence call bit for bit (the reference runs one
+    sequence per call) and matches the oracle.  Cases cover the contiguous and
+    pair-dealt fast kernels and the general kernel (head_dim 96)."""
+    from qdc_amd import ops
+    T = B * S
+    qgate = host((T, H, 2 * hd), 75, 1.0, dtype)
+    k = host((T, KV, hd), 76, 1.0, dtype)
+    qn, kn = host((hd,), 77, 0.02, dtype), host((hd,), 78, 0.02, dtype)
+    tables = ops.rope_tables(S, rd, 1e6, DEV)
+    qg, kk = dev(qgate, dtype), dev(k, dtype)
+    qw, kw = dev(qn, dtype), dev(kn, dtype)
+    q_hm = torch.full((B, H, S, hd), float("nan"), dtype=dtype, device=DEV)
+    k_hm = torch.full((B, KV, S, hd), float("nan"), dtype=dtype, device=DEV)
+    ops.prepare_heads(qg[:, :, :hd], kk, qw, kw, tables, rd, 1e-6, seq_len=S,
+                      q_out=q_hm.permute(0, 2, 1, 3), k_out=k_hm.permute(0, 2, 1, 3))
+    for b in range(B):
+        rows = slice(b * S, (b + 1) * S)
+        qo, ko = ops.prepare_heads(qg[rows, :, :hd], kk[rows], qw, kw, tables, rd, 1e-6,
+                                   seq_len=S)
+        assert torch.equal(q_hm[b].permute(1, 0, 2), qo), b
+        assert torch.equal(k_hm[b].permute(1, 0, 2), ko), b
+    cos, sin = O.rope_tables(S, rd, 1e6)
+    take = slice(0, min(T, 4096))  # oracle on the first sequences only
+    got_q = back(q_hm).transpose(0, 2, 1, 3).reshape(T, H, hd)[take]
+    got_k = back(k_hm).transpose(0, 2, 1, 3).reshape(T, KV, hd)[take]
+    report("q batched", got_q, O.qk_norm_rope(qgate[take, :, :hd], qn, cos, sin, rd, 1e-6, S), dtype)
+    report("k batched", got_k, O.qk_norm_rope(k[take], kn, cos, sin, rd, 1e-6, S), dtype)
+
+
 def test_device_copy():
     """The streaming copy the benchmark uses as its per-size ceiling moves
     every byte (sizes not a multiple of a workgroup's 4 KB included)."""
