@@ -95,25 +95,43 @@ __device__ __forceinline__ void store_chunk(float *p, const float (&v)[4]) { sto
 __device__ __forceinline__ void store_chunk(bf16_t *p, const float (&v)[8]) { store_raw(p, pack(v)); }
 
 // ----------------------------------------------- V-element fragments ---
-// V consecutive elements of type T (V*sizeof(T) bytes, a multiple of 16) held
-// as raw 16-byte vectors; lets one kernel mix fp32 and bf16 tensors at the
-// same element granularity (8 bf16 = 1 load, 8 fp32 = 2 loads).
+// V consecutive elements of type T held as raw vectors: whole 16-byte chunks,
+// or one 8-byte piece (4 bf16).  Lets one kernel mix fp32 and bf16 tensors at
+// the same element granularity: at 4 elements per lane an fp32 tensor moves in
+// 16-byte chunks and a bf16 tensor in 8-byte pieces, so every load or store
+// instruction of a wavefront covers one contiguous span (8 elements per lane
+// would split each fp32 group over two 16-byte accesses 32 bytes apart).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 template <typename T, int V> struct Frag {
-    static constexpr int kN = V * (int)sizeof(T) / 16;
-    static_assert(kN >= 1 && kN * 16 == V * (int)sizeof(T), "fragment must be whole 16-byte chunks");
+    static constexpr int kBytes = V * (int)sizeof(T);
+    static constexpr bool kHalf = kBytes == 8;  // one 8-byte piece in r[0].xy
+    static constexpr int kN = kHalf ? 1 : kBytes / 16;
+    static_assert(kHalf || (kN >= 1 && kN * 16 == kBytes),
+                  "fragment must be an 8-byte piece or whole 16-byte chunks");
     u32x4 r[kN];
 };
 
 template <typename T, int V> __device__ __forceinline__ Frag<T, V> load_frag(const T *p) {
     Frag<T, V> f;
+    if constexpr (Frag<T, V>::kHalf) {
+        const u32x2 h = *reinterpret_cast<const u32x2 *>(p);
+        f.r[0] = u32x4{h[0], h[1], 0u, 0u};
+    } else {
 #pragma unroll
-    for (int i = 0; i < Frag<T, V>::kN; ++i) f.r[i] = load_raw(p + i * (16 / (int)sizeof(T)));
+        for (int i = 0; i < Frag<T, V>::kN; ++i) f.r[i] = load_raw(p + i * (16 / (int)sizeof(T)));
+    }
     return f;
 }
 template <typename T, int V> __device__ __forceinline__ Frag<T, V> stream_frag(const T *p) {
     Frag<T, V> f;
+    if constexpr (Frag<T, V>::kHalf) {
+        const u32x2 h = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+        f.r[0] = u32x4{h[0], h[1], 0u, 0u};
+    } else {
 #pragma unroll
-    for (int i = 0; i < Frag<T, V>::kN; ++i) f.r[i] = load_stream(p + i * (16 / (int)sizeof(T)));
+        for (int i = 0; i < Frag<T, V>::kN; ++i) f.r[i] = load_stream(p + i * (16 / (int)sizeof(T)));
+    }
     return f;
 }
 template <int V> __device__ __forceinline__ void unpack(const Frag<float, V> &f, float (&v)[V]) {
@@ -138,12 +156,17 @@ template <int V> __device__ __forceinline__ void store_frag(float *p, const floa
     }
 }
 template <int V> __device__ __forceinline__ void store_frag(bf16_t *p, const float (&v)[V]) {
+    if constexpr (V == 4) {  // one 8-byte piece
+        const u32x2 h = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        __builtin_nontemporal_store(h, reinterpret_cast<u32x2 *>(p));
+    } else {
 #pragma unroll
-    for (int i = 0; i < V / 8; ++i) {
-        u32x4 r;
+        for (int i = 0; i < V / 8; ++i) {
+            u32x4 r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = pack_bf16x2(v[8 * i + 2 * e], v[8 * i + 2 * e + 1]);
-        store_raw(p + 8 * i, r);
+            for (int e = 0; e < 4; ++e) r[e] = pack_bf16x2(v[8 * i + 2 * e], v[8 * i + 2 * e + 1]);
+            store_raw(p + 8 * i, r);
+        }
     }
 }
 

@@ -8,12 +8,15 @@
 // The supported mixes keep the residual stream in fp32 while the activations
 // fed to the GEMMs are bf16.
 //
-// Fast path: a row is split into G = width/V groups of V elements (V = 4 when
-// every tensor is fp32, else 8, so a group of any tensor is whole 16-byte
-// chunks).  A set of LPR lanes owns a row; lane l holds groups l, l+LPR, ...
-// (CPL groups), so each load instruction of the set covers one contiguous
-// segment.  All loads of a row (x, mixed, gate, weights) are issued before the
-// first dependent instruction; streamed inputs use nontemporal loads.  The row
+// Fast path: a row is split into G = width/V groups of V elements (V = 8 when
+// every tensor is bf16, a 16-byte chunk; else 4: a 16-byte chunk of an fp32
+// tensor, an 8-byte piece of a bf16 one; 8 elements of a mixed fp32/bf16 row
+// per lane split each fp32 group over two accesses 32 bytes apart, which
+// measured 12% slower with 7% more bytes written).  A set of LPR lanes owns a
+// row; lane l holds groups l, l+LPR, ... (CPL groups), so each load or store
+// instruction of the set covers one contiguous segment of every tensor.  All
+// loads of a row (x, mixed, gate, weights) are issued before the first
+// dependent instruction; streamed inputs use nontemporal loads.  The row
 // stays in registers: HBM sees each input byte read once and each output byte
 // written once.  The sum of squares is reduced across the LPR lanes (DPP inside
 // 16-lane rows, lane swaps across them); 64/LPR rows share a wavefront, 4
@@ -43,8 +46,10 @@ struct RowMap {
     int64_t o_tok, o_head;  // output (and residual output)
 };
 
+// 8 elements (one 16-byte chunk) per group when every tensor is bf16, else 4
+// (16-byte fp32 chunks, 8-byte bf16 pieces)
 template <typename TX, typename TM, typename TO> constexpr int group_elems() {
-    return (sizeof(TX) == 4 && sizeof(TM) == 4 && sizeof(TO) == 4) ? 4 : 8;
+    return (sizeof(TX) == 2 && sizeof(TM) == 2 && sizeof(TO) == 2) ? 8 : 4;
 }
 
 template <typename TX, typename TM, typename TO, int LPR, int CPL, Mode M, bool CENTERED>
@@ -200,16 +205,18 @@ int32_t launch_fast(const Args &a, hipStream_t stream) {
 
 // Fast-path shapes by G = groups per row: a lane holds 2 groups for rows of up
 // to 64 groups and 4 groups for 128- and 256-group rows (8 for plain all-bf16
-// 128-group rows; the splits that measured fastest on MI355X); wider rows use
-// all 64 lanes with G/64 groups each.  kNoFastPath when no instantiation matches.
+// 128-group rows; the splits that measured fastest on MI355X, 32 x 8 and
+// 16 x 16 were not faster for the 256-group fp32-to-bf16 rows); wider rows use
+// all 64 lanes with G/64 groups each.  kNoFastPath when no instantiation
+// matches.
 template <typename TX, typename TM, typename TO, Mode M, bool C>
 int32_t dispatch_fast(const Args &a, hipStream_t stream) {
     constexpr int V = group_elems<TX, TM, TO>();
     if (a.width % V) return kNoFastPath;
     // Plain all-bf16 rows of 128 groups (width 1024): 16 lanes x 8 groups, 16
     // rows per workgroup, measured ~5% faster than 32 x 4 (more bytes in flight
-    // per wavefront at occupancy 3); the residual and mixed-type rows measured
-    // no gain and keep 32 x 4.
+    // per wavefront at occupancy 3); the all-bf16 residual rows measured no
+    // gain and keep 32 x 4.
     if constexpr (M == Mode::kPlain && sizeof(TX) == 2 && sizeof(TO) == 2) {
         if (a.width / V == 128) return launch_fast<TX, TM, TO, 16, 8, M, C>(a, stream);
     }
