@@ -98,9 +98,11 @@ def masks(n, rng):
             "zeros": np.zeros(n, np.int64)}
 
 
-@pytest.mark.parametrize("n", [1, 9, 64, 65, 128])
+@pytest.mark.parametrize("n", [1, 9, 63, 64, 65, 128, 129, 256, 257])
 def test_plumbing_backbone_fp32(n):
-    """2-layer hidden-256 backbone with rotary 16 of 64 at theta 1e7."""
+    """2-layer hidden-256 backbone with rotary 16 of 64 at theta 1e7, at the
+    reference hardware suite's lengths (test/cuda.jl: 1, 9, 63, 64, 65, 129, 256,
+    257) and masks with and without holes; backbone_last_hidden is the last row."""
     from qdc_amd import backbone
     from qdc_amd.config import plumbing_config
     from qdc_amd.weights import random_weights
@@ -115,6 +117,8 @@ def test_plumbing_backbone_fp32(n):
         err = normwise(got, exp)
         print(f"plumbing fp32 n={n} {tag}: {err:.2e}", flush=True)
         assert err <= 1e-5, (n, tag, err)
+        last = backbone.backbone_last_hidden(model, ids, mask)
+        assert normwise(last, exp[-1]) <= 1e-5, (n, tag)
 
 
 def bf16_weights(weights):
