@@ -736,6 +736,10 @@ def main():
              "us": round(k.avg_ms * 1e3, 3),
              "gbs": round(k.algo_bytes / (k.avg_ms / 1e3) / 1e9, 1),
              "pct_peak": round(100 * k.algo_bytes / (k.avg_ms / 1e3) / 1e9 / PEAK_GBS, 1)}
+        t = load_traffic(k.name)
+        if t is not None:  # HBM bytes per launch counted by rocprofv3 (FETCH_SIZE + WRITE_SIZE)
+            e.update(hbm_bytes_counted=t,
+                     hbm_gbs_counted=round(t / (k.avg_ms / 1e3) / 1e9, 1))
         c = ceilings.get(k.name)
         if c is not None:  # the same bytes as one plain streaming copy launch
             copy_gbs = c.algo_bytes / (c.avg_ms / 1e3) / 1e9
