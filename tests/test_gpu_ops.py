@@ -130,6 +130,7 @@ QK_CASES = [
     (9, 3, 1, 16, 16, 5, 1e4),          # two bf16 chunks per row: one lane per row
     (7, 2, 1, 24, 16, 7, 1e4),          # odd chunk count: general kernel
     (21, 4, 2, 256, 48, 7, 1e6),        # rotary chunks not a power of two: pair-dealt lanes
+    (37, 8, 2, 256, 64, 16, 1e7),       # 0.8B heads, sequences of 16 with a partial last one
 ]
 
 
