@@ -201,6 +201,11 @@ def test_qk_norm_rope_batched_validation():
     assert f(k=Q + 4 * (H * L * hd - 1)) == -5  # k output inside the q output
     assert f(q=QI) == -5  # not the same rows as the input: rejected in place
     assert f(tokens=0) == 0
+    # partial last sequence: the q output's extent ends at the last head of its last
+    # sequence's third token; a k output starting one element before that end overlaps
+    T = 2 * L + 3
+    far = max(2 * qhm[0] + 2 * qhm[1], qhm[0] + (L - 1) * qhm[1]) + (H - 1) * qhm[2] + hd
+    assert f(tokens=T, k=Q + 4 * (far - 1)) == -5
     # the flat entry point's checks agree with a sequence stride of seq_len * token stride
     flat = lib.qdc_qk_norm_rope(Q, K, QI, KI, QN, KN, C, S, B * L, H, KV, hd, 8, L, 0, L,
                                 2 * H * hd, 2 * hd, hd, B * L * hd - 1, hd, hd, hd, hd,
