@@ -251,6 +251,11 @@ __global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
 // outputs in two.
 constexpr int kC = 16;        // tokens per chunk: one MFMA tile edge
 constexpr int kRowsWG = 64;   // value rows per workgroup, 16 per row tile
+// LDS row stride of the v and output tiles: the four 16-lane groups of a
+// wavefront read or write rows 4(l/16) + j, which 4 pad floats put on disjoint
+// banks (an unpadded 64-float row put all four on the same banks; the padding
+// measured 1-2.5% faster at the 0.8B shapes)
+constexpr int kVS = kRowsWG + 4;
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -285,15 +290,18 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
     constexpr int kHelper = NT / kWave - 1;  // wavefront forming the inverse
     __shared__ __align__(16) float sK[NB][kC][KS];
     __shared__ __align__(16) float sQ[NB][kC][KS];
-    __shared__ __align__(16) float sV[NB][kC][kRowsWG];
+    __shared__ __align__(16) float sV[NB][kC][kVS];
     // per token: beta, the running log-decay sum g, e^g and e^(g_15 - g)
     __shared__ float sBeta[NB][kC], sG[NB][kC], sEg[NB][kC], sEt[NB][kC];
     __shared__ __align__(16) float sA[kC][kC];   // read as whole rows by the inverse
-    __shared__ float sProd[4][kC][MS];           // K K^T and Q K^T, two key halves each
+    // written and read as rows 4(l/16) + j by the 16-lane groups: a row stride of
+    // 20 puts the four groups on disjoint banks
+    constexpr int RS = kC + 4;
+    __shared__ float sProd[4][kC][RS];           // K K^T and Q K^T, two key halves each
     __shared__ float sP[2][kC][MS], sTb[kC][MS];
     __shared__ float sT[kC][MS];                 // diagonal blocks of T (inverse)
-    __shared__ float sO[2][kC][kRowsWG + 1];
-    __shared__ float sPart[KSPLIT > 1 ? 2 * KSPLIT * 4 : 1][kC][kC + 1];  // Z / Q S0^T halves
+    __shared__ float sO[2][kC][kVS];
+    __shared__ float sPart[KSPLIT > 1 ? 2 * KSPLIT * 4 : 1][kC][RS];  // Z / Q S0^T halves
 
     const int tid = threadIdx.x;
     const int wv = tid / kWave, l = tid % kWave, lr = l % 16, lg = l / 16;
@@ -464,7 +472,7 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
     // outputs of chunk cw (rows of sO[cw & 1]) to memory, by threads 0..nt-1
     auto write_out = [&](int cw, int nt) {
         const int n = min(kC, S - cw * kC);
-        const float(*so)[kRowsWG + 1] = sO[cw & 1];
+        const float(*so)[kVS] = sO[cw & 1];
         for (int e = tid; e < kC * kRowsWG; e += nt) {
             const int tt = e / kRowsWG, r = e - tt * kRowsWG;
             if (tt < n && row0 + r < a.vd)
