@@ -85,8 +85,12 @@ def _store(x, bf16):
 
 
 def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, tables,
-                   bf16: bool = False):
-    """``full_attention`` (``src/backbone.jl:224-262``) on ``x [T, hidden]``."""
+                   bf16: bool = False, trace: dict | None = None):
+    """``full_attention`` (``src/backbone.jl:224-262``) on ``x [T, hidden]``.
+
+    ``trace``, when given, receives the intermediates under the names of the
+    stages (``qgate``, ``k_proj``, ``v``, ``q``, ``k``, ``scores``, ``probs``,
+    ``values``, ``merged``, ``mixed``), each as stored."""
     T = x.shape[0]
     hd, H, KV = cfg["head_dim"], cfg["heads"], cfg["kv_heads"]
     qgate = _store(_linear(x, W[p + "self_attn.q_proj.weight"]), bf16).reshape(T, H, 2 * hd)
@@ -108,8 +112,12 @@ def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, 
     probs = _store(attention_softmax(scores[None], mask[None], F32(1) / np.sqrt(F32(hd)))[0],
                    bf16)
     values = (probs @ vh).astype(F32)                           # [H, query, hd]
-    out = attention_gate(values[None], qgate[:, :, hd:])
-    return _linear(_store(out, bf16), W[p + "self_attn.o_proj.weight"])
+    merged = _store(attention_gate(values[None], qgate[:, :, hd:]), bf16)
+    mixed = _linear(merged, W[p + "self_attn.o_proj.weight"])
+    if trace is not None:
+        trace.update(qgate=qgate, k_proj=kp, v=v, q=q, k=k, scores=scores, probs=probs,
+                     values=values, merged=merged, mixed=mixed)
+    return mixed
 
 
 def attention_softmax(scores: np.ndarray, mask, scale, q_offset: int = 0) -> np.ndarray:
@@ -153,13 +161,16 @@ def causal_depthwise(x: np.ndarray, w: np.ndarray) -> np.ndarray:
 
 
 def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
-                    bf16: bool = False):
+                    bf16: bool = False, trace: dict | None = None):
     """Gated DeltaNet, recurrent form of the CPU default path.
 
     ``cpu_delta_prepare`` (``src/backbone_cpu.jl:465-499``) and
     ``cpu_delta_recurrent_heads!`` / ``cpu_delta_recurrent_step!``
     (``src/backbone_cpu.jl:680-759``), which equals the chunked generic form
-    ``delta_attention`` (``src/backbone.jl:284-345``) up to rounding."""
+    ``delta_attention`` (``src/backbone.jl:284-345``) up to rounding.
+    ``trace``, when given, receives the intermediates (``masked``, ``qkv``,
+    ``z``, ``a``, ``b``, ``q``, ``k``, ``v``, ``beta``, ``decay``,
+    ``recurrence`` (fp32), ``result`` (stored), ``gated``, ``mixed``)."""
     T = x.shape[0]
     kd, kh, vd, vh = cfg["key_dim"], cfg["key_heads"], cfg["value_dim"], cfg["value_heads"]
     masked = (x * mask.astype(F32)[:, None]).astype(F32)
@@ -172,10 +183,14 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
     a_decay = (F32(-1) * np.exp(W[p + "linear_attn.A_log"].astype(F32))).astype(F32)
     q, k, v, beta, decay = delta_prologue(qkv, conv, a_raw, b_raw, a_decay,
                                           W[p + "linear_attn.dt_bias"], kh, kd, vh, vd)
-    result = delta_recurrence(q, k, v, beta, decay)
-    out = _store(ops.gated_rms(_store(result, bf16), z, W[p + "linear_attn.norm.weight"],
-                               cfg["eps"]), bf16)
-    return _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
+    recurrence = delta_recurrence(q, k, v, beta, decay)
+    result = _store(recurrence, bf16)
+    out = _store(ops.gated_rms(result, z, W[p + "linear_attn.norm.weight"], cfg["eps"]), bf16)
+    mixed = _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
+    if trace is not None:
+        trace.update(masked=masked, qkv=qkv, z=z, a=a_raw, b=b_raw, q=q, k=k, v=v, beta=beta,
+                     decay=decay, recurrence=recurrence, result=result, gated=out, mixed=mixed)
+    return mixed
 
 
 def normalize_heads(x, multiplier):
@@ -244,39 +259,62 @@ def check_sequence(ids, mask, vocab):
         raise ValueError("Mask values must be zero or one.")
 
 
+def backbone_layer(W: dict, cfg: dict, i: int, h: np.ndarray, normed: np.ndarray,
+                   mask: np.ndarray, tables, bf16: bool = False, trace: dict | None = None):
+    """Layer ``i`` of ``native_hidden_states`` (``native_layer``,
+    ``src/backbone.jl:358-388``) from the residual stream ``h`` and its input
+    norm ``normed``: returns the next ``(h, normed)``, where ``normed`` is the next
+    layer's input norm (the final norm after the last layer) fused with the MLP
+    residual add.  ``trace`` also receives ``residual``, ``post_normed``, ``gate``,
+    ``up``, ``act`` and ``down`` besides the attention intermediates."""
+    eps = cfg["eps"]
+    kinds = cfg["layer_types"]
+    p = f"layers.{i}."
+    if kinds[i] == "full_attention":
+        mixed = full_attention(W, p, normed, mask, cfg, tables, bf16, trace)
+    elif kinds[i] == "linear_attention":
+        mixed = delta_attention(W, p, normed, mask, cfg, bf16, trace)
+    else:
+        raise ValueError(f"Unsupported layer type {kinds[i]}.")
+    residual, post = ops.residual_rms(h, mixed, W[p + "post_attention_layernorm.weight"], eps)
+    post = _store(post, bf16)
+    gate = _store(_linear(post, W[p + "mlp.gate_proj.weight"]), bf16)
+    up = _store(_linear(post, W[p + "mlp.up_proj.weight"]), bf16)
+    act = _store(ops.swiglu(gate, up), bf16)
+    down = _linear(act, W[p + "mlp.down_proj.weight"])
+    last = i + 1 == len(kinds)
+    nxt = W["norm.weight"] if last else W[f"layers.{i + 1}.input_layernorm.weight"]
+    # native_residual_add! (src/backbone.jl:358-361), then the next RMSNorm
+    h, normed = ops.residual_rms(residual, down, nxt, eps)
+    if not last:
+        normed = _store(normed, bf16)
+    if trace is not None:
+        trace.update(residual=residual, post_normed=post, gate=gate, up=up, act=act, down=down)
+    return h, normed
+
+
+def embed(W: dict, cfg: dict, ids, mask, bf16: bool = False):
+    """Checked ids, the gathered residual stream and the first input norm:
+    ``(ids, mask, h, normed, tables)`` (``src/backbone.jl:433-446``)."""
+    embed_table = W["embed_tokens.weight"]
+    check_sequence(ids, mask, embed_table.shape[0])
+    ids = np.asarray(ids, dtype=np.int32).reshape(-1)
+    mask = np.asarray(mask, dtype=np.int64).reshape(-1)
+    T = ids.size
+    h = ops.gather(embed_table, ids)
+    tables = ops.rope_tables(T, cfg["rotary_dim"], cfg["rope_theta"]) if cfg["rotary_dim"] else (
+        np.zeros((T, 0), F32), np.zeros((T, 0), F32))
+    normed = _store(ops.rms(h, W["layers.0.input_layernorm.weight"], cfg["eps"]), bf16)
+    return ids, mask, h, normed, tables
+
+
 def backbone_hidden(W: dict, cfg: dict, ids, mask, bf16: bool = False) -> np.ndarray:
     """``backbone_hidden`` (``src/backbone.jl:433-460``) -> ``[T, hidden]`` fp32.
 
     The residual add of each layer is computed together with the next RMSNorm
     (the final norm after the last layer); ``bf16`` selects bf16 storage of
     the activations listed in the module docstring."""
-    embed = W["embed_tokens.weight"]
-    check_sequence(ids, mask, embed.shape[0])
-    ids = np.asarray(ids, dtype=np.int32).reshape(-1)
-    mask = np.asarray(mask, dtype=np.int64).reshape(-1)
-    T = ids.size
-    h = ops.gather(embed, ids)
-    tables = ops.rope_tables(T, cfg["rotary_dim"], cfg["rope_theta"]) if cfg["rotary_dim"] else (
-        np.zeros((T, 0), F32), np.zeros((T, 0), F32))
-    eps = cfg["eps"]
-    kinds = cfg["layer_types"]
-    normed = _store(ops.rms(h, W["layers.0.input_layernorm.weight"], eps), bf16)
-    for i, kind in enumerate(kinds):
-        p = f"layers.{i}."
-        if kind == "full_attention":
-            mixed = full_attention(W, p, normed, mask, cfg, tables, bf16)
-        elif kind == "linear_attention":
-            mixed = delta_attention(W, p, normed, mask, cfg, bf16)
-        else:
-            raise ValueError(f"Unsupported layer type {kind}.")
-        residual, normed = ops.residual_rms(h, mixed, W[p + "post_attention_layernorm.weight"], eps)
-        normed = _store(normed, bf16)
-        gate = _store(_linear(normed, W[p + "mlp.gate_proj.weight"]), bf16)
-        up = _store(_linear(normed, W[p + "mlp.up_proj.weight"]), bf16)
-        down = _linear(_store(ops.swiglu(gate, up), bf16), W[p + "mlp.down_proj.weight"])
-        nxt = W[f"layers.{i + 1}.input_layernorm.weight"] if i + 1 < len(kinds) else W["norm.weight"]
-        # native_residual_add! (src/backbone.jl:358-361), then the next RMSNorm
-        h, normed = ops.residual_rms(residual, down, nxt, eps)
-        if i + 1 < len(kinds):
-            normed = _store(normed, bf16)
+    ids, mask, h, normed, tables = embed(W, cfg, ids, mask, bf16)
+    for i in range(len(cfg["layer_types"])):
+        h, normed = backbone_layer(W, cfg, i, h, normed, mask, tables, bf16)
     return normed

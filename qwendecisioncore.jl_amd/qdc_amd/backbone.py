@@ -9,7 +9,8 @@ Mirrors the reference's public entry points and their validation:
 * :func:`backbone_hidden` / :func:`backbone_last_hidden` (``src/backbone.jl:433-501``):
   one sequence per call, ids checked on the host (``check_sequence`` :413-422).
 * :func:`batch_backbone_hidden`: the optional batched hook (``src/backbone.jl:66-70``),
-  here returning every position of every row.
+  one final-normalised last-position state per row; :func:`batch_backbone_states`
+  returns every position of every row.
 
 Per layer (``native_layer``, ``src/backbone.jl:363-388``) the fused kernels do
 the row work: the layer's input RMSNorm is fused with the previous layer's MLP
@@ -139,14 +140,22 @@ class QwenBackbone:
 
     # ------------------------------------------------------------ forward --
     @torch.no_grad()
-    def forward(self, ids: torch.Tensor, mask: torch.Tensor | None) -> torch.Tensor:
+    def forward(self, ids: torch.Tensor, mask: torch.Tensor | None, last_only: bool = False,
+                error_flag: torch.Tensor | None = None) -> torch.Tensor:
         """Final-normalised hidden states ``[B*S, hidden]`` (device, fp32)
         for device ids ``[B, S]`` (int32) and mask ``[B, S]`` (0/1); ``mask=None``
-        means every token is kept (no masking work is done)."""
+        means every token is kept (no masking work is done).
+
+        ``last_only`` returns ``[B, hidden]``, the last position of each row:
+        after the last attention block only those rows go through the last MLP
+        and the final norm (the last-token forward ``native_hidden_forward``,
+        ``src/backbone.jl:390-396``).  ``error_flag`` (device int32, cleared by
+        the caller) is set by the gather when an id is outside the vocabulary."""
         B, S = ids.shape
         cfg = self.cfg
         # residual stream h in fp32 (a bf16 table widens exactly while gathered)
-        h = ops.native_gather(self.embedding, ids.reshape(-1).contiguous(), out_dtype=torch.float32)
+        h = ops.native_gather(self.embedding, ids.reshape(-1).contiguous(), out_dtype=torch.float32,
+                              error_flag=error_flag)
         mask32 = None if mask is None else mask.to(torch.int32).contiguous()
         # Masked tokens are zeroed before the DeltaNet projections (src/backbone.jl:286):
         # the norm producing a DeltaNet layer's input writes the masked rows itself.
@@ -158,12 +167,15 @@ class QwenBackbone:
                 mixed = self._full_attention(layer, normed, mask32, B, S)
             else:
                 mixed = self._delta_attention(layer, normed, B, S)
+            last = i + 1 == len(self.layers)
+            if last and last_only:  # the MLP and the final norm of the last rows only
+                h = h.view(B, S, -1)[:, -1].contiguous()
+                mixed = mixed.view(B, S, -1)[:, -1].contiguous()
             residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps)
             gate_up = normed @ layer["gate_up"]
             inter = gate_up.shape[1] // 2
             act = ops.native_mlp_gate(gate_up[:, :inter], gate_up[:, inter:])
             down = self._mm32(act, layer["down"])
-            last = i + 1 == len(self.layers)
             nxt = self.final_norm if last else self.layers[i + 1]["input_norm"]
             # residual add of the MLP fused with the next RMSNorm
             h, normed = ops.native_residual_rms(residual, down, nxt, cfg.eps,
@@ -275,16 +287,80 @@ def backbone_hidden(model: QwenBackbone, ids, mask, positions=None) -> np.ndarra
 
 
 def backbone_last_hidden(model: QwenBackbone, ids, mask) -> np.ndarray:
-    """Final-normalised hidden state of the last position (``src/backbone.jl:470-490``)."""
-    return backbone_hidden(model, ids, mask)[-1]
+    """Final-normalised hidden state of the last position, a ``[hidden]`` vector
+    (``src/backbone.jl:470-490``): the last-token forward, which normalises and
+    copies back only that row."""
+    d_ids, d_mask = _device_inputs(model, ids, mask)
+    return model.forward(d_ids, d_mask, last_only=True)[0].float().cpu().numpy()
 
 
-def batch_backbone_hidden(model: QwenBackbone, ids: torch.Tensor,
-                          mask: torch.Tensor | None) -> torch.Tensor:
-    """Every position of ``B`` equal-length sequences at once: device int32 ids
-    ``[B, S]`` and 0/1 mask ``[B, S]`` (None: nothing masked) -> ``[B, S, hidden]``
-    on the device.  RoPE positions restart at 0 for every row.  Ids are not
-    re-checked here: device ids outside the vocabulary gather zero rows (see
-    ``ops.native_gather``)."""
-    B, S = ids.shape
-    return model.forward(ids.to(torch.int32).contiguous(), mask).view(B, S, -1)
+def _batch_inputs(model: QwenBackbone, ids, mask):
+    """``[B, S]`` ids and mask as device tensors, checked as ``check_sequence``
+    checks one sequence (``src/backbone.jl:413-422``).  Host inputs are checked
+    before anything runs.  Device ids are checked by the gather itself (an id
+    outside the vocabulary sets a device flag) and a device mask by a device
+    comparison; both are read after the forward by :func:`_raise_if_invalid`.
+    Returns ``(ids, mask or None, pending)``."""
+    if not isinstance(ids, torch.Tensor) or ids.device.type != "cuda":
+        ids = np.asarray(ids, dtype=np.int64)
+        host_mask = np.ones(ids.shape, np.int64) if mask is None else np.asarray(mask, np.int64)
+        if ids.ndim != 2 or host_mask.shape != ids.shape:
+            raise ValueError("Input IDs and mask must be [batch, sequence] arrays of one shape.")
+        check_sequence(model, ids.reshape(-1), host_mask.reshape(-1))
+        d_ids = torch.from_numpy(ids.astype(np.int32)).to(model.device)
+        d_mask = None if host_mask.all() else torch.from_numpy(
+            host_mask.astype(np.int32)).to(model.device)
+        return d_ids, d_mask, None
+    if ids.dim() != 2 or ids.numel() == 0:
+        raise ValueError("Inputs must be a non-empty [batch, sequence] array.")
+    if ids.dtype not in (torch.int32, torch.int64):
+        raise ValueError("Token IDs must be integers.")
+    if ids.dtype == torch.int64:  # ids beyond int32 cannot be in the vocabulary
+        ids = torch.clamp(ids, -1, model.vocab).to(torch.int32)
+    flag = torch.zeros(1, dtype=torch.int32, device=model.device)
+    bad_mask = None
+    if mask is not None:
+        if not isinstance(mask, torch.Tensor) or mask.device != ids.device:
+            raise ValueError("A device id tensor needs its mask on the same device.")
+        if mask.shape != ids.shape:
+            raise ValueError("Input IDs and mask must have identical lengths.")
+        bad_mask = ((mask != 0) & (mask != 1)).any()
+        mask = mask.to(torch.int32)
+    return ids.contiguous(), mask, (flag, bad_mask)
+
+
+def _raise_if_invalid(pending) -> None:
+    if pending is None:
+        return
+    flag, bad_mask = pending
+    if int(flag.item()) != 0:
+        raise ValueError("Token ID is outside the vocabulary.")
+    if bad_mask is not None and bool(bad_mask.item()):
+        raise ValueError("Mask values must be zero or one.")
+
+
+def batch_backbone_hidden(model: QwenBackbone, ids, mask) -> np.ndarray:
+    """The optional batched hook (``batch_backbone_hidden``, ``src/backbone.jl:66-70``;
+    Metal ``ext/metal_batch_forward.jl:100-138``): ``B`` equal-length sequences,
+    ids and 0/1 mask ``[B, S]`` (host arrays, or device tensors; ``mask=None``:
+    nothing masked) -> the final-normalised hidden state of each row's last
+    position, ``[B, hidden]`` fp32 on the host (the reference's
+    ``(hidden, batch)``).  RoPE positions restart at 0 for every row.  Invalid
+    ids or mask values raise ``ValueError`` as ``check_sequence`` does."""
+    d_ids, d_mask, pending = _batch_inputs(model, ids, mask)
+    flag = None if pending is None else pending[0]
+    out = model.forward(d_ids, d_mask, last_only=True, error_flag=flag)
+    _raise_if_invalid(pending)
+    return out.float().cpu().numpy()
+
+
+def batch_backbone_states(model: QwenBackbone, ids, mask) -> torch.Tensor:
+    """Every position of ``B`` equal-length sequences: as :func:`batch_backbone_hidden`
+    but returning all final-normalised states ``[B, S, hidden]`` (fp32) on the
+    device, the batched form of ``backbone_hidden``."""
+    d_ids, d_mask, pending = _batch_inputs(model, ids, mask)
+    flag = None if pending is None else pending[0]
+    B, S = d_ids.shape
+    out = model.forward(d_ids, d_mask, error_flag=flag).view(B, S, -1)
+    _raise_if_invalid(pending)
+    return out

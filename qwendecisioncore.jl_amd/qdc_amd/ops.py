@@ -19,7 +19,9 @@ Tensors are row-major ``[rows, width]`` (the reference's column-major
 tensor device's current PyTorch stream; torch supplies device memory and the
 stream only.  dtype is float32 or bfloat16 (fp32 arithmetic either way).
 Argument errors raise ``ValueError`` before anything is enqueued, as the
-reference raises ``ArgumentError`` / ``DimensionMismatch``.
+reference raises ``ArgumentError`` / ``DimensionMismatch``: every tensor a call
+reads or writes, caller-supplied outputs included, must be on the device of the
+call's first input and of the dtype the kernel writes there.
 """
 from __future__ import annotations
 
@@ -87,7 +89,7 @@ def native_gather(embedding: torch.Tensor, ids, out: torch.Tensor | None = None,
     (then an out-of-range id writes a zero row and sets ``error_flag``)."""
     _device(embedding)
     vocab, hidden = embedding.shape
-    if isinstance(ids, torch.Tensor) and ids.device.type == "cuda":
+    if isinstance(ids, torch.Tensor) and ids.device.type != "cpu":
         if ids.dtype != torch.int32 or not ids.is_contiguous():
             raise ValueError("device ids must be a contiguous int32 tensor")
         dev_ids = ids
@@ -99,15 +101,18 @@ def native_gather(embedding: torch.Tensor, ids, out: torch.Tensor | None = None,
     out_dtype = out_dtype or embedding.dtype
     if out is None:
         out = torch.empty((n, hidden), dtype=out_dtype, device=embedding.device)
+    _device(embedding, dev_ids, out)
     if out.shape != (n, hidden) or not out.is_contiguous() or out.dtype != out_dtype:
         raise ValueError("out must be a contiguous [n_ids, hidden] tensor of out_dtype")
+    if out_dtype not in _DTYPES:
+        raise ValueError("out_dtype must be float32 or bfloat16")
     if not embedding.is_contiguous():
         raise ValueError("embedding must be contiguous")
     flag = 0
     if error_flag is not None:
-        _device(error_flag)
-        if error_flag.dtype != torch.int32:
-            raise ValueError("error_flag must be int32")
+        _device(embedding, error_flag)
+        if error_flag.dtype != torch.int32 or error_flag.numel() < 1:
+            raise ValueError("error_flag must be an int32 device tensor")
         flag = error_flag.data_ptr()
     check(lib().qdc_embedding_gather(out.data_ptr(), _DTYPES[out_dtype], embedding.data_ptr(),
                                      _dtype_code(embedding), dev_ids.data_ptr(), n, vocab, hidden,
@@ -145,6 +150,7 @@ def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool
         raise ValueError("weight must be a contiguous vector of the row width")
     if out is None:
         out = torch.empty(x.shape, dtype=weight.dtype, device=x.device)
+    _device(x, out)
     if out.shape != x.shape or out.dtype != weight.dtype:
         raise ValueError("out must have the shape of x and the dtype of weight")
     _, _, ld_out = _rows_view(out)
@@ -183,6 +189,7 @@ def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tens
         raise ValueError("weight must be a vector of the row width")
     residual = torch.empty_like(x) if residual is None else residual
     out = torch.empty(x.shape, dtype=weight.dtype, device=x.device) if out is None else out
+    _device(x, residual, out)
     if residual.shape != x.shape or not residual.is_contiguous() or residual.dtype != x.dtype:
         raise ValueError("residual must be a contiguous tensor like x")
     if out.shape != x.shape or not out.is_contiguous() or out.dtype != weight.dtype:
@@ -219,6 +226,9 @@ def native_gated_rms(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps
             raise ValueError("heads must be contiguous within a token")
     if out is None:
         out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _device(x, out)
+    if out.dtype != x.dtype:
+        raise ValueError(f"out must have the dtype of x ({x.dtype}), got {out.dtype}")
     if out.shape != x.shape or out.stride(2) != 1 or (heads > 1 and out.stride(1) != width):
         raise ValueError("out must be [tokens, heads, width] with contiguous heads")
     tok = lambda t: t.stride(0) if tokens > 1 else heads * width  # noqa: E731
@@ -271,6 +281,9 @@ def prepare_heads(q: torch.Tensor | None, k: torch.Tensor | None, q_norm, k_norm
             raise ValueError("q/k must be [tokens, heads, head_dim] with contiguous rows")
         if out is None:
             out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        _device(x, out)
+        if out.dtype != x.dtype:
+            raise ValueError(f"q_out/k_out must have the dtype of q/k ({x.dtype}), got {out.dtype}")
         if out.dim() == 4:
             n_seq = -(-tokens // seq_len)
             if (out.shape[0] * out.shape[1] != tokens or out.shape[2:] != x.shape[1:]
@@ -322,6 +335,9 @@ def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
             raise ValueError("rows must be contiguous")
     if out is None:
         out = torch.empty((tokens, width), dtype=gate.dtype, device=gate.device)
+    _device(gate, out)
+    if out.dtype != gate.dtype:
+        raise ValueError(f"out must have the dtype of gate ({gate.dtype}), got {out.dtype}")
     if out.shape != gate.shape or (width > 1 and out.stride(1) != 1):
         raise ValueError("out must be [tokens, width] with contiguous rows")
     ld = lambda t: t.stride(0) if tokens > 1 else width  # noqa: E731
@@ -347,6 +363,7 @@ def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Te
         raise ValueError("inconsistent delta_scan shapes")
     if out is None:
         out = torch.empty((B, S, H, vd), dtype=out_dtype, device=q.device)
+    _device(q, out)
     if out.shape != (B, S, H, vd) or out.dtype not in _DTYPES or not out.is_contiguous():
         raise ValueError("out must be a contiguous [B, S, H, vd] float32/bfloat16 tensor")
     out_dtype = out.dtype
@@ -381,6 +398,7 @@ def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor
              for o, sh in zip(out, shapes)):
         raise ValueError("out must be five contiguous float32 tensors of the output shapes")
     q, k, v, beta, decay = out
+    _device(proj, q, k, v, beta, decay)
     ld = proj.stride(0) if T > 1 else proj.shape[1]
     check(lib().qdc_delta_prologue(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
                                    decay.data_ptr(), proj.data_ptr(), _DTYPES[proj.dtype], ld,
@@ -403,11 +421,12 @@ def attention_softmax(scores: torch.Tensor, mask: torch.Tensor | None, scale: fl
         raise ValueError("scores must be a contiguous float32 [B, H, Q, K] tensor")
     B, H, Q, K = scores.shape
     if mask is not None:
-        _device(mask)
+        _device(scores, mask)
         if mask.dtype != torch.int32 or mask.shape != (B, K) or not mask.is_contiguous():
             raise ValueError("mask must be a contiguous int32 [B, K] tensor")
     if out is None:
         out = torch.empty(scores.shape, dtype=out_dtype or torch.float32, device=scores.device)
+    _device(scores, out)
     if out.shape != scores.shape or not out.is_contiguous() or out.dtype not in _DTYPES:
         raise ValueError("out must be a contiguous float32/bfloat16 tensor shaped like scores")
     check(lib().qdc_attention_softmax(out.data_ptr(), _DTYPES[out.dtype], scores.data_ptr(),
@@ -431,6 +450,7 @@ def attention_gate(values: torch.Tensor, gate: torch.Tensor, out_dtype=None,
         raise ValueError("gate must be a [B*S, H, hd] view with unit element stride")
     if out is None:
         out = torch.empty((B * S, H * hd), dtype=out_dtype or gate.dtype, device=values.device)
+    _device(values, out)
     if out.dtype not in _DTYPES or out.shape != (B * S, H * hd) or out.stride(1) != 1:
         raise ValueError("out must be [B*S, H*hd] with unit element stride")
     tok = out.stride(0) if B * S > 1 else H * hd

@@ -1,0 +1,113 @@
+"""Host-side argument checks of the ``qdc_amd.ops`` wrappers, on the CPU.
+
+Every wrapper must reject a caller-supplied output of the wrong dtype or on
+another device before anything reaches the library: a bf16 ``out`` given to an
+fp32 kernel would be written past its end on the device, and a host ``out``
+would hand a host pointer to the kernel.  Here the library is replaced by a
+stub that fails the test if any entry point is reached, and ``meta`` tensors
+stand in for device tensors (``ops._device`` is switched to accept them), so a
+missing check shows up as a stub call instead of a launch.
+"""
+import pytest
+import torch
+
+from qdc_amd import ops
+
+F32, BF16 = torch.float32, torch.bfloat16
+
+
+class _Stub:
+    def __getattr__(self, name):
+        raise AssertionError(f"{name} reached the library")
+
+
+@pytest.fixture
+def no_launch(monkeypatch):
+    def device(*tensors):
+        dev = tensors[0].device
+        if dev.type != "meta":
+            raise ValueError("device tensors required")
+        for t in tensors:
+            if t.device != dev:
+                raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+
+    monkeypatch.setattr(ops, "_device", device)
+    monkeypatch.setattr(ops, "lib", lambda: _Stub())
+    monkeypatch.setattr(ops, "_stream", lambda t: 0)
+
+
+def d(*shape, dtype=F32):
+    return torch.empty(shape, dtype=dtype, device="meta")
+
+
+def host(*shape, dtype=F32):
+    return torch.empty(shape, dtype=dtype)
+
+
+def _calls():
+    """(name, valid call, [invalid calls]) per wrapper: the valid call must reach
+    the library (the stub), every invalid one must raise ValueError first."""
+    tables = (d(8, 4), d(8, 4))
+    return [
+        ("native_gather",
+         lambda **kw: ops.native_gather(d(10, 16, dtype=BF16), d(4, dtype=torch.int32), **kw),
+         [dict(out=d(4, 16, dtype=F32)),                      # bf16 table -> bf16 out expected
+          dict(out=host(4, 16, dtype=BF16)),
+          dict(out_dtype=F32, out=d(4, 16, dtype=BF16)),
+          dict(error_flag=host(1, dtype=torch.int32)),
+          dict(error_flag=d(1, dtype=torch.int64))]),
+        ("native_rms",
+         lambda **kw: ops.native_rms(d(8, 64), d(64, dtype=BF16), 1e-6, **kw),
+         [dict(out=d(8, 64, dtype=F32)), dict(out=host(8, 64, dtype=BF16)),
+          dict(token_mask=host(8, dtype=torch.int32)), dict(token_mask=d(8, dtype=torch.int64))]),
+        ("native_residual_rms",
+         lambda **kw: ops.native_residual_rms(d(8, 64), d(8, 64, dtype=BF16), d(64, dtype=BF16),
+                                              1e-6, **kw),
+         [dict(residual=d(8, 64, dtype=BF16)), dict(residual=host(8, 64)),
+          dict(out=d(8, 64, dtype=F32)), dict(out=host(8, 64, dtype=BF16))]),
+        ("native_gated_rms",
+         lambda **kw: ops.native_gated_rms(d(4, 2, 16, dtype=BF16), d(4, 2, 16, dtype=BF16),
+                                           d(16, dtype=BF16), 1e-6, **kw),
+         [dict(out=d(4, 2, 16, dtype=F32)), dict(out=host(4, 2, 16, dtype=BF16))]),
+        ("prepare_heads",
+         lambda **kw: ops.prepare_heads(d(8, 2, 16), d(8, 1, 16), d(16), d(16), tables, 8, 1e-6,
+                                        **kw),
+         [dict(q_out=d(8, 2, 16, dtype=BF16)), dict(k_out=d(8, 1, 16, dtype=BF16)),
+          dict(q_out=host(8, 2, 16)), dict(k_out=host(8, 1, 16)),
+          dict(q_out=d(1, 8, 2, 16, dtype=BF16))]),
+        ("native_mlp_gate",
+         lambda **kw: ops.native_mlp_gate(d(4, 16), d(4, 16), **kw),
+         [dict(out=d(4, 16, dtype=BF16)), dict(out=host(4, 16))]),
+        ("delta_scan",
+         lambda **kw: ops.delta_scan(d(1, 4, 2, 8), d(1, 4, 2, 8), d(1, 4, 2, 8), d(1, 4, 2),
+                                     d(1, 4, 2), **kw),
+         [dict(out=host(1, 4, 2, 8)), dict(out=d(1, 4, 2, 8, dtype=torch.float16))]),
+        ("delta_prologue",
+         lambda **kw: ops.delta_prologue(d(4, 3 * 16 + 16 + 4, dtype=BF16), d(48, 4), d(2), d(2),
+                                         4, 1, 16, 2, 8, **kw),
+         [dict(out=(host(4, 1, 16), d(4, 1, 16), d(4, 2, 8), d(4, 2), d(4, 2))),
+          dict(out=(d(4, 1, 16), d(4, 1, 16), d(4, 2, 8), d(4, 2), host(4, 2))),
+          dict(out=(d(4, 1, 16, dtype=BF16), d(4, 1, 16), d(4, 2, 8), d(4, 2), d(4, 2)))]),
+        ("attention_softmax",
+         lambda **kw: ops.attention_softmax(d(1, 2, 4, 4), None, 0.5, **kw),
+         [dict(out=host(1, 2, 4, 4)), dict(out=d(1, 2, 4, 4, dtype=torch.float16))]),
+        ("attention_gate",
+         lambda **kw: ops.attention_gate(d(1, 2, 4, 8), d(4, 2, 8, dtype=BF16), **kw),
+         [dict(out=host(4, 16, dtype=BF16)), dict(out=d(4, 16, dtype=torch.float16))]),
+    ]
+
+
+@pytest.mark.parametrize("name,call,bad", _calls(), ids=[c[0] for c in _calls()])
+def test_outputs_checked_before_launch(no_launch, name, call, bad):
+    with pytest.raises(AssertionError, match="reached the library"):
+        call()
+    for kwargs in bad:
+        with pytest.raises(ValueError):
+            call(**kwargs)
+
+
+def test_host_tensors_rejected(no_launch):
+    with pytest.raises(ValueError):
+        ops.native_rms(host(8, 64), host(64), 1e-6)
+    with pytest.raises(ValueError):
+        ops.native_mlp_gate(d(4, 16), host(4, 16))
