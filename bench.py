@@ -80,9 +80,12 @@ class Kernel:
     """One fused kernel at its benchmark shape with rotating buffer sets."""
 
     def __init__(self, name, symbol, algo_bytes, make_set, launch, shape, dtype, group="hot",
-                 flops=None, launches=None):
+                 flops=None, launches=None, ceiling=None):
         self.name, self.symbol, self.algo_bytes = name, symbol, algo_bytes
         self.shape, self.dtype = shape, dtype
+        # (make_set, launch) of a plain kernel with this kernel's access pattern
+        # and bytes, timed beside it as its ceiling (None: the contiguous copy)
+        self.ceiling = ceiling
         # "hot": the fused row kernels at the per-kernel shapes; "next": widened;
         # "forward": the fused row kernels as the 0.8B-like forward launches them
         self.group, self.flops = group, flops
@@ -94,6 +97,23 @@ class Kernel:
 
     def run(self, i):
         self.launch(self.sets[i % len(self.sets)])
+
+
+def row_copy_ceiling(dev, g, table, n, repeat):
+    """The random-row copy (qdc_copy_rows) of the same table: n rows at
+    uniformly random places, written contiguously `repeat` times (repeat 2
+    writes as many bytes as the fp32-widening gather).  Bytes: the rows read,
+    the rows written and the int32 row indices, as the gather's."""
+    import torch
+    from qdc_amd import ops
+    vocab, hidden = table.shape
+    row_bytes = hidden * table.element_size()
+
+    def make_set(i):
+        return (torch.randint(0, vocab, (n,), generator=g, device=dev, dtype=torch.int32),
+                torch.empty((n, hidden * repeat), dtype=table.dtype, device=dev))
+
+    return make_set, lambda s: ops.device_copy_rows(s[1], table, s[0], repeat)
 
 
 def build_kernels(dev):
@@ -141,7 +161,8 @@ def build_kernels(dev):
         "gather_bf16", "gather_flat", 2 * n * hidden * 2 + n * 4,
         lambda i: (torch.randint(0, vocab, (n,), generator=g, device=dev, dtype=torch.int32),
                    torch.empty((n, hidden), dtype=bf, device=dev)),
-        lambda s: ops.native_gather(table, s[0], out=s[1]), [vocab, hidden, n], "bfloat16"))
+        lambda s: ops.native_gather(table, s[0], out=s[1]), [vocab, hidden, n], "bfloat16",
+        ceiling=row_copy_ceiling(dev, g, table, n, 1)))
 
     Ti, I = 16384, 3584
     kernels.append(Kernel(
@@ -257,11 +278,12 @@ def build_forward_kernels(dev):
     wb, wf = randn((Hd,), bf, 0.02), randn((Hd,), f32, 0.02)
     table = randn((cfg.vocab, Hd), bf, 0.02)
     ks.append(Kernel(
-        "fwd_gather_bf16_f32", "gather_flat", T * Hd * 2 + T * Hd * 4 + T * 4,
+        "fwd_gather_bf16_f32", "gather_widen", T * Hd * 2 + T * Hd * 4 + T * 4,
         lambda i: (torch.randint(0, cfg.vocab, (T,), generator=g, device=dev, dtype=torch.int32),
                    torch.empty((T, Hd), dtype=f32, device=dev)),
         lambda s: ops.native_gather(table, s[0], out=s[1], out_dtype=f32), [T, Hd],
-        "bfloat16->float32", group="forward", launches=1))
+        "bfloat16->float32", group="forward", launches=1,
+        ceiling=row_copy_ceiling(dev, g, table, T, 2)))
     ks.append(Kernel(
         "fwd_input_rms_f32_bf16", "rms_rows_fast", T * Hd * (4 + 2) + Hd * 2,
         lambda i: (randn((T, Hd), f32), torch.empty((T, Hd), dtype=bf, device=dev)),
@@ -382,6 +404,10 @@ def copy_ceilings(dev, kernels, steps, warmup):
             lambda i, side=side: (torch.empty(side, dtype=torch.uint8, device=dev),
                                   torch.empty(side, dtype=torch.uint8, device=dev)),
             lambda st: ops.device_copy(st[1], st[0]), [side], "u8"))
+        if k.ceiling is not None:  # the same access pattern as a plain copy
+            make_set, launch = k.ceiling
+            copies.append(Kernel(f"rows_{k.name}", "copy_rows", k.algo_bytes, make_set, launch,
+                                 k.shape, k.dtype))
     for i in range(warmup):
         for c in copies:
             c.run(i)
@@ -389,7 +415,8 @@ def copy_ceilings(dev, kernels, steps, warmup):
     for c in copies:  # one untimed replay
         c.graph.replay()
     time_gpu(copies, steps)
-    return {k.name: c for k, c in zip(kernels, copies)}
+    by_name = {c.name: c for c in copies}
+    return {k.name: (by_name[f"copy_{k.name}"], by_name.get(f"rows_{k.name}")) for k in kernels}
 
 
 CALIB_BYTES = 512 << 20
@@ -678,14 +705,30 @@ def cpu_baseline(min_seconds=10.0, all_cores_seconds=5.0):
     }
 
 
-def load_traffic(symbol):
+def _pmc():
     try:
         with open(PMC_FILE) as f:
-            data = json.load(f)
+            return json.load(f)
     except (OSError, ValueError):
-        return None
-    entry = data.get("kernels", {}).get(symbol)
+        return {}
+
+
+def load_traffic(name):
+    """HBM bytes per launch of a kernel counted by rocprofv3 (FETCH_SIZE +
+    WRITE_SIZE, calibrated) in the profiling run recorded in PMC_FILE; not
+    counted by this run."""
+    entry = _pmc().get("kernels", {}).get(name)
     return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def traffic_source():
+    """Where the traffic figures of this line come from."""
+    data = _pmc()
+    if not data:
+        return None
+    return {"file": os.path.relpath(PMC_FILE, ROOT), "summary": data.get("source"),
+            "commit": data.get("commit"), "commands": data.get("commands"),
+            "note": "counted by rocprofv3 --pmc in that profiling run of bench.py, not in this run"}
 
 
 def main():
@@ -737,15 +780,20 @@ def main():
              "gbs": round(k.algo_bytes / (k.avg_ms / 1e3) / 1e9, 1),
              "pct_peak": round(100 * k.algo_bytes / (k.avg_ms / 1e3) / 1e9 / PEAK_GBS, 1)}
         t = load_traffic(k.name)
-        if t is not None:  # HBM bytes per launch counted by rocprofv3 (FETCH_SIZE + WRITE_SIZE)
-            e.update(hbm_bytes_counted=t,
-                     hbm_gbs_counted=round(t / (k.avg_ms / 1e3) / 1e9, 1))
-        c = ceilings.get(k.name)
+        if t is not None:  # counted in the profiling run named by traffic_source
+            e.update(hbm_bytes_counted=t, traffic_per_algorithmic=round(t / k.algo_bytes, 4))
+        c, rows = ceilings.get(k.name, (None, None))
         if c is not None:  # the same bytes as one plain streaming copy launch
             copy_gbs = c.algo_bytes / (c.avg_ms / 1e3) / 1e9
             e.update(copy_us=round(c.avg_ms * 1e3, 3),
                      copy_pct_peak=round(100 * copy_gbs / PEAK_GBS, 1),
                      pct_of_copy=round(100 * e["gbs"] / copy_gbs, 1))
+        if rows is not None:  # the same access pattern as a plain random-row copy
+            e.update(ceiling="random-row copy (qdc_copy_rows), same table, bytes and row count",
+                     ceiling_us=round(rows.avg_ms * 1e3, 3),
+                     ceiling_pct_peak=round(100 * rows.algo_bytes / (rows.avg_ms / 1e3) / 1e9
+                                            / PEAK_GBS, 1),
+                     pct_of_ceiling=round(100 * rows.avg_ms / k.avg_ms, 1))
         if k.flops:
             tf = k.flops / (k.avg_ms / 1e3) / 1e12
             e.update(bound="mfma", tflops=round(tf, 2), mfma_f32_peak_tflops=MFMA_F32_PEAK_TF,
@@ -760,14 +808,17 @@ def main():
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(hot_ms / args.steps, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        # the arithmetic type; every kernel computes in fp32 whatever it stores
+        "dtype": "f32", "storage_dtypes": {k.name: k.dtype for k in hot},
         "data": "synthetic",
         "config": {"workload": "fused row kernels of one Qwen3.5-0.8B-like layer set: "
                                + ", ".join(k.name for k in hot),
                    "storage": "bf16 and fp32 as named per kernel", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": dom.name, "achieved": round(achieved, 1),
                      "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes": dom.algo_bytes},
+                     "traffic": traffic, "algorithmic_bytes": dom.algo_bytes,
+                     "traffic_source": traffic_source()},
         "kernels": per,
     }
     if widened:

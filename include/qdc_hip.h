@@ -296,6 +296,20 @@ int32_t qdc_attention_gate(void *out, int32_t out_dtype, const float *values, co
  */
 int32_t qdc_copy(void *dst, const void *src, int64_t bytes, hipStream_t stream);
 
+/*
+ * Random-row copy: destination row i (row_bytes * repeat bytes, rows
+ * contiguous) holds `repeat` copies of source row rows[i] (rows: device int32,
+ * each in [0, n_src); one outside writes zeros).  row_bytes a multiple of 16,
+ * repeat 1 or 2, both pointers 16-byte aligned, fewer than 2^31 chunks of 16
+ * bytes (QDC_ERR_SHAPE otherwise); no overlap.  No counterpart in the
+ * reference: the single-launch ceiling of the embedding gather's access
+ * pattern (rows read at random places of a large table, written contiguously;
+ * repeat = 2 writes as many bytes as the fp32-widening gather) that the
+ * benchmark times beside the gathers.
+ */
+int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows, int64_t n_rows,
+                      int64_t n_src, int64_t row_bytes, int32_t repeat, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,9 +1,11 @@
-// qdc_copy.hip -- a plain device copy in the streaming shape the row kernels
+// qdc_copy.hip -- plain device copies in the streaming shape the row kernels
 // use at their best: one 16-byte chunk per thread, nontemporal load and store,
-// no arithmetic.  It has no counterpart in the reference.  A single launch of
-// this copy at a given byte count is the practical bandwidth ceiling that a
+// no arithmetic.  Neither has a counterpart in the reference.  A single launch
+// of qdc_copy at a given byte count is the practical bandwidth ceiling that a
 // row kernel moving the same bytes can be held against (launch ramp-up and
-// drain included), so the benchmark times it beside each kernel.
+// drain included), so the benchmark times it beside each kernel; qdc_copy_rows
+// is the same for the embedding gather's access pattern (whole rows read at
+// random places of a large table, written contiguously).
 #include "qdc_common.hpp"
 
 namespace qdc {
@@ -19,6 +21,28 @@ __global__ __launch_bounds__(kBlock) void copy_chunks(u32x4 *__restrict__ dst,
 // below 2^32 work-items
 constexpr int64_t kMaxChunks = ((int64_t)1 << 32) - kBlock;
 
+// Random-row copy: thread g copies 16-byte chunk c of source row rows[i]
+// (g = i * chunks + c) into each of the `repeat` copies of destination row i.
+// A store instruction of a wavefront writes one contiguous span per copy.  A
+// row index outside [0, n_src) copies nothing and writes zeros.
+template <int REPEAT>
+__global__ __launch_bounds__(kBlock) void copy_rows(u32x4 *__restrict__ dst,
+                                                    const u32x4 *__restrict__ src,
+                                                    const int32_t *__restrict__ rows,
+                                                    uint32_t total, FastDiv chunks,
+                                                    int64_t n_src) {
+    const uint32_t g = blockIdx.x * kBlock + threadIdx.x;
+    if (g >= total) return;
+    const uint32_t i = fastdiv(g, chunks);
+    const uint32_t c = g - i * chunks.d;
+    const int64_t r = rows[i];
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r >= 0 && r < n_src) v = __builtin_nontemporal_load(src + r * chunks.d + c);
+    u32x4 *d = dst + (int64_t)i * chunks.d * REPEAT + c;
+#pragma unroll
+    for (int k = 0; k < REPEAT; ++k) __builtin_nontemporal_store(v, d + k * (int64_t)chunks.d);
+}
+
 }  // namespace
 }  // namespace qdc
 
@@ -33,5 +57,32 @@ extern "C" int32_t qdc_copy(void *dst, const void *src, int64_t bytes, hipStream
     const int64_t n = bytes / 16;
     hipLaunchKernelGGL(copy_chunks, dim3((uint32_t)ceil_div(n, kBlock)), dim3(kBlock), 0, stream,
                        static_cast<u32x4 *>(dst), static_cast<const u32x4 *>(src), (uint32_t)n);
+    return launch_status();
+}
+
+extern "C" int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows, int64_t n_rows,
+                                 int64_t n_src, int64_t row_bytes, int32_t repeat,
+                                 hipStream_t stream) {
+    if (n_rows < 0 || n_src < 0 || row_bytes < 0 || row_bytes % 16 != 0 ||
+        (repeat != 1 && repeat != 2))
+        return QDC_ERR_SHAPE;
+    const int64_t chunks = row_bytes / 16;
+    if (n_rows * chunks >= ((int64_t)1 << 31)) return QDC_ERR_SHAPE;
+    if (n_rows == 0 || chunks == 0) return QDC_OK;
+    if (!dst || !src || !rows) return QDC_ERR_NULL;
+    if (!aligned16(dst) || !aligned16(src)) return QDC_ERR_SHAPE;
+    const int64_t out_bytes = n_rows * row_bytes * repeat;
+    if (overlaps(dst, out_bytes, src, n_src * row_bytes) || overlaps(dst, out_bytes, rows, n_rows * 4))
+        return QDC_ERR_ALIAS;
+    const uint32_t total = (uint32_t)(n_rows * chunks);
+    const dim3 grid((uint32_t)ceil_div(total, kBlock));
+    if (repeat == 1)
+        hipLaunchKernelGGL(copy_rows<1>, grid, dim3(kBlock), 0, stream, static_cast<u32x4 *>(dst),
+                           static_cast<const u32x4 *>(src), rows, total,
+                           make_fastdiv((uint32_t)chunks), n_src);
+    else
+        hipLaunchKernelGGL(copy_rows<2>, grid, dim3(kBlock), 0, stream, static_cast<u32x4 *>(dst),
+                           static_cast<const u32x4 *>(src), rows, total,
+                           make_fastdiv((uint32_t)chunks), n_src);
     return launch_status();
 }

@@ -1,12 +1,19 @@
 // qdc_gather.hip -- embedding gather (token id -> row copy) for gfx950, plus
 // the host-side id check and the library's version/status strings.
 //
-// Fast path: one thread per 16-byte chunk of the output (row = thread / chunks
-// per row), nontemporal load and store: the plain-copy shape that measured
-// fastest on gfx950.  A wavefront-per-row kernel covers launches too large for
-// 32-bit thread indices.  bf16->bf16 and f32->f32 move bits; bf16->f32 widens
-// each value by a 16-bit shift, so results are bit-exact.  An id outside
-// [0, vocab) yields a zero row and sets *error_flag (when given).
+// Fast paths move 16-byte chunks with nontemporal loads and stores.  A copy of
+// the bits (bf16->bf16, f32->f32) takes one thread per chunk (row = thread /
+// chunks per row), the plain-copy shape that measured fastest on gfx950.  The
+// widening gather (bf16 table -> fp32 rows, each value shifted left by 16 bits)
+// turns every 16-byte input chunk into 32 output bytes; there lane 2m of a
+// wavefront loads chunk m and lane 2m+1 chunk 32+m of the wavefront's 64, and
+// one neighbour swap (DPP) of half a chunk lets each of the two store
+// instructions write one contiguous 1 KB span (each lane storing its own two
+// halves would write 16-byte pieces 32 bytes apart, which left partly written
+// lines and ~5% more bytes written than the output holds).  A wavefront-per-row
+// kernel covers launches too large for 32-bit thread indices.  Results are
+// bit-exact.  An id outside [0, vocab) yields a zero row and sets *error_flag
+// (when given).
 #include "qdc_common.hpp"
 
 namespace qdc {
@@ -49,6 +56,49 @@ __global__ __launch_bounds__(kBlock) void gather_flat(TO *__restrict__ out,
         return;
     }
     put_chunk<TI, TO>(dst, load_stream(table + id * hidden + (int64_t)c * V));
+}
+
+// bf16 table -> fp32 rows, 16-byte input chunks g of the flat [n_ids, chunks]
+// grid; wavefront w covers chunks [64w, 64w + 64) and output chunks (4 fp32)
+// [128w, 128w + 128).  No lane returns early: every lane takes part in the swap.
+__device__ __forceinline__ u32x4 widen_pair(uint32_t a, uint32_t b) {
+    return u32x4{a << 16, a & 0xffff0000u, b << 16, b & 0xffff0000u};
+}
+
+__global__ __launch_bounds__(kBlock) void gather_widen(float *__restrict__ out,
+                                                       const bf16_t *__restrict__ table,
+                                                       const int32_t *__restrict__ ids,
+                                                       uint32_t total, FastDiv chunks,
+                                                       int64_t vocab, int32_t *error_flag) {
+    constexpr int V = Elem<bf16_t>::kVec;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t base = blockIdx.x * kBlock + (threadIdx.x - lane);
+    const uint32_t half = lane >> 1;
+    const bool odd = lane & 1u;
+    const uint32_t g = base + half + (odd ? kWave / 2 : 0u);
+    u32x4 r = {0u, 0u, 0u, 0u};
+    if (g < total) {
+        const uint32_t row = fastdiv(g, chunks);
+        const uint32_t c = g - row * chunks.d;
+        const int64_t id = ids[row];
+        if (id >= 0 && id < vocab)
+            r = load_stream(table + id * ((int64_t)chunks.d * V) + (int64_t)c * V);
+        else if (c == 0 && error_flag)
+            atomicOr(error_flag, 1);
+    }
+    // Even lanes keep the low half (r[0], r[1]) of chunk `half` and send its high
+    // half; odd lanes keep the high half (r[2], r[3]) of chunk 32 + half and send
+    // its low half.  quad_perm [1,0,3,2] exchanges lane pairs (l, l ^ 1).
+    const uint32_t send0 = odd ? r[0] : r[2], send1 = odd ? r[1] : r[3];
+    const uint32_t got0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send0, 0xB1, 0xf, 0xf, true);
+    const uint32_t got1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)send1, 0xB1, 0xf, 0xf, true);
+    // store 0: output chunk 2*base + lane = half (lane & 1) of input chunk base + lane/2
+    // store 1: output chunk 2*base + 64 + lane, from input chunk base + 32 + lane/2
+    const u32x4 first = odd ? widen_pair(got0, got1) : widen_pair(r[0], r[1]);
+    const u32x4 second = odd ? widen_pair(r[2], r[3]) : widen_pair(got0, got1);
+    float *dst = out + ((int64_t)base * 2 + lane) * 4;
+    if (base + half < total) store_raw(dst, first);
+    if (base + kWave / 2 + half < total) store_raw(dst + kWave * 4, second);
 }
 
 template <typename TI, typename TO>
@@ -117,9 +167,14 @@ int32_t launch(void *out, const void *table, const int32_t *ids, int64_t n_ids, 
     const int64_t chunks = hidden / Elem<TI>::kVec;
     if (fast && hidden % Elem<TI>::kVec == 0 && n_ids * chunks < ((int64_t)1 << 31)) {
         const uint32_t total = (uint32_t)(n_ids * chunks);
-        hipLaunchKernelGGL((gather_flat<TI, TO>), dim3((uint32_t)ceil_div(total, kBlock)),
-                           dim3(kBlock), 0, stream, (TO *)out, (const TI *)table, ids, total,
-                           make_fastdiv((uint32_t)chunks), vocab, error_flag);
+        if constexpr (sizeof(TI) != sizeof(TO))
+            hipLaunchKernelGGL(gather_widen, dim3((uint32_t)ceil_div(total, kBlock)),
+                               dim3(kBlock), 0, stream, (float *)out, (const bf16_t *)table, ids,
+                               total, make_fastdiv((uint32_t)chunks), vocab, error_flag);
+        else
+            hipLaunchKernelGGL((gather_flat<TI, TO>), dim3((uint32_t)ceil_div(total, kBlock)),
+                               dim3(kBlock), 0, stream, (TO *)out, (const TI *)table, ids, total,
+                               make_fastdiv((uint32_t)chunks), vocab, error_flag);
     } else if (fast && hidden % Elem<TI>::kVec == 0)
         hipLaunchKernelGGL((gather_rows<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
                            (TO *)out, (const TI *)table, ids, n_ids, vocab, hidden, error_flag);

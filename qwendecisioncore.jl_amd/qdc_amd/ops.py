@@ -476,6 +476,26 @@ def device_copy(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
     return dst
 
 
+def device_copy_rows(dst: torch.Tensor, table: torch.Tensor, rows: torch.Tensor,
+                     repeat: int = 1) -> torch.Tensor:
+    """``dst[i]`` = ``repeat`` copies of the bytes of ``table[rows[i]]`` (``table``
+    ``[n, width]`` contiguous, ``rows`` device int32, ``dst`` contiguous with
+    ``repeat`` times a table row's bytes per row): the gather's access pattern
+    with no conversion, the ceiling the benchmark sets beside the gathers."""
+    _device(table, rows, dst)
+    if not dst.is_contiguous() or not table.is_contiguous() or table.dim() != 2:
+        raise ValueError("table must be a contiguous 2-D tensor and dst contiguous")
+    if rows.dtype != torch.int32 or not rows.is_contiguous():
+        raise ValueError("rows must be a contiguous int32 tensor")
+    row_bytes = table.shape[1] * table.element_size()
+    if dst.numel() * dst.element_size() != rows.numel() * row_bytes * repeat:
+        raise ValueError("dst must hold repeat copies of one table row per index")
+    check(lib().qdc_copy_rows(dst.data_ptr(), table.data_ptr(), rows.data_ptr(), rows.numel(),
+                              table.shape[0], row_bytes, repeat, _stream(table)),
+          "device_copy_rows")
+    return dst
+
+
 def check_ids(ids: Sequence[int], vocab: int) -> None:
     """Host id check of ``check_sequence`` (``src/backbone.jl:417-418``)."""
     host = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))

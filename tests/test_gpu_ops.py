@@ -286,6 +286,55 @@ def test_gather_checks_and_device_ids():
     assert not got[1].any() and not got[3].any()
 
 
+def test_gather_widening_invalid_ids_mid_wavefront():
+    """The fp32-widening gather (lanes exchange half chunks) with out-of-range
+    device ids inside a wavefront: those rows are zero, the flag is set, every
+    other row is the widened table row bit for bit; rows narrower and wider
+    than a wavefront's 64 chunks."""
+    from qdc_amd import ops
+    rng = np.random.default_rng(31)
+    for vocab, hidden, n in ((40, 64, 37), (300, 1024, 9), (7, 8, 130)):
+        bits = rng.integers(0, 1 << 16, size=(vocab, hidden), dtype=np.uint16)
+        table = torch.from_numpy(bits.view(np.int16)).to(DEV).view(torch.bfloat16)
+        ids = rng.integers(0, vocab, size=n).astype(np.int32)
+        bad = [1, n // 2, n - 1]
+        ids[bad] = [vocab, -1, vocab + 5]
+        flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+        out = ops.native_gather(table, torch.from_numpy(ids).to(DEV), out_dtype=torch.float32,
+                                error_flag=flag)
+        torch.cuda.synchronize()
+        assert flag.item() == 1
+        got = out.cpu().view(torch.int32).numpy().view(np.uint32)
+        ok = np.setdiff1d(np.arange(n), bad)
+        assert np.array_equal(got[ok], bits[ids[ok]].astype(np.uint32) << 16), (vocab, hidden)
+        assert not got[bad].any()
+
+
+def test_device_copy_rows():
+    """The random-row copy the benchmark holds the gathers against: each
+    output row is `repeat` copies of the indexed table row's bytes; an index
+    outside the table gives zeros."""
+    from qdc_amd import ops
+    rng = np.random.default_rng(32)
+    for vocab, hidden, n, repeat in ((248320, 1024, 16384, 1), (248320, 1024, 16384, 2),
+                                     (50, 24, 33, 2), (9, 8, 5, 1)):
+        bits = rng.integers(0, 1 << 16, size=(vocab, hidden), dtype=np.uint16)
+        table = torch.from_numpy(bits.view(np.int16)).to(DEV)
+        rows = rng.integers(0, vocab, size=n).astype(np.int32)
+        rows[-1] = vocab  # outside: zeros
+        dst = torch.full((n, hidden * repeat), 7, dtype=torch.int16, device=DEV)
+        ops.device_copy_rows(dst, table, torch.from_numpy(rows).to(DEV), repeat)
+        torch.cuda.synchronize()
+        got = dst.cpu().numpy().view(np.uint16).reshape(n, repeat, hidden)
+        for k in range(repeat):
+            assert np.array_equal(got[:-1, k], bits[rows[:-1]]), (vocab, hidden, repeat)
+        assert not got[-1].any()
+    with pytest.raises(ValueError):
+        ops.device_copy_rows(torch.empty((3, 8), dtype=torch.int16, device=DEV),
+                             torch.empty((4, 8), dtype=torch.int16, device=DEV),
+                             torch.zeros(3, dtype=torch.int32, device=DEV), repeat=2)
+
+
 # ------------------------------------------- fp32 residual stream mixes ------
 @pytest.mark.parametrize("rows,width", [(16384, 1024), (33, 256), (5, 1000)])
 def test_rmsnorm_fp32_to_bf16(rows, width):
