@@ -308,17 +308,18 @@ def build_forward_kernels(dev):
     tables = ops.rope_tables(S, rd, cfg.rope_theta, dev)
     qkv_w = 2 * hd * nh + 2 * hd * kv
 
-    def qk_launch(s):
-        ops.prepare_heads(s[0][:, :2 * hd * nh].view(T, nh, 2 * hd)[:, :, :hd],
-                          s[0][:, 2 * hd * nh:2 * hd * nh + hd * kv].view(T, kv, hd),
-                          qn, kn, tables, rd, 1e-6, seq_len=S, q_out=s[1].permute(0, 2, 1, 3),
-                          k_out=s[2].permute(0, 2, 1, 3))
+    def prep_launch(s):  # the packed projection [q | k | v | gate] as the forward lays it out
+        ops.attention_prepare(s[0][:, :hd * nh].view(T, nh, hd),
+                              s[0][:, hd * nh:hd * (nh + kv)].view(T, kv, hd),
+                              s[0][:, hd * (nh + kv):hd * (nh + 2 * kv)].view(T, kv, hd),
+                              qn, kn, tables, rd, 1e-6, B, out=s[1:])
     ks.append(Kernel(
-        "fwd_qk_norm_rope_bf16", "qk_norm_rope_fast",
-        2 * T * (nh + kv) * hd * 2 + 2 * hd * 2 + 2 * S * (rd // 2) * 4,
+        "fwd_attention_prepare_bf16", "attention_prepare_fast",
+        2 * T * (nh + 2 * kv) * hd * 2 + 2 * hd * 2 + 2 * S * (rd // 2) * 4,
         lambda i: (randn((T, qkv_w), bf), torch.empty((B, nh, S, hd), dtype=bf, device=dev),
+                   torch.empty((B, kv, hd, S), dtype=bf, device=dev),
                    torch.empty((B, kv, S, hd), dtype=bf, device=dev)),
-        qk_launch, [B, S, nh, kv, hd, rd], "bfloat16", group="forward", launches=n_full))
+        prep_launch, [B, S, nh, kv, hd, rd], "bfloat16", group="forward", launches=n_full))
     vh, vd = cfg.value_heads, cfg.value_dim
     cq = 2 * cfg.key_dim * cfg.key_heads + vh * vd
     pw = -(-(cq + vh * vd + 2 * vh) // 256) * 256
@@ -439,9 +440,9 @@ E2E_BATCH, E2E_SEQ = 8, 2048
 
 def fused_sequence(cfg, dev, tokens):
     """The fused row-kernel launches of one bf16 forward at `tokens` tokens
-    (gather, input norm, 2 residual norms per layer, SwiGLU per layer, q/k
-    norm + RoPE per full-attention layer, gated norm per DeltaNet layer) on
-    buffers of the forward's shapes and strides."""
+    (gather, input norm, 2 residual norms per layer, SwiGLU per layer, the
+    attention prologue per full-attention layer, gated norm per DeltaNet layer)
+    on buffers of the forward's shapes and strides."""
     import torch
     from qdc_amd import ops
     bf, f32 = torch.bfloat16, torch.float32
@@ -459,10 +460,11 @@ def fused_sequence(cfg, dev, tokens):
     hd, nh, kv = cfg.head_dim, cfg.heads, cfg.kv_heads
     qkv = rn((tokens, 2 * hd * nh + 2 * hd * kv), bf)
     qn = rn((hd,), bf)
-    # head-major per sequence, as the forward writes them for the attention products
+    # the layouts the forward writes for the attention products
     n_seq = tokens // E2E_SEQ
-    q_out = torch.empty((n_seq, nh, E2E_SEQ, hd), dtype=bf, device=dev).permute(0, 2, 1, 3)
-    k_out = torch.empty((n_seq, kv, E2E_SEQ, hd), dtype=bf, device=dev).permute(0, 2, 1, 3)
+    prep_out = (torch.empty((n_seq, nh, E2E_SEQ, hd), dtype=bf, device=dev),
+                torch.empty((n_seq, kv, hd, E2E_SEQ), dtype=bf, device=dev),
+                torch.empty((n_seq, kv, E2E_SEQ, hd), dtype=bf, device=dev))
     tables = ops.rope_tables(E2E_SEQ, cfg.rotary_dim, cfg.rope_theta, dev)
     vw = cfg.value_dim * cfg.value_heads
     cq = 2 * cfg.key_dim * cfg.key_heads + vw
@@ -477,10 +479,10 @@ def fused_sequence(cfg, dev, tokens):
         ops.native_rms(h, w, 1e-6, out=normed)
         for kind in cfg.layer_types:
             if kind == "full_attention":
-                ops.prepare_heads(qkv[:, :2 * hd * nh].view(tokens, nh, 2 * hd)[:, :, :hd],
-                                  qkv[:, 2 * hd * nh:2 * hd * nh + hd * kv].view(tokens, kv, hd),
-                                  qn, qn, tables, cfg.rotary_dim, 1e-6, seq_len=E2E_SEQ,
-                                  q_out=q_out, k_out=k_out)
+                ops.attention_prepare(qkv[:, :hd * nh].view(tokens, nh, hd),
+                                      qkv[:, hd * nh:hd * (nh + kv)].view(tokens, kv, hd),
+                                      qkv[:, hd * (nh + kv):hd * (nh + 2 * kv)].view(tokens, kv, hd),
+                                      qn, qn, tables, cfg.rotary_dim, 1e-6, n_seq, out=prep_out)
             else:
                 ops.native_gated_rms(dx, proj[:, cq:cq + vw].view(tokens, cfg.value_heads,
                                                                   cfg.value_dim), wv, 1e-6,

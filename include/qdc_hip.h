@@ -21,8 +21,9 @@
  *    slower general kernel; the fast kernels need 16-byte alignment.
  *  - Size limits (QDC_ERR_SHAPE beyond them) keep every launch grid below 2^32
  *    work-items: fewer than 2^26 rows for the RMSNorm entry points (tokens *
- *    heads for the gated norm), q rows + k rows for qdc_qk_norm_rope, ids for
- *    the gather, score rows for the softmax and tokens for the DeltaNet prologue.
+ *    heads for the gated norm), q rows + k rows for qdc_qk_norm_rope, q + k + v
+ *    rows for qdc_attention_prepare, ids for the gather, score rows for the
+ *    softmax and tokens for the DeltaNet prologue.
  */
 #ifndef QDC_HIP_H
 #define QDC_HIP_H
@@ -184,6 +185,36 @@ int32_t qdc_qk_norm_rope_batched(void *q_out, void *k_out, const void *q_in, con
                                  int64_t q_out_tok, int64_t q_out_head, int64_t k_in_tok,
                                  int64_t k_in_head, int64_t k_out_seq, int64_t k_out_tok,
                                  int64_t k_out_head, float eps, int32_t dtype, hipStream_t stream);
+
+/*
+ * The attention prologue of a full-attention layer in one launch, for `batch`
+ * sequences of `seq_len` tokens (token t = b*seq_len + s at position
+ * pos_offset + s): each Q and K head row is normalised with its zero-centred
+ * RMSNorm weight and rotated by half-split partial RoPE (as qdc_qk_norm_rope),
+ * and each V head row is moved, into the layouts the two attention products
+ * read as plain batched GEMMs:
+ *   q_out [batch, heads, seq_len, head_dim]
+ *   k_out [batch, kv_heads, head_dim, seq_len]   (K transposed)
+ *   v_out [batch, kv_heads, seq_len, head_dim]
+ * (contiguous).  Inputs: Q row (t, h) at q_in + t*q_in_tok + h*q_in_head
+ * (q_in_head = 2*head_dim reads q out of the interleaved q||gate projection);
+ * K row (t, g) at k_in + t*k_in_tok + g*head_dim, V row (t, g) at
+ * v_in + t*v_in_tok + g*head_dim (inputs may share one packed projection).
+ * Replaces prepare_head_kernel! for Q and for K and prepare_value_kernel!
+ * (ext/amdgpu_attention.jl:1-59, launches :119-155): K and V are not expanded
+ * per query head, since the heads/kv_heads query heads of KV head g are the
+ * rows of one [heads/kv_heads * seq_len, head_dim] block of q_out.  heads a
+ * multiple of kv_heads; tables as qdc_qk_norm_rope (pos_offset + seq_len <=
+ * table_len); outputs may not overlap each other or an input.
+ */
+int32_t qdc_attention_prepare(void *q_out, void *k_out, void *v_out, const void *q_in,
+                              const void *k_in, const void *v_in, const void *q_norm,
+                              const void *k_norm, const float *cos_table, const float *sin_table,
+                              int64_t batch, int64_t seq_len, int64_t heads, int64_t kv_heads,
+                              int64_t head_dim, int64_t rotary_dim, int64_t pos_offset,
+                              int64_t table_len, int64_t q_in_tok, int64_t q_in_head,
+                              int64_t k_in_tok, int64_t v_in_tok, float eps, int32_t dtype,
+                              hipStream_t stream);
 
 /*
  * Host-side RoPE tables, fp32 [n_pos, rotary_dim/2] each, built the way the

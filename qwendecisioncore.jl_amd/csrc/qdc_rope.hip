@@ -3,19 +3,8 @@
 // host-side RoPE table builder.
 //
 // Fast path (head_dim a power-of-two number >= 2 of 16-byte chunks, at most
-// 128, rotary_dim/2 a multiple of the chunk): a group of LPR = chunks/2 lanes
-// owns up to 4 consecutive heads of one token, two 16-byte chunks of each row
-// per lane, so the position's cos/sin and the norm weights are loaded once for
-// all of them.  When the rotary block fits in the first chunk of each lane
-// (2*hc <= LPR, hc = rotary_dim/2 / chunk a power of two), lane l holds chunks
-// l and l + LPR (whole cache lines per load) and swaps its rotary chunk with
-// lane l ^ hc, which holds the other half of the rotation pair; otherwise the
-// chunks are dealt so that each of the first hc lanes holds a whole rotation
-// pair (element i of the first rotary half and its partner i + half) and the
-// rotation needs no exchange.  Rows are normalised in registers; every input
-// byte is read from HBM once and every output byte written once.  cos/sin come
-// from small fp32 tables (L2-resident) built on the host exactly as the
-// reference CPU path builds them.
+// 128, rotary_dim/2 a multiple of the chunk): the row groups of
+// qdc_rope_rows.hpp, Q rows on the first workgroups and K rows on the rest.
 //
 // General path (any shape/alignment): one wavefront per row; the normalised
 // rotary block is staged in LDS so in-place operation stays correct.
@@ -24,228 +13,10 @@
 #include <type_traits>
 
 #include "qdc_common.hpp"
+#include "qdc_rope_rows.hpp"
 
 namespace qdc {
 namespace {
-
-template <typename T> struct Side {
-    const T *in;
-    T *out;
-    const T *w;
-    int64_t in_tok, in_head, out_tok, out_head;
-    int64_t out_seq;  // output stride between sequences of seq_len tokens
-    int64_t rows;  // tokens * heads of this side
-    FastDiv heads;
-};
-
-template <typename T> struct QKArgs {
-    Side<T> q, k;
-    const float *cos, *sin;
-    int64_t q_blocks;  // workgroups covering the Q rows; the rest cover K
-    FastDiv seq_len;
-    int64_t pos_offset;
-    int32_t half;      // rotary_dim / 2
-    int32_t dim;
-    float eps;
-};
-
-// Chunk held in slot `slot` (0 or 1) by lane `lane` of a row group: lanes below
-// hc hold a rotation pair (chunk lane of the first rotary half and chunk
-// lane + hc of the second), the others hold the remaining chunks in order.
-// A bijection of [0, 2*LPR) onto the lane slots whenever hc <= LPR.
-template <int LPR> __device__ __forceinline__ int pair_chunk(int lane, int slot, int hc) {
-    if (lane < hc) return lane + slot * hc;
-    return slot == 0 ? lane + hc : lane + LPR;
-}
-
-// One side (Q or K) of the fast kernel, pair-dealt chunks.  A group of LPR
-// lanes owns RPG consecutive heads of one token (heads % RPG == 0), so the
-// cos/sin of the token's position and the norm weights are loaded once for RPG
-// rows and every lane keeps 2*RPG row chunks in flight.
-template <typename T, int LPR, int RPG>
-__device__ __forceinline__ void qk_side_paired(const QKArgs<T> &a, const Side<T> &sd, int64_t block) {
-    constexpr int V = Elem<T>::kVec;
-    constexpr int GPB = kBlock / LPR;  // lane groups per workgroup
-    const int lane = threadIdx.x % LPR;
-    const int64_t row0 = (block * GPB + threadIdx.x / LPR) * RPG;
-    const bool active = row0 < sd.rows;
-    const int hc = a.half / V;  // chunks per half of the rotary block
-    const bool rotary = lane < hc;
-    const int c0 = pair_chunk<LPR>(lane, 0, hc), c1 = pair_chunk<LPR>(lane, 1, hc);
-
-    // Every load first: both chunks of each row, the norm weights and (rotary
-    // lanes) the cos/sin of the position, so the latencies overlap.
-    uint32_t t = 0, h0 = 0, tq = 0;  // token, first head, sequence
-    u32x4 x0[RPG], x1[RPG];
-    u32x4 cr[V / 4], sr[V / 4];
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) x0[r] = x1[r] = u32x4{0u, 0u, 0u, 0u};
-    if (active) {
-        t = fastdiv((uint32_t)row0, sd.heads);
-        h0 = (uint32_t)row0 - t * sd.heads.d;
-        tq = fastdiv(t, a.seq_len);
-        const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h0 * sd.in_head;
-#pragma unroll
-        for (int r = 0; r < RPG; ++r) {
-            x0[r] = load_stream(src + r * sd.in_head + c0 * V);
-            x1[r] = load_stream(src + r * sd.in_head + c1 * V);
-        }
-        if (rotary) {
-            const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
-            const int64_t i0 = pos * a.half + lane * V;
-#pragma unroll
-            for (int q = 0; q < V / 4; ++q) {
-                cr[q] = load_raw(a.cos + i0 + 4 * q);
-                sr[q] = load_raw(a.sin + i0 + 4 * q);
-            }
-        }
-    }
-    const u32x4 w0 = load_raw(sd.w + c0 * V), w1 = load_raw(sd.w + c1 * V);
-
-    float v0[RPG][V], v1[RPG][V], ss[RPG];
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) {
-        unpack(x0[r], v0[r]);
-        unpack(x1[r], v1[r]);
-        ss[r] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < V; ++j) ss[r] += v0[r][j] * v0[r][j];
-#pragma unroll
-        for (int j = 0; j < V; ++j) ss[r] += v1[r][j] * v1[r][j];
-    }
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) ss[r] = group_sum<LPR>(ss[r]);
-    if (!active) return;
-    float wv0[V], wv1[V];
-    unpack(w0, wv0);
-    unpack(w1, wv1);
-    T *dst = sd.out + (int64_t)tq * sd.out_seq + (int64_t)(t - tq * a.seq_len.d) * sd.out_tok +
-             (int64_t)h0 * sd.out_head;
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) {
-        const float s = rms_scale(ss[r], (float)a.dim, a.eps);
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-            v0[r][j] = (v0[r][j] * s) * (1.0f + wv0[j]);
-            v1[r][j] = (v1[r][j] * s) * (1.0f + wv1[j]);
-        }
-        if (rotary) {  // v0 = first-half element i, v1 = its partner i + half
-#pragma unroll
-            for (int q = 0; q < V / 4; ++q)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 4 * q + e;
-                    const float c = __uint_as_float(cr[q][e]), sn = __uint_as_float(sr[q][e]);
-                    const float a0 = v0[r][j], b0 = v1[r][j];
-                    v0[r][j] = a0 * c - b0 * sn;
-                    v1[r][j] = b0 * c + a0 * sn;
-                }
-        }
-        store_chunk(dst + r * sd.out_head + c0 * V, v0[r]);
-        store_chunk(dst + r * sd.out_head + c1 * V, v1[r]);
-    }
-}
-
-// One side, contiguous chunks (2*hc <= LPR, hc a power of two): lane l holds
-// chunks l and l + LPR, so each load instruction of a lane group covers whole
-// lines.  The rotary chunks are all in slot 0 of lanes [0, 2*hc); lane l and
-// lane l ^ hc hold the two halves of a rotation pair and swap their raw
-// chunks; each normalises the partner's chunk exactly as the partner does
-// (same row scale, same weights) before rotating its own.
-template <typename T, int LPR, int RPG>
-__device__ __forceinline__ void qk_side_contig(const QKArgs<T> &a, const Side<T> &sd, int64_t block) {
-    constexpr int V = Elem<T>::kVec;
-    constexpr int GPB = kBlock / LPR;
-    const int lane = threadIdx.x % LPR;
-    const int64_t row0 = (block * GPB + threadIdx.x / LPR) * RPG;
-    const bool active = row0 < sd.rows;
-    const int hc = a.half / V;
-    const bool rotary = lane < 2 * hc;
-    const bool first = lane < hc;  // holds element i of the pair (else i + half)
-    const int c0 = lane, c1 = lane + LPR;
-    const int pc = lane ^ hc;      // the partner's chunk (rotary lanes)
-
-    uint32_t t = 0, h0 = 0, tq = 0;  // token, first head, sequence
-    u32x4 x0[RPG], x1[RPG];
-    u32x4 cr[V / 4], sr[V / 4];
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) x0[r] = x1[r] = u32x4{0u, 0u, 0u, 0u};
-    if (active) {
-        t = fastdiv((uint32_t)row0, sd.heads);
-        h0 = (uint32_t)row0 - t * sd.heads.d;
-        tq = fastdiv(t, a.seq_len);
-        const T *src = sd.in + (int64_t)t * sd.in_tok + (int64_t)h0 * sd.in_head;
-#pragma unroll
-        for (int r = 0; r < RPG; ++r) {
-            x0[r] = load_stream(src + r * sd.in_head + c0 * V);
-            x1[r] = load_stream(src + r * sd.in_head + c1 * V);
-        }
-        if (rotary) {
-            const int64_t pos = a.pos_offset + (int64_t)(t - tq * a.seq_len.d);
-            const int64_t i0 = pos * a.half + (lane & (hc - 1)) * V;
-#pragma unroll
-            for (int q = 0; q < V / 4; ++q) {
-                cr[q] = load_raw(a.cos + i0 + 4 * q);
-                sr[q] = load_raw(a.sin + i0 + 4 * q);
-            }
-        }
-    }
-    const u32x4 w0 = load_raw(sd.w + c0 * V), w1 = load_raw(sd.w + c1 * V);
-    const u32x4 wp = load_raw(sd.w + (rotary ? pc : c0) * V);
-
-    // the partner's raw slot-0 chunk (lane ^ hc stays inside the lane group)
-    u32x4 xp[RPG];
-#pragma unroll
-    for (int r = 0; r < RPG; ++r)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xp[r][e] = (uint32_t)__shfl_xor((int)x0[r][e], hc, kWave);
-
-    float v0[RPG][V], v1[RPG][V], ss[RPG];
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) {
-        unpack(x0[r], v0[r]);
-        unpack(x1[r], v1[r]);
-        ss[r] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < V; ++j) ss[r] += v0[r][j] * v0[r][j];
-#pragma unroll
-        for (int j = 0; j < V; ++j) ss[r] += v1[r][j] * v1[r][j];
-    }
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) ss[r] = group_sum<LPR>(ss[r]);
-    if (!active) return;
-    float wv0[V], wv1[V], wvp[V];
-    unpack(w0, wv0);
-    unpack(w1, wv1);
-    unpack(wp, wvp);
-    T *dst = sd.out + (int64_t)tq * sd.out_seq + (int64_t)(t - tq * a.seq_len.d) * sd.out_tok +
-             (int64_t)h0 * sd.out_head;
-#pragma unroll
-    for (int r = 0; r < RPG; ++r) {
-        const float s = rms_scale(ss[r], (float)a.dim, a.eps);
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-            v0[r][j] = (v0[r][j] * s) * (1.0f + wv0[j]);
-            v1[r][j] = (v1[r][j] * s) * (1.0f + wv1[j]);
-        }
-        if (rotary) {
-            float p[V];
-            unpack(xp[r], p);
-#pragma unroll
-            for (int j = 0; j < V; ++j) p[j] = (p[j] * s) * (1.0f + wvp[j]);
-#pragma unroll
-            for (int q = 0; q < V / 4; ++q)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 4 * q + e;
-                    const float c = __uint_as_float(cr[q][e]), sn = __uint_as_float(sr[q][e]);
-                    v0[r][j] = first ? v0[r][j] * c - p[j] * sn : v0[r][j] * c + p[j] * sn;
-                }
-        }
-        store_chunk(dst + r * sd.out_head + c0 * V, v0[r]);
-        store_chunk(dst + r * sd.out_head + c1 * V, v1[r]);
-    }
-}
 
 // Q rows take workgroups [0, q_blocks), K rows the rest (block-uniform branch).
 template <typename T, int LPR, int RPGQ, int RPGK>

@@ -143,6 +143,18 @@ qdc_qk_norm_rope_batched(q_out, k_out, q_in, k_in, q_norm, k_norm, cos_table, si
           q_out_seq, q_out_tok, q_out_head, k_in_tok, k_in_head, k_out_seq, k_out_tok,
           k_out_head, eps, dtype, stream)
 
+qdc_attention_prepare(q_out, k_out, v_out, q_in, k_in, v_in, q_norm, k_norm, cos_table,
+                      sin_table, batch, seq_len, heads, kv_heads, head_dim, rotary_dim,
+                      pos_offset, table_len, q_in_tok, q_in_head, k_in_tok, v_in_tok, eps, dtype,
+                      stream) =
+    ccall(qdc_sym(:qdc_attention_prepare), Int32,
+          (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid},
+           Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Int64, Int64, Int64, Int64, Int64, Int64,
+           Int64, Int64, Int64, Int64, Int64, Int64, Float32, Int32, Ptr{Cvoid}),
+          q_out, k_out, v_out, q_in, k_in, v_in, q_norm, k_norm, cos_table, sin_table, batch,
+          seq_len, heads, kv_heads, head_dim, rotary_dim, pos_offset, table_len, q_in_tok,
+          q_in_head, k_in_tok, v_in_tok, eps, dtype, stream)
+
 qdc_rope_tables(cos_table, sin_table, n_pos, rotary_dim, theta) =
     ccall(qdc_sym(:qdc_rope_tables), Int32,
           (Ptr{Float32}, Ptr{Float32}, Int64, Int64, Float32),
@@ -272,11 +284,13 @@ end
 
 # ---------------------------------------------------------- full attention --
 # full_attention (ext/amdgpu_attention.jl:108-178).  The two prepare_head_kernel!
-# launches become one qdc_qk_norm_rope call writing q and k head-major
-# (dim, tokens, heads); K is normalised and rotated once per KV head and never
-# expanded: the `groups` query heads of KV head g are the contiguous block
+# launches and prepare_value_kernel! become one qdc_attention_prepare call: q
+# normalised and rotated into (dim, tokens, heads), K into its transpose
+# (tokens, dim, kv_heads) and v into (dim, tokens, kv_heads), read in place from
+# the three projections.  K and V are never expanded per query head: the
+# `groups` query heads of KV head g are the contiguous block
 # q[:, :, (g-1)*groups+1:g*groups], one (dim, tokens*groups) matrix, so both
-# products run as strided batches over the KV heads.
+# products run as plain strided batches over the KV heads.
 function QwenDecisionCore.full_attention(attention, x::AMDGPU.ROCArray{Float32,2,ROCBuffer},
                                          mask, cfg)
     tokens = size(x, 2)
@@ -286,25 +300,22 @@ function QwenDecisionCore.full_attention(attention, x::AMDGPU.ROCArray{Float32,2
     kp = QwenDecisionCore.native_linear(attention.k, x)            # (dim*kv_heads, tokens)
     vp = QwenDecisionCore.native_linear(attention.v, x)
     q = scratch(Float32, (dim, tokens, heads))
-    k = scratch(Float32, (dim, tokens, kv_heads))
+    kt = scratch(Float32, (tokens, dim, kv_heads))                 # K transposed
+    v = scratch(Float32, (dim, tokens, kv_heads))
     cos_d, sin_d, table_len = cfg.rotary_dim > 0 ?
         qdc_device_rope_tables(tokens, cfg.rotary_dim, cfg.rope_theta) :
         (nothing, nothing, 0)
     cos_p = cos_d === nothing ? Ptr{Float32}(C_NULL) : qdc_fptr(cos_d)
     sin_p = sin_d === nothing ? Ptr{Float32}(C_NULL) : qdc_fptr(sin_d)
-    qdc_check(qdc_qk_norm_rope(qdc_ptr(q), qdc_ptr(k), qdc_ptr(qgate), qdc_ptr(kp),
-                               qdc_ptr(attention.q_norm), qdc_ptr(attention.k_norm), cos_p,
-                               sin_p, tokens, heads, kv_heads, dim, cfg.rotary_dim, tokens, 0,
-                               table_len,
-                               2dim * heads, 2dim, dim, dim * tokens,       # q in; q out
-                               dim * kv_heads, dim, dim, dim * tokens,      # k in; k out
-                               Float32(cfg.eps), QDC_F32, qdc_stream()), "prepare_heads")
-    # V head-major for the strided batches (the reference expands it per query head)
-    v = scratch(Float32, (dim, tokens, kv_heads))
-    permutedims!(v, reshape(vp, dim, kv_heads, tokens), (1, 3, 2))
+    qdc_check(qdc_attention_prepare(qdc_ptr(q), qdc_ptr(kt), qdc_ptr(v), qdc_ptr(qgate),
+                                    qdc_ptr(kp), qdc_ptr(vp), qdc_ptr(attention.q_norm),
+                                    qdc_ptr(attention.k_norm), cos_p, sin_p, 1, tokens, heads,
+                                    kv_heads, dim, cfg.rotary_dim, 0, table_len, 2dim * heads,
+                                    2dim, dim * kv_heads, dim * kv_heads, Float32(cfg.eps),
+                                    QDC_F32, qdc_stream()), "prepare_heads")
     scores = scratch(Float32, (tokens, tokens, heads))              # (keys, queries, heads)
-    batched_matmul!(reshape(scores, tokens, tokens * groups, kv_heads), k,
-                    reshape(q, dim, tokens * groups, kv_heads), 'T', 'N')
+    batched_matmul!(reshape(scores, tokens, tokens * groups, kv_heads), kt,
+                    reshape(q, dim, tokens * groups, kv_heads), 'N', 'N')
     device_mask = mask isa AMDGPU.ROCArray ? mask : QwenDecisionCore.native_prepare_mask(x, mask)
     # attention_softmax_kernel! (ext/amdgpu_attention.jl:61-88), in place
     qdc_check(qdc_attention_softmax(qdc_ptr(scores), QDC_F32, qdc_fptr(scores),

@@ -40,6 +40,7 @@ SIGNATURES = {
                          + [_f32, _i32, _vp]),
     "qdc_qk_norm_rope_batched": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 18
                                  + [_f32, _i32, _vp]),
+    "qdc_attention_prepare": (_i32, [_vp] * 10 + [_i64] * 12 + [_f32, _i32, _vp]),
     "qdc_rope_tables": (_i32, [_vp, _vp, _i64, _i64, _f32]),
     "qdc_gated_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                  _i32, _vp]),

@@ -4,8 +4,9 @@ Mirrors the reference's public entry points and their validation:
 
 * :class:`QwenBackbone` -- ``QwenBackbone(dir; device=:amdgpu)`` (``src/backbone.jl:74-192``):
   weights uploaded once, projection weights stored transposed and packed
-  (``[q; k; v]``, ``[qkv; z; a; b]``, ``[gate; up]``) the way the reference's AMDGPU
-  extension packs them (``ext/amdgpu_mlp.jl:15-52``).
+  (``[qkv; z; a; b]`` and ``[gate; up]`` the way the reference's AMDGPU extension
+  packs them, ``ext/amdgpu_mlp.jl:15-52``; the attention projections as
+  ``[q; k; v; gate]``, q_proj's per-head q and gate rows regrouped).
 * :func:`backbone_hidden` / :func:`backbone_last_hidden` (``src/backbone.jl:433-501``):
   one sequence per call, ids checked on the host (``check_sequence`` :413-422).
 * :func:`batch_backbone_hidden`: the optional batched hook (``src/backbone.jl:66-70``),
@@ -16,8 +17,9 @@ Per layer (``native_layer``, ``src/backbone.jl:363-388``) the fused kernels do
 the row work: the layer's input RMSNorm is fused with the previous layer's MLP
 residual add (``qdc_residual_rmsnorm``; the last one with the final norm) and,
 before a DeltaNet layer, with its input mask (``qdc_residual_rmsnorm_masked``),
-post-attention residual + RMSNorm, q/k norm + partial RoPE read straight out of
-the packed projection, the attention masked softmax and output-gate merge, the
+post-attention residual + RMSNorm, the attention prologue (q/k norm + partial
+RoPE, and K transposed and V head-major for the two products, read straight out
+of the packed projection), the attention masked softmax and output-gate merge, the
 DeltaNet prologue (convolution, SiLU, q/k L2 norm, gates), the gated-delta
 recurrence, the DeltaNet gated RMSNorm reading z inside the packed projection,
 and SwiGLU reading the packed gate||up GEMM output.  GEMMs and the two attention
@@ -75,7 +77,16 @@ class QwenBackbone:
             }
             if kind == "full_attention":
                 a = p + "self_attn."
-                layer.update(qkv=lin(a + "q_proj.weight", a + "k_proj.weight", a + "v_proj.weight"),
+                # q_proj's rows are [q_h; gate_h] per head; regrouped so the packed
+                # projection of a token is [q (all heads) | k | v | gate (all heads)]:
+                # the attention prologue reads q, k and v as one contiguous span
+                # and the gate merge reads the gate block whole
+                hd, H = cfg.head_dim, cfg.heads
+                qg = dev(weights[a + "q_proj.weight"]).reshape(H, 2, hd, -1)
+                layer.update(qkv=torch.cat([qg[:, 0].reshape(H * hd, -1),
+                                            dev(weights[a + "k_proj.weight"]),
+                                            dev(weights[a + "v_proj.weight"]),
+                                            qg[:, 1].reshape(H * hd, -1)], 0).t().contiguous(),
                              out=lin(a + "o_proj.weight"), q_norm=dev(weights[a + "q_norm.weight"]),
                              k_norm=dev(weights[a + "k_norm.weight"]))
             elif kind == "linear_attention":
@@ -184,35 +195,32 @@ class QwenBackbone:
 
     def _full_attention(self, layer, x, mask32, B, S):
         """``full_attention`` in the AMDGPU form (``ext/amdgpu_attention.jl:108-178``;
-        generic ``src/backbone.jl:224-262``).  Q and K are normalised and rotated
-        straight into head-major per-sequence layouts ``[B, H, S, hd]`` and
-        ``[B, KV, S, hd]``: the G = H / KV query heads sharing a KV head are then one
-        ``[G*S, hd]`` block, so both products run per (sequence, KV head) without
-        expanding K or V.  The masked softmax and the gate merge are HIP kernels."""
+        generic ``src/backbone.jl:224-262``).  One prologue launch normalises and
+        rotates q and k and moves v out of the packed projection into the layouts
+        the products read: q ``[B, H, S, hd]``, K transposed ``[B, KV, hd, S]``,
+        v ``[B, KV, S, hd]``.  The G = H / KV query heads sharing a KV head are one
+        ``[G*S, hd]`` block, so both products are plain batched GEMMs over
+        (sequence, KV head), with no K/V expansion and no layout copy.  The
+        masked softmax and the gate merge are HIP kernels."""
         cfg = self.cfg
         hd, H, KV = cfg.head_dim, cfg.heads, cfg.kv_heads
         G = H // KV
         T = B * S
-        dt = self.dtype
-        proj = x @ layer["qkv"]                              # [T, 2*hd*H + 2*hd*KV]
-        qgate = proj[:, :2 * hd * H].view(T, H, 2 * hd)
-        k_in = proj[:, 2 * hd * H:2 * hd * H + hd * KV].view(T, KV, hd)
-        v = proj[:, 2 * hd * H + hd * KV:].view(T, KV, hd)
+        proj = x @ layer["qkv"]                              # [T, q | k | v | gate]
+        q_in = proj[:, :H * hd].view(T, H, hd)
+        k_in = proj[:, H * hd:(H + KV) * hd].view(T, KV, hd)
+        v_in = proj[:, (H + KV) * hd:(H + 2 * KV) * hd].view(T, KV, hd)
+        gate = proj[:, (H + 2 * KV) * hd:].view(T, H, hd)
         tables = self.rope_tables(S) if cfg.rotary_dim else None
-        q = torch.empty((B, H, S, hd), dtype=dt, device=self.device)
-        k = torch.empty((B, KV, S, hd), dtype=dt, device=self.device)
-        # all sequences in one launch, written head-major per sequence
-        ops.prepare_heads(qgate[:, :, :hd], k_in, layer["q_norm"], layer["k_norm"], tables,
-                          cfg.rotary_dim, cfg.eps, seq_len=S, q_out=q.permute(0, 2, 1, 3),
-                          k_out=k.permute(0, 2, 1, 3))
-        kt = k.transpose(-1, -2).contiguous().view(B * KV, hd, S)
-        vh = v.view(B, S, KV, hd).permute(0, 2, 1, 3).contiguous().view(B * KV, S, hd)
-        scores = self._bmm32(q.view(B * KV, G * S, hd), kt)          # [B*KV, G*S, S] fp32
+        q, kt, v = ops.attention_prepare(q_in, k_in, v_in, layer["q_norm"], layer["k_norm"],
+                                         tables, cfg.rotary_dim, cfg.eps, B)
+        scores = self._bmm32(q.view(B * KV, G * S, hd), kt.view(B * KV, hd, S))  # [B*KV, G*S, S]
         scale = float(np.float32(1) / np.sqrt(np.float32(hd)))      # inv(sqrt(Float32(dim)))
-        probs = ops.attention_softmax(scores.view(B, H, S, S), mask32, scale, out_dtype=dt,
-                                      out=scores.view(B, H, S, S) if dt == torch.float32 else None)
-        values = self._bmm32(probs.view(B * KV, G * S, S), vh)       # [B, H, S, hd] fp32
-        merged = ops.attention_gate(values.view(B, H, S, hd), qgate[:, :, hd:], out_dtype=dt)
+        probs = ops.attention_softmax(scores.view(B, H, S, S), mask32, scale, out_dtype=self.dtype,
+                                      out=scores.view(B, H, S, S) if self.dtype == torch.float32
+                                      else None)
+        values = self._bmm32(probs.view(B * KV, G * S, S), v.view(B * KV, S, hd))  # [B, H, S, hd]
+        merged = ops.attention_gate(values.view(B, H, S, hd), gate, out_dtype=self.dtype)
         return self._mm32(merged, layer["out"])
 
     def _bmm32(self, a, b):

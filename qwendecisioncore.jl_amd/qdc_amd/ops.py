@@ -317,6 +317,56 @@ def prepare_heads(q: torch.Tensor | None, k: torch.Tensor | None, q_norm, k_norm
     return qo, ko
 
 
+def attention_prepare(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm: torch.Tensor,
+                      k_norm: torch.Tensor, tables, rotary_dim: int, eps: float, batch: int,
+                      pos_offset: int = 0, out=None):
+    """The attention prologue in one launch (``prepare_head_kernel!`` for Q and K
+    and ``prepare_value_kernel!``, ``ext/amdgpu_attention.jl:1-59``): per-head
+    zero-centred RMSNorm + half-split partial RoPE of ``q [T, H, hd]`` and
+    ``k [T, KV, hd]``, and ``v [T, KV, hd]`` moved, for ``batch`` sequences of
+    ``T // batch`` tokens.  ``q``/``k``/``v`` are views with contiguous rows (q may
+    stride its heads, e.g. inside a q||gate projection; k and v heads are
+    contiguous within a token).  Returns ``(q_out [B, H, S, hd], k_t [B, KV, hd, S],
+    v_out [B, KV, S, hd])``: K transposed, so both attention products are plain
+    batched GEMMs.  ``out`` optionally supplies the three contiguous outputs."""
+    _device(q, k, v, q_norm, k_norm)
+    code = _dtype_code(q, k, v, q_norm, k_norm)
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
+        raise ValueError("q must be [T, H, hd] and k, v [T, KV, hd]")
+    T, H, hd = q.shape
+    KV = k.shape[1]
+    if k.shape[0] != T or k.shape[2] != hd or batch <= 0 or T % batch:
+        raise ValueError("q, k and v must share tokens and head_dim; tokens a multiple of batch")
+    for t in (q, k, v):
+        if t.stride(2) != 1:
+            raise ValueError("rows must be contiguous")
+    for t in (k, v):
+        if KV > 1 and t.stride(1) != hd:
+            raise ValueError("k and v heads must be contiguous within a token")
+    if q_norm.numel() != hd or k_norm.numel() != hd:
+        raise ValueError("norm weights must be vectors of head_dim")
+    S = T // batch
+    shapes = ((batch, H, S, hd), (batch, KV, hd, S), (batch, KV, S, hd))
+    if out is None:
+        out = tuple(torch.empty(sh, dtype=q.dtype, device=q.device) for sh in shapes)
+    for o, sh in zip(out, shapes):
+        _device(q, o)
+        if o.dtype != q.dtype or tuple(o.shape) != sh or not o.is_contiguous():
+            raise ValueError("out must be three contiguous tensors [B, H, S, hd], "
+                             "[B, KV, hd, S], [B, KV, S, hd] of q's dtype")
+    cos, sin = tables if rotary_dim else (None, None)
+    ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+    tok = lambda t: t.stride(0) if T > 1 else t.shape[1] * t.shape[2]  # noqa: E731
+    check(lib().qdc_attention_prepare(out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
+                                      q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      q_norm.data_ptr(), k_norm.data_ptr(), ptr(cos), ptr(sin),
+                                      batch, S, H, KV, hd, rotary_dim, pos_offset,
+                                      cos.shape[0] if rotary_dim else 0, tok(q),
+                                      q.stride(1) if H > 1 else hd, tok(k), tok(v), eps, code,
+                                      _stream(q)), "attention_prepare")
+    return out
+
+
 # ----------------------------------------------------------------- SwiGLU ---
 def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
                     out: torch.Tensor | None = None) -> torch.Tensor:

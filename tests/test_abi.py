@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 19, names
+    assert len(names) == 20, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name

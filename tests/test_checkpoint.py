@@ -92,8 +92,11 @@ def test_from_directory_packs_bf16_without_widening(tmp_path):
             assert layer["conv"].dtype == torch.float32
         else:
             a = p + "self_attn."
-            packed = torch.cat([t(a + n) for n in ("q_proj.weight", "k_proj.weight",
-                                                   "v_proj.weight")]).t()
+            # q_proj rows [q_h; gate_h] per head, regrouped as [q; k; v; gate]
+            hd, H = model.cfg.head_dim, model.cfg.heads
+            qg = t(a + "q_proj.weight").reshape(H, 2, hd, -1)
+            packed = torch.cat([qg[:, 0].reshape(H * hd, -1), t(a + "k_proj.weight"),
+                                t(a + "v_proj.weight"), qg[:, 1].reshape(H * hd, -1)]).t()
             assert torch.equal(layer["qkv"], packed)
     # fp32 storage of the same checkpoint widens exactly
     wide = backbone.QwenBackbone.from_directory(str(tmp_path), device="cpu", dtype=torch.float32)

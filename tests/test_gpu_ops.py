@@ -995,3 +995,77 @@ def test_device_copy():
     with pytest.raises(ValueError):
         ops.device_copy(torch.empty(32, dtype=torch.uint8, device=DEV),
                         torch.empty(24, dtype=torch.uint8, device=DEV))
+
+
+# ------------------------------------------------------ attention prologue ----
+PREP_CASES = [
+    # B, S, H, KV, hd, rotary, packed [q|k|v|gate] (else q read from interleaved q||gate)
+    (8, 2048, 8, 2, 256, 64, True),     # the 0.8B-like forward: fast path, bf16 LPR 16
+    (2, 200, 8, 2, 256, 64, False),     # a partial 64-token tile at each sequence end
+    (3, 40, 4, 1, 64, 16, True),        # the plumbing shape: LPR 4 (bf16) / 8 (fp32)
+    (2, 96, 4, 2, 128, 0, True),        # no rotation
+    (1, 37, 4, 2, 64, 16, True),        # seq not a multiple of a chunk: general path
+    (2, 16, 2, 1, 24, 8, False),        # head_dim not a multiple of a chunk: general path
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", PREP_CASES)
+def test_attention_prepare(dtype, case):
+    """q, k normalised + rotated and v moved by one launch into [B, H, S, hd],
+    K transposed [B, KV, hd, S] and [B, KV, S, hd], against the oracle's q/k
+    norm + RoPE per sequence (positions restart at every sequence, offset 3 in
+    the last case) and the v rows themselves (bit for bit)."""
+    from qdc_amd import ops
+    B, S, H, KV, hd, rd, packed = case
+    T = B * S
+    pos_offset = 3 if hd == 24 else 0
+    width = (2 * H + 2 * KV) * hd
+    proj = host((T, width), 41, 1.0, dtype)
+    qn, kn = host((hd,), 42, 0.02, dtype), host((hd,), 43, 0.02, dtype)
+    if packed:   # [q | k | v | gate]
+        qv, kv_ = proj[:, :H * hd].reshape(T, H, hd), proj[:, H * hd:(H + KV) * hd]
+        vv = proj[:, (H + KV) * hd:(H + 2 * KV) * hd]
+    else:        # [q0 g0 q1 g1 ... | k | v]
+        qv = proj[:, :2 * H * hd].reshape(T, H, 2 * hd)[:, :, :hd]
+        kv_, vv = proj[:, 2 * H * hd:(2 * H + KV) * hd], proj[:, (2 * H + KV) * hd:]
+    kv_, vv = kv_.reshape(T, KV, hd), vv.reshape(T, KV, hd)
+    d = dev(proj, dtype)
+    if packed:
+        qd = d[:, :H * hd].view(T, H, hd)
+        kd, vd = d[:, H * hd:(H + KV) * hd].view(T, KV, hd), d[:, (H + KV) * hd:(H + 2 * KV) * hd].view(T, KV, hd)
+    else:
+        qd = d[:, :2 * H * hd].view(T, H, 2 * hd)[:, :, :hd]
+        kd = d[:, 2 * H * hd:(2 * H + KV) * hd].view(T, KV, hd)
+        vd = d[:, (2 * H + KV) * hd:].view(T, KV, hd)
+    tables = ops.rope_tables(S + pos_offset, rd, 1e7, DEV) if rd else None
+    q_out, k_t, v_out = ops.attention_prepare(qd, kd, vd, dev(qn, dtype), dev(kn, dtype), tables, rd,
+                                              1e-6, B, pos_offset=pos_offset)
+    torch.cuda.synchronize()
+    cos, sin = O.rope_tables(S + pos_offset, rd, 1e7) if rd else (np.zeros((1, 0), np.float32),) * 2
+    exp_q = O.qk_norm_rope(np.ascontiguousarray(qv), qn, cos, sin, rd, 1e-6, S, pos_offset)
+    exp_k = O.qk_norm_rope(np.ascontiguousarray(kv_), kn, cos, sin, rd, 1e-6, S, pos_offset)
+    got_q = back(q_out).transpose(0, 2, 1, 3).reshape(T, H, hd)
+    got_k = back(k_t).transpose(0, 3, 1, 2).reshape(T, KV, hd)
+    report(f"prepare q {case}", got_q, exp_q, dtype)
+    report(f"prepare k {case}", got_k, exp_k, dtype)
+    got_v = v_out.permute(0, 2, 1, 3).reshape(T, KV, hd)
+    assert torch.equal(got_v, vd.contiguous()), case
+
+
+def test_attention_prepare_checks():
+    from qdc_amd import ops
+    T, H, KV, hd = 64, 4, 2, 64
+    q = torch.zeros((T, H, hd), device=DEV)
+    k = torch.zeros((T, KV, hd), device=DEV)
+    v = torch.zeros((T, KV, hd), device=DEV)
+    w = torch.zeros(hd, device=DEV)
+    tables = ops.rope_tables(16, 16, 1e4, DEV)
+    with pytest.raises(ValueError):     # sequences of 32 need 32 table rows
+        ops.attention_prepare(q, k, v, w, w, tables, 16, 1e-6, 2)
+    with pytest.raises(ValueError):     # tokens not a multiple of batch
+        ops.attention_prepare(q, k, v, w, w, ops.rope_tables(64, 16, 1e4, DEV), 16, 1e-6, 3)
+    with pytest.raises(ValueError):     # output overlapping an input
+        out = (q.view(1, H, T, hd), torch.empty((1, KV, hd, T), device=DEV),
+               torch.empty((1, KV, T, hd), device=DEV))
+        ops.attention_prepare(q, k, v, w, w, ops.rope_tables(64, 16, 1e4, DEV), 16, 1e-6, 1, out=out)

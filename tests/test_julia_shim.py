@@ -104,7 +104,7 @@ def shim_ccalls() -> list:
 
 def test_header_parses():
     protos = header_prototypes()
-    assert len(protos) == 19, sorted(protos)
+    assert len(protos) == 20, sorted(protos)
     assert protos["qdc_version"] == ("Cstring", [])
     assert protos["qdc_check_ids"] == ("Int32", ["Ptr{Int64}", "Int64", "Int64"])
 
