@@ -80,18 +80,21 @@ class Kernel:
     """One fused kernel at its benchmark shape with rotating buffer sets."""
 
     def __init__(self, name, symbol, algo_bytes, make_set, launch, shape, dtype, group="hot",
-                 flops=None, launches=None, ceiling=None):
+                 flops=None, launches=None, ceiling=None, workgroups=None):
         self.name, self.symbol, self.algo_bytes = name, symbol, algo_bytes
         self.shape, self.dtype = shape, dtype
         # (make_set, launch) of a plain kernel with this kernel's access pattern
         # and bytes, timed beside it as its ceiling (None: the contiguous copy)
         self.ceiling = ceiling
+        # workgroups of the kernel's launch grid (the rocprofv3 trace's Grid_Size
+        # / 256 confirms it), for the empty-launch floor timed beside it
+        self.workgroups = workgroups
         # "hot": the fused row kernels at the per-kernel shapes; "next": widened;
         # "forward": the fused row kernels as the 0.8B-like forward launches them
         self.group, self.flops = group, flops
         self.launches = launches  # launches per forward ("forward" group)
         self.launch = launch
-        self.sets = [make_set(i) for i in range(_sets(algo_bytes))]
+        self.sets = [make_set(i) for i in range(_sets(algo_bytes) if algo_bytes else 1)]
         self.graph = None
         self.avg_ms = None
 
@@ -129,18 +132,22 @@ def build_kernels(dev):
 
     kernels = []
 
-    def rms(name, rows, width, dtype):
+    def rms(name, rows, width, dtype, rows_per_wg):
         es = 2 if dtype == bf else 4
         w = randn((width,), dtype, 0.02)
         kernels.append(Kernel(
             name, "rms_rows_fast", 2 * rows * width * es + width * es,
             lambda i: (randn((rows, width), dtype), torch.empty((rows, width), dtype=dtype, device=dev)),
-            lambda s: ops.native_rms(s[0], w, 1e-6, out=s[1]), [rows, width], str(dtype)[6:]))
+            lambda s: ops.native_rms(s[0], w, 1e-6, out=s[1]), [rows, width], str(dtype)[6:],
+            workgroups=rows // rows_per_wg))
 
-    rms("rmsnorm_f32", 8192, 1024, f32)
-    rms("rmsnorm_bf16", 8192, 1024, bf)
-    rms("headnorm_f32", 81920, 256, f32)
-    rms("headnorm_bf16", 81920, 256, bf)
+    # rows per workgroup of rms_rows_fast: 256 / lanes per row (64 lanes x 4 groups
+    # for fp32 rows of 1024, 16 x 8 for bf16 rows of 1024, 32 x 2 and 16 x 2 for
+    # fp32 and bf16 rows of 256)
+    rms("rmsnorm_f32", 8192, 1024, f32, 4)
+    rms("rmsnorm_bf16", 8192, 1024, bf, 16)
+    rms("headnorm_f32", 81920, 256, f32, 8)
+    rms("headnorm_bf16", 81920, 256, bf, 16)
 
     T, H, KV, hd, rd, seq = 8192, 8, 2, 256, 64, 2048
     qn, kn = randn((hd,), bf, 0.02), randn((hd,), bf, 0.02)
@@ -153,7 +160,9 @@ def build_kernels(dev):
                    torch.empty((T, KV, hd), dtype=bf, device=dev)),
         lambda s: ops.prepare_heads(s[0], s[1], qn, kn, tables, rd, 1e-6, seq_len=seq,
                                     q_out=s[2], k_out=s[3]),
-        [T, H, KV, hd, rd, seq], "bfloat16"))
+        [T, H, KV, hd, rd, seq], "bfloat16",
+        # 16-lane groups of 4 Q heads / 2 K heads, 16 groups per workgroup
+        workgroups=T * H // 4 // 16 + T * KV // 2 // 16))
 
     vocab, hidden, n = 248320, 1024, 16384
     table = randn((vocab, hidden), bf, 0.02)
@@ -185,7 +194,7 @@ def build_kernels(dev):
         lambda i: (randn((Tr, Hr), bf), randn((Tr, Hr), bf),
                    torch.empty((Tr, Hr), dtype=bf, device=dev), torch.empty((Tr, Hr), dtype=bf, device=dev)),
         lambda s: ops.native_residual_rms(s[0], s[1], wr, 1e-6, residual=s[2], out=s[3]),
-        [Tr, Hr], "bfloat16"))
+        [Tr, Hr], "bfloat16", workgroups=Tr // 8))  # 32 lanes x 4 groups per row
 
     # Attention row work of one full-attention layer (8 sequences of 2048, 8 heads).
     # Softmax: the causally visible scores are read (the rest are -floatmax by
@@ -277,18 +286,29 @@ def build_forward_kernels(dev):
     ks = []
     wb, wf = randn((Hd,), bf, 0.02), randn((Hd,), f32, 0.02)
     table = randn((cfg.vocab, Hd), bf, 0.02)
+    # the gather fused with the first input norm, as the forward launches it:
+    # bf16 table rows -> fp32 residual rows + bf16 normalised rows
+    ks.append(Kernel(
+        "fwd_gather_rms_bf16", "gather_rms_fast", T * Hd * (2 + 4 + 2) + T * 4 + Hd * 2,
+        lambda i: (torch.randint(0, cfg.vocab, (T,), generator=g, device=dev, dtype=torch.int32),
+                   torch.empty((T, Hd), dtype=f32, device=dev),
+                   torch.empty((T, Hd), dtype=bf, device=dev)),
+        lambda s: ops.native_gather_rms(table, s[0], wb, 1e-6, hidden=s[1], normed=s[2]),
+        [T, Hd], "bfloat16->float32,bfloat16", group="forward", launches=1,
+        ceiling=row_copy_ceiling(dev, g, table, T, 3)))
+    # the two launches it replaces, at the same shapes (not launched by the forward)
     ks.append(Kernel(
         "fwd_gather_bf16_f32", "gather_widen", T * Hd * 2 + T * Hd * 4 + T * 4,
         lambda i: (torch.randint(0, cfg.vocab, (T,), generator=g, device=dev, dtype=torch.int32),
                    torch.empty((T, Hd), dtype=f32, device=dev)),
         lambda s: ops.native_gather(table, s[0], out=s[1], out_dtype=f32), [T, Hd],
-        "bfloat16->float32", group="forward", launches=1,
+        "bfloat16->float32", group="standalone",
         ceiling=row_copy_ceiling(dev, g, table, T, 2)))
     ks.append(Kernel(
         "fwd_input_rms_f32_bf16", "rms_rows_fast", T * Hd * (4 + 2) + Hd * 2,
         lambda i: (randn((T, Hd), f32), torch.empty((T, Hd), dtype=bf, device=dev)),
         lambda s: ops.native_rms(s[0], wb, 1e-6, out=s[1]), [T, Hd], "float32->bfloat16",
-        group="forward", launches=1))
+        group="standalone"))
     ks.append(Kernel(
         "fwd_residual_rms_f32_bf16", "rms_rows_fast", T * Hd * (4 + 4 + 4 + 2) + Hd * 2,
         lambda i: (randn((T, Hd), f32), randn((T, Hd), f32),
@@ -390,6 +410,24 @@ def time_gpu(kernels, steps):
     return start.elapsed_time(end)
 
 
+def empty_floors(kernels, steps, warmup):
+    """For each kernel with a known grid, qdc_empty over the same number of
+    workgroups, graph-replayed like the kernels: the fixed cost of the launch."""
+    import torch
+    from qdc_amd import ops
+    empties = [Kernel(f"empty_{k.name}", "empty_grid", 0, lambda i: (),
+                      lambda st, n=k.workgroups, d=torch.device("cuda:0"): ops.empty_launch(n, d),
+                      [k.workgroups], "-") for k in kernels if k.workgroups]
+    for i in range(warmup):
+        for e in empties:
+            e.run(i)
+    capture(empties, steps)
+    for e in empties:
+        e.graph.replay()
+    time_gpu(empties, steps)
+    return {e.name[len("empty_"):]: e for e in empties}
+
+
 def copy_ceilings(dev, kernels, steps, warmup):
     """For each kernel, the library's plain streaming copy (qdc_copy: one
     16-byte chunk per thread, nontemporal) of the same total bytes, half read
@@ -440,7 +478,7 @@ E2E_BATCH, E2E_SEQ = 8, 2048
 
 def fused_sequence(cfg, dev, tokens):
     """The fused row-kernel launches of one bf16 forward at `tokens` tokens
-    (gather, input norm, 2 residual norms per layer, SwiGLU per layer, the
+    (gather + first input norm, 2 residual norms per layer, SwiGLU per layer, the
     attention prologue per full-attention layer, gated norm per DeltaNet layer)
     on buffers of the forward's shapes and strides."""
     import torch
@@ -475,8 +513,7 @@ def fused_sequence(cfg, dev, tokens):
     I = cfg.intermediate
 
     def run():
-        ops.native_gather(table, ids, out=h, out_dtype=f32)
-        ops.native_rms(h, w, 1e-6, out=normed)
+        ops.native_gather_rms(table, ids, w, 1e-6, hidden=h, normed=normed)
         for kind in cfg.layer_types:
             if kind == "full_attention":
                 ops.attention_prepare(qkv[:, :hd * nh].view(tokens, nh, hd),
@@ -770,8 +807,10 @@ def main():
     time_gpu(kernels, args.steps)
     hot = [k for k in kernels if k.group == "hot"] or kernels
     fwd = [k for k in kernels if k.group == "forward"]
-    ceilings = copy_ceilings(dev, hot + [k for k in fwd if k not in hot], args.steps,
+    alone = [k for k in kernels if k.group == "standalone"]
+    ceilings = copy_ceilings(dev, hot + [k for k in fwd + alone if k not in hot], args.steps,
                              args.warmup)
+    floors = empty_floors(hot, args.steps, args.warmup)
     hot_ms = sum(k.avg_ms for k in hot) * args.steps
     step_bytes = sum(k.algo_bytes for k in hot)
     value = step_bytes * args.steps / (hot_ms / 1e3) / 1e9
@@ -796,6 +835,9 @@ def main():
                      ceiling_pct_peak=round(100 * rows.algo_bytes / (rows.avg_ms / 1e3) / 1e9
                                             / PEAK_GBS, 1),
                      pct_of_ceiling=round(100 * rows.avg_ms / k.avg_ms, 1))
+        f = floors.get(k.name)
+        if f is not None:  # an empty launch of the same grid
+            e.update(workgroups=k.workgroups, empty_us=round(f.avg_ms * 1e3, 3))
         if k.flops:
             tf = k.flops / (k.avg_ms / 1e3) / 1e12
             e.update(bound="mfma", tflops=round(tf, 2), mfma_f32_peak_tflops=MFMA_F32_PEAK_TF,
@@ -834,6 +876,11 @@ def main():
             "kernels": {k.name: dict(entry(k), launches_per_forward=k.launches) for k in fwd},
             "gbs_forward_weighted": round(fb / fs / 1e9, 1),
             "pct_peak_forward_weighted": round(100 * fb / fs / 1e9 / PEAK_GBS, 1)}
+        if alone:
+            line["forward_shapes"]["standalone"] = {
+                "note": "the gather and the first input norm as two launches at the forward's "
+                        "shapes; the forward runs them fused (fwd_gather_rms_bf16)",
+                "kernels": {k.name: entry(k) for k in alone}}
     if not args.no_e2e:
         for k in kernels:  # release the kernel benchmark's buffers first
             k.sets, k.graph = None, None

@@ -69,6 +69,25 @@ int32_t qdc_embedding_gather(void *out, int32_t out_dtype, const void *table, in
                              int32_t *error_flag, hipStream_t stream);
 
 /*
+ * The embedding gather fused with the first layer's input RMSNorm, one pass
+ * over the table rows: hidden[t, :] = table[ids[t], :] (fp32, the residual
+ * stream; bf16 table entries widened exactly by <<16) and normed[t, :] =
+ * zero-centred RMSNorm(hidden[t, :]) with `weight` (normed_dtype, as the
+ * weight), times token_mask[t] when token_mask is not NULL (the DeltaNet input
+ * mask when the first layer is a DeltaNet layer, as qdc_rmsnorm_masked).
+ * Replaces native_gather (ext/amdgpu_workspace.jl:206-236) followed by the
+ * first layer's native_rms (src/backbone.jl:364; ext/amdgpu_workspace.jl:
+ * 113-149), which reads the gathered rows back.  Ids as qdc_embedding_gather
+ * (an id outside [0, vocab) gives zero rows and sets *error_flag).  Outputs
+ * contiguous [n_ids, width]; no overlap with an input.
+ */
+int32_t qdc_embedding_gather_rmsnorm(void *hidden, void *normed, const void *table,
+                                     int32_t table_dtype, const int32_t *ids, const void *weight,
+                                     int32_t normed_dtype, const int32_t *token_mask,
+                                     int64_t n_ids, int64_t vocab, int64_t width, float eps,
+                                     int32_t *error_flag, hipStream_t stream);
+
+/*
  * Host-side id check of check_sequence / native_gather (src/backbone.jl:417-418,
  * ext/amdgpu_workspace.jl:223-224): QDC_OK when every ids[t] is in [0, vocab),
  * QDC_ERR_RANGE otherwise.  `ids` is host memory.
@@ -331,15 +350,24 @@ int32_t qdc_copy(void *dst, const void *src, int64_t bytes, hipStream_t stream);
  * Random-row copy: destination row i (row_bytes * repeat bytes, rows
  * contiguous) holds `repeat` copies of source row rows[i] (rows: device int32,
  * each in [0, n_src); one outside writes zeros).  row_bytes a multiple of 16,
- * repeat 1 or 2, both pointers 16-byte aligned, fewer than 2^31 chunks of 16
+ * repeat 1 to 4, both pointers 16-byte aligned, fewer than 2^31 chunks of 16
  * bytes (QDC_ERR_SHAPE otherwise); no overlap.  No counterpart in the
  * reference: the single-launch ceiling of the embedding gather's access
  * pattern (rows read at random places of a large table, written contiguously;
- * repeat = 2 writes as many bytes as the fp32-widening gather) that the
- * benchmark times beside the gathers.
+ * repeat = 2 writes as many bytes as the fp32-widening gather, repeat = 3 as
+ * many as the gather fused with the first bf16 norm) that the benchmark times
+ * beside the gathers.
  */
 int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows, int64_t n_rows,
                       int64_t n_src, int64_t row_bytes, int32_t repeat, hipStream_t stream);
+
+/*
+ * Launches `workgroups` workgroups of 256 threads that do nothing (fewer than
+ * 2^24 workgroups, QDC_ERR_SHAPE otherwise).  No counterpart in the reference:
+ * the fixed cost of a launch of a row kernel's grid, which the benchmark times
+ * beside the kernel and its same-size copy.
+ */
+int32_t qdc_empty(int64_t workgroups, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,8 @@
 // row kernel moving the same bytes can be held against (launch ramp-up and
 // drain included), so the benchmark times it beside each kernel; qdc_copy_rows
 // is the same for the embedding gather's access pattern (whole rows read at
-// random places of a large table, written contiguously).
+// random places of a large table, written contiguously), and qdc_empty the
+// fixed cost of a launch of a given grid (workgroups that do nothing).
 #include "qdc_common.hpp"
 
 namespace qdc {
@@ -20,6 +21,9 @@ __global__ __launch_bounds__(kBlock) void copy_chunks(u32x4 *__restrict__ dst,
 // chunks * 16 bytes; the grid (chunks rounded up to whole workgroups) stays
 // below 2^32 work-items
 constexpr int64_t kMaxChunks = ((int64_t)1 << 32) - kBlock;
+
+// An empty workgroup: the fixed cost of a launch of a given grid.
+__global__ __launch_bounds__(kBlock) void empty_grid() {}
 
 // Random-row copy: thread g copies 16-byte chunk c of source row rows[i]
 // (g = i * chunks + c) into each of the `repeat` copies of destination row i.
@@ -63,8 +67,8 @@ extern "C" int32_t qdc_copy(void *dst, const void *src, int64_t bytes, hipStream
 extern "C" int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows, int64_t n_rows,
                                  int64_t n_src, int64_t row_bytes, int32_t repeat,
                                  hipStream_t stream) {
-    if (n_rows < 0 || n_src < 0 || row_bytes < 0 || row_bytes % 16 != 0 ||
-        (repeat != 1 && repeat != 2))
+    if (n_rows < 0 || n_src < 0 || row_bytes < 0 || row_bytes % 16 != 0 || repeat < 1 ||
+        repeat > 4)
         return QDC_ERR_SHAPE;
     const int64_t chunks = row_bytes / 16;
     if (n_rows * chunks >= ((int64_t)1 << 31)) return QDC_ERR_SHAPE;
@@ -76,13 +80,22 @@ extern "C" int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows
         return QDC_ERR_ALIAS;
     const uint32_t total = (uint32_t)(n_rows * chunks);
     const dim3 grid((uint32_t)ceil_div(total, kBlock));
-    if (repeat == 1)
-        hipLaunchKernelGGL(copy_rows<1>, grid, dim3(kBlock), 0, stream, static_cast<u32x4 *>(dst),
-                           static_cast<const u32x4 *>(src), rows, total,
-                           make_fastdiv((uint32_t)chunks), n_src);
-    else
-        hipLaunchKernelGGL(copy_rows<2>, grid, dim3(kBlock), 0, stream, static_cast<u32x4 *>(dst),
-                           static_cast<const u32x4 *>(src), rows, total,
-                           make_fastdiv((uint32_t)chunks), n_src);
+#define QDC_ROWS(R)                                                                        \
+    if (repeat == R)                                                                       \
+        hipLaunchKernelGGL(copy_rows<R>, grid, dim3(kBlock), 0, stream,                    \
+                           static_cast<u32x4 *>(dst), static_cast<const u32x4 *>(src), rows, \
+                           total, make_fastdiv((uint32_t)chunks), n_src);
+    QDC_ROWS(1)
+    QDC_ROWS(2)
+    QDC_ROWS(3)
+    QDC_ROWS(4)
+#undef QDC_ROWS
+    return launch_status();
+}
+
+extern "C" int32_t qdc_empty(int64_t workgroups, hipStream_t stream) {
+    if (workgroups < 0 || workgroups >= ((int64_t)1 << 32) / kBlock) return QDC_ERR_SHAPE;
+    if (workgroups == 0) return QDC_OK;
+    hipLaunchKernelGGL(empty_grid, dim3((uint32_t)workgroups), dim3(kBlock), 0, stream);
     return launch_status();
 }

@@ -84,6 +84,14 @@ qdc_embedding_gather(out, out_dtype, table, table_dtype, ids, n_ids, vocab, hidd
            Ptr{Cvoid}),
           out, out_dtype, table, table_dtype, ids, n_ids, vocab, hidden, error_flag, stream)
 
+qdc_embedding_gather_rmsnorm(hidden, normed, table, table_dtype, ids, weight, normed_dtype,
+                             token_mask, n_ids, vocab, width, eps, error_flag, stream) =
+    ccall(qdc_sym(:qdc_embedding_gather_rmsnorm), Int32,
+          (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int32, Ptr{Int32}, Ptr{Cvoid}, Int32, Ptr{Int32},
+           Int64, Int64, Int64, Float32, Ptr{Int32}, Ptr{Cvoid}),
+          hidden, normed, table, table_dtype, ids, weight, normed_dtype, token_mask, n_ids, vocab,
+          width, eps, error_flag, stream)
+
 qdc_check_ids(ids::Vector{Int64}, vocab) =
     ccall(qdc_sym(:qdc_check_ids), Int32, (Ptr{Int64}, Int64, Int64), ids, length(ids), vocab)
 

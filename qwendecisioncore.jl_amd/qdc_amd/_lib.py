@@ -28,6 +28,8 @@ SIGNATURES = {
     "qdc_version": (ctypes.c_char_p, []),
     "qdc_status_string": (ctypes.c_char_p, [_i32]),
     "qdc_embedding_gather": (_i32, [_vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "qdc_embedding_gather_rmsnorm": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _i64, _i64,
+                                            _i64, _f32, _vp, _vp]),
     "qdc_check_ids": (_i32, [_vp, _i64, _i64]),
     "qdc_rmsnorm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _vp]),
     "qdc_residual_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _i32, _i32,
@@ -55,6 +57,7 @@ SIGNATURES = {
                                   _i64, _vp]),
     "qdc_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "qdc_copy_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
+    "qdc_empty": (_i32, [_i64, _vp]),
 }
 
 _lib = None

@@ -14,7 +14,8 @@ Mirrors the reference's public entry points and their validation:
   returns every position of every row.
 
 Per layer (``native_layer``, ``src/backbone.jl:363-388``) the fused kernels do
-the row work: the layer's input RMSNorm is fused with the previous layer's MLP
+the row work: the embedding gather is fused with the first input RMSNorm, each
+later layer's input RMSNorm with the previous layer's MLP
 residual add (``qdc_residual_rmsnorm``; the last one with the final norm) and,
 before a DeltaNet layer, with its input mask (``qdc_residual_rmsnorm_masked``),
 post-attention residual + RMSNorm, the attention prologue (q/k norm + partial
@@ -164,15 +165,16 @@ class QwenBackbone:
         the caller) is set by the gather when an id is outside the vocabulary."""
         B, S = ids.shape
         cfg = self.cfg
-        # residual stream h in fp32 (a bf16 table widens exactly while gathered)
-        h = ops.native_gather(self.embedding, ids.reshape(-1).contiguous(), out_dtype=torch.float32,
-                              error_flag=error_flag)
         mask32 = None if mask is None else mask.to(torch.int32).contiguous()
         # Masked tokens are zeroed before the DeltaNet projections (src/backbone.jl:286):
         # the norm producing a DeltaNet layer's input writes the masked rows itself.
         keep = None if mask32 is None else mask32.view(-1)
         delta_keep = lambda i: keep if self.layers[i]["kind"] != "full_attention" else None  # noqa: E731
-        normed = ops.native_rms(h, self.layers[0]["input_norm"], cfg.eps, token_mask=delta_keep(0))
+        # the gather fused with the first input norm: the residual stream h in
+        # fp32 (a bf16 table widens exactly) and its normalised rows in one pass
+        h, normed = ops.native_gather_rms(self.embedding, ids.reshape(-1).contiguous(),
+                                          self.layers[0]["input_norm"], cfg.eps,
+                                          token_mask=delta_keep(0), error_flag=error_flag)
         for i, layer in enumerate(self.layers):
             if layer["kind"] == "full_attention":
                 mixed = self._full_attention(layer, normed, mask32, B, S)

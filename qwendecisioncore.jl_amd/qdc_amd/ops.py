@@ -120,6 +120,51 @@ def native_gather(embedding: torch.Tensor, ids, out: torch.Tensor | None = None,
     return out
 
 
+def native_gather_rms(embedding: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor,
+                      eps: float, token_mask: torch.Tensor | None = None,
+                      error_flag: torch.Tensor | None = None, hidden: torch.Tensor | None = None,
+                      normed: torch.Tensor | None = None):
+    """The gather fused with the first layer's input norm: returns ``(hidden,
+    normed)``, ``hidden [n, width]`` fp32 = the gathered rows (the residual
+    stream) and ``normed`` = their zero-centred RMSNorm in the weight's dtype,
+    times ``token_mask`` when given.  ``ids`` a contiguous device int32 vector;
+    an id outside the vocabulary gives zero rows and sets ``error_flag``."""
+    _device(embedding, ids, weight)
+    if ids.dtype != torch.int32 or not ids.is_contiguous() or ids.dim() != 1:
+        raise ValueError("ids must be a contiguous int32 device vector")
+    if embedding.dim() != 2 or not embedding.is_contiguous() or embedding.dtype not in _DTYPES:
+        raise ValueError("embedding must be a contiguous float32/bfloat16 [vocab, width] tensor")
+    vocab, width = embedding.shape
+    if weight.dtype not in _DTYPES or weight.numel() != width or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous float32/bfloat16 vector of the row width")
+    n = ids.numel()
+    if hidden is None:
+        hidden = torch.empty((n, width), dtype=torch.float32, device=embedding.device)
+    if normed is None:
+        normed = torch.empty((n, width), dtype=weight.dtype, device=embedding.device)
+    _device(embedding, hidden, normed)
+    if (hidden.dtype != torch.float32 or hidden.shape != (n, width)
+            or not hidden.is_contiguous()):
+        raise ValueError("hidden must be a contiguous float32 [n_ids, width] tensor")
+    if normed.dtype != weight.dtype or normed.shape != (n, width) or not normed.is_contiguous():
+        raise ValueError("normed must be a contiguous [n_ids, width] tensor of the weight's dtype")
+    keep = _row_mask(token_mask, n, embedding)
+    flag = 0
+    if error_flag is not None:
+        _device(embedding, error_flag)
+        if error_flag.dtype != torch.int32 or error_flag.numel() < 1:
+            raise ValueError("error_flag must be an int32 device tensor")
+        flag = error_flag.data_ptr()
+    check(lib().qdc_embedding_gather_rmsnorm(hidden.data_ptr(), normed.data_ptr(),
+                                             embedding.data_ptr(), _DTYPES[embedding.dtype],
+                                             ids.data_ptr(), weight.data_ptr(),
+                                             _DTYPES[weight.dtype],
+                                             0 if keep is None else keep.data_ptr(), n, vocab,
+                                             width, eps, flag, _stream(embedding)),
+          "native_gather_rms")
+    return hidden, normed
+
+
 # ------------------------------------------------------------------ norms ---
 def _row_mask(token_mask: torch.Tensor | None, rows: int, like: torch.Tensor):
     """Validate an optional device int32 row mask (one 0/1 entry per row)."""
@@ -544,6 +589,13 @@ def device_copy_rows(dst: torch.Tensor, table: torch.Tensor, rows: torch.Tensor,
                               table.shape[0], row_bytes, repeat, _stream(table)),
           "device_copy_rows")
     return dst
+
+
+def empty_launch(workgroups: int, device) -> None:
+    """A launch of ``workgroups`` workgroups that do nothing on ``device``'s
+    current stream: the fixed cost of a grid of that size."""
+    check(lib().qdc_empty(workgroups, torch.cuda.current_stream(device).cuda_stream),
+          "empty_launch")
 
 
 def check_ids(ids: Sequence[int], vocab: int) -> None:

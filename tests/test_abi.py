@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 20, names
+    assert len(names) == 22, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -345,7 +345,7 @@ def test_copy_rows_validation():
     lib = _lib.lib()
     cr = lambda *a: lib.qdc_copy_rows(*a, None)  # noqa: E731
     assert cr(FAKE, FAKE, FAKE, 4, 10, 24, 1) == -2        # row bytes not a multiple of 16
-    assert cr(FAKE, FAKE, FAKE, 4, 10, 32, 3) == -2        # repeat 1 or 2
+    assert cr(FAKE, FAKE, FAKE, 4, 10, 32, 5) == -2        # repeat 1 to 4
     assert cr(FAKE, FAKE, FAKE, -1, 10, 32, 1) == -2
     assert cr(FAKE, FAKE, FAKE, 1 << 28, 10, 1 << 8, 1) == -2   # 2^32 chunks
     assert cr(None, FAKE, FAKE, 4, 10, 32, 1) == -1
@@ -353,3 +353,10 @@ def test_copy_rows_validation():
     assert cr(FAKE + 8, FAKE, FAKE, 4, 10, 32, 1) == -2    # misaligned
     assert cr(FAKE, FAKE + 64, 0x900000, 4, 10, 32, 2) == -5   # dst overlaps the table
     assert cr(None, None, None, 0, 10, 32, 1) == 0
+
+
+def test_empty_validation():
+    lib = _lib.lib()
+    assert lib.qdc_empty(-1, None) == -2
+    assert lib.qdc_empty(1 << 24, None) == -2
+    assert lib.qdc_empty(0, None) == 0

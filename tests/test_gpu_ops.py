@@ -317,7 +317,7 @@ def test_device_copy_rows():
     from qdc_amd import ops
     rng = np.random.default_rng(32)
     for vocab, hidden, n, repeat in ((248320, 1024, 16384, 1), (248320, 1024, 16384, 2),
-                                     (50, 24, 33, 2), (9, 8, 5, 1)):
+                                     (248320, 1024, 4096, 3), (50, 24, 33, 2), (9, 8, 5, 4)):
         bits = rng.integers(0, 1 << 16, size=(vocab, hidden), dtype=np.uint16)
         table = torch.from_numpy(bits.view(np.int16)).to(DEV)
         rows = rng.integers(0, vocab, size=n).astype(np.int32)
@@ -1069,3 +1069,48 @@ def test_attention_prepare_checks():
         out = (q.view(1, H, T, hd), torch.empty((1, KV, hd, T), device=DEV),
                torch.empty((1, KV, T, hd), device=DEV))
         ops.attention_prepare(q, k, v, w, w, ops.rope_tables(64, 16, 1e4, DEV), 16, 1e-6, 1, out=out)
+
+
+# ------------------------------------------------- gather + first input norm --
+@pytest.mark.parametrize("table_dtype,norm_dtype", [(torch.bfloat16, torch.bfloat16),
+                                                    (torch.float32, torch.float32),
+                                                    (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("vocab,width,n", [(248320, 1024, 16384), (4096, 256, 129), (64, 8, 65),
+                                           (100, 12, 33), (50, 1000, 7), (30, 4096, 5),
+                                           (60, 512, 70), (40, 2048, 9)])
+def test_gather_rms(table_dtype, norm_dtype, vocab, width, n):
+    """hidden = the gathered rows widened to fp32 bit for bit; normed = their
+    zero-centred RMSNorm (oracle, fp32 1e-5 / bf16 1e-2), masked rows times
+    their 0/1 entry bit for bit; out-of-range device ids give zero rows and
+    set the flag."""
+    from qdc_amd import ops
+    rng = np.random.default_rng(51)
+    table = host((vocab, width), 52, 0.02, table_dtype)
+    w = host((width,), 53, 0.02, norm_dtype)
+    ids = rng.integers(0, vocab, size=n).astype(np.int32)
+    ids[:2] = [0, vocab - 1][:min(2, n)]
+    dt, dw, di = dev(table, table_dtype), dev(w, norm_dtype), dev(ids, torch.int32)
+    hidden, normed = ops.native_gather_rms(dt, di, dw, 1e-6)
+    torch.cuda.synchronize()
+    rows = table[ids]
+    assert np.array_equal(back(hidden).view(np.uint32), rows.view(np.uint32))
+    report(f"gather_rms {vocab}x{width} n={n}", back(normed), O.rms(rows, w, 1e-6), norm_dtype)
+    mask = (rng.random(n) > 0.3).astype(np.int32)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    h2, masked = ops.native_gather_rms(dt, di, dw, 1e-6, token_mask=dev(mask, torch.int32),
+                                       error_flag=flag)
+    torch.cuda.synchronize()
+    assert flag.item() == 0 and torch.equal(h2, hidden)
+    got, plain = back(masked), back(normed)
+    assert np.array_equal(got[mask == 1].view(np.uint32), plain[mask == 1].view(np.uint32))
+    assert not got[mask == 0].any()
+    if n > 3:
+        bad = ids.copy()
+        bad[[1, n - 1]] = [vocab, -3]
+        h3, n3 = ops.native_gather_rms(dt, dev(bad, torch.int32), dw, 1e-6, error_flag=flag)
+        torch.cuda.synchronize()
+        assert flag.item() == 1
+        hb, nb = back(h3), back(n3)
+        assert not hb[[1, n - 1]].any() and not nb[[1, n - 1]].any()
+        keep = np.setdiff1d(np.arange(n), [1, n - 1])
+        assert np.array_equal(hb[keep].view(np.uint32), rows[keep].view(np.uint32))
