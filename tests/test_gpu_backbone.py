@@ -371,6 +371,26 @@ def _teacher_forced_layer(model, cfg, i, tr, h, normed, mask):
     return out, (c(h2), c(n2)), last
 
 
+def _free_running_layer(model, cfg, i, h, normed, mask):
+    """Layer i of the GPU forward on the GPU's own residual stream and input
+    norm (device tensors): returns the next (h, normed)."""
+    from qdc_amd import ops
+    T = h.shape[0]
+    L = model.layers[i]
+    mask32 = torch.from_numpy(mask.astype(np.int32)).to(model.device).view(1, -1)
+    if cfg.layer_types[i] == "full_attention":
+        mixed = model._full_attention(L, normed, mask32, 1, T)
+    else:  # the forward's masked norm writes 0/1 times the row: the same values
+        mixed = model._delta_attention(L, normed * mask32.view(-1, 1).to(normed.dtype), 1, T)
+    residual, post = ops.native_residual_rms(h, mixed, L["post_norm"], cfg.eps)
+    gate_up = post @ L["gate_up"]
+    inter = gate_up.shape[1] // 2
+    act = ops.native_mlp_gate(gate_up[:, :inter], gate_up[:, inter:])
+    last = i + 1 == len(cfg.layer_types)
+    nxt = model.final_norm if last else model.layers[i + 1]["input_norm"]
+    return ops.native_residual_rms(residual, model._mm32(act, L["down"]), nxt, cfg.eps)
+
+
 @pytest.mark.timeout(900)
 def test_full_depth_bf16_teacher_forced():
     """Every layer of the 24-layer bf16 forward, and every stage inside it that
@@ -380,16 +400,26 @@ def test_full_depth_bf16_teacher_forced():
     1e-5, each whole attention / DeltaNet block within 1e-2, and the next
     layer's input norm within 1e-2.  This is the per-rounding-point parity of
     the bf16 path at the full 0.8B-like shape; the GEMMs on the existing path
-    are printed, not asserted."""
+    are printed, not asserted.  Beside it the GPU forward runs free, layer by
+    layer on its own state, and its distance to the oracle after each layer is
+    printed: how per-layer agreement compounds over 24 layers.  Nothing about
+    the free run is asserted here (test_full_depth_qwen35_backbone holds the
+    end-to-end bar)."""
     cfg, weights, ids, mask = _full_depth_case(torch.bfloat16)
     model = model_for(weights, cfg, torch.bfloat16)
     cd = cfg.as_dict()
     _, mask, h, normed, tables = forward.embed(weights, cd, ids, mask, bf16=True)
     worst = {}
+    # the GPU's own forward, layer by layer from the same first input (free running)
+    free_h = torch.from_numpy(h).cuda()
+    free_n = torch.from_numpy(normed).cuda().to(torch.bfloat16)
+    free = []
     for i in range(len(cfg.layer_types)):
         tr = {}
         h_next, n_next = forward.backbone_layer(weights, cd, i, h, normed, mask, tables,
                                                 bf16=True, trace=tr)
+        free_h, free_n = _free_running_layer(model, cfg, i, free_h, free_n, mask)
+        free.append(normwise(free_n.float().cpu().numpy(), n_next))
         stages, (gh, gn), last = _teacher_forced_layer(model, cfg, i, tr, h, normed, mask)
         stages += [("next residual", gh, h_next, "f32"),
                    ("next input norm" if not last else "final norm", gn, n_next,
@@ -408,6 +438,8 @@ def test_full_depth_bf16_teacher_forced():
     for name, (err, flips, kind) in worst.items():
         print(f"teacher-forced bf16, worst over 24 layers: {name:26s} {kind:5s} normwise "
               f"{err:.2e}, elements rounded differently {flips:.2e}", flush=True)
+    print("free-running bf16, GPU vs bf16-storage oracle after each layer: "
+          + " ".join(f"{e:.1e}" for e in free), flush=True)
 
 
 @pytest.mark.timeout(900)
