@@ -15,17 +15,20 @@
 // two in [4, 32], the rotary block inside the first chunk of each lane, seq a
 // multiple of a chunk).  Workgroups take one of three roles:
 //   Q rows:  the row groups of qdc_rope_rows.hpp (consecutive heads of a token).
-//   K/V tiles: 64 tokens of one sequence and one KV head.  Each LPR-lane group
+//   K tiles: 64 tokens of one sequence and one KV head.  Each LPR-lane group
 //            normalises and rotates 64 / (256 / LPR) token rows (per-row
 //            positions), the tile is staged in LDS token-major with a row pitch
 //            of dim*es + 4 bytes, and read back a column at a time: lane (d, k)
 //            gathers tokens k*V .. k*V+V-1 of dimension d and stores them as one
 //            16-byte piece, so every 8 (bf16) or 16 (fp32) lanes write one whole
 //            128-byte line of a transposed row.  The 4-byte pad puts the 16-lane
-//            row writes and the column reads on distinct banks.  The same
-//            workgroup then copies the tile's V rows (one contiguous span of
-//            64 * dim elements in the head-major output).
-// The two roles are dealt through the grid in proportion.
+//            row writes and the column reads on distinct banks.
+//   V tiles: 16 tokens of one sequence and one KV head, copied into one
+//            contiguous span of 16 * dim elements of the head-major output.
+//            Small tiles: copying the V rows inside the K tiles (one workgroup per
+//            64 tokens) measured 5.5% slower for the whole launch at 8 x 2048
+//            tokens; 8-token tiles were 7% slower and 32-token tiles 1.5%.
+// The three roles are dealt through the grid in proportion.
 //
 // General path (any alignment or shape): one wavefront per (token, head) row;
 // the normalised rotary block is staged in LDS; K elements are written with the
@@ -48,14 +51,12 @@ template <typename T> struct PrepArgs {
     int64_t k_in_tok, v_in_tok;
     int64_t batch, seq, kv_heads;
     int64_t tiles;                     // tiles of kTileTokens per sequence
-    int64_t q_blocks, k_blocks;        // workgroups of the Q and K/V roles
+    int64_t q_blocks, k_blocks, v_blocks;
 };
 
-// One K/V tile: tokens [s0, s0 + 64) of sequence b, KV head g.  The V rows of
-// the tile are copied after the transposed K stores (loading them with the K
-// rows kept 32 more registers live across the K work and measured 5% slower).
+// One K tile: tokens [s0, s0 + 64) of sequence b, KV head g.
 template <typename T, int LPR>
-__device__ __forceinline__ void kv_tile(const PrepArgs<T> &a, int64_t index) {
+__device__ __forceinline__ void k_tile(const PrepArgs<T> &a, int64_t index) {
     constexpr int V = Elem<T>::kVec;
     constexpr int ES = (int)sizeof(T);
     constexpr int DIM = 2 * LPR * V;
@@ -78,8 +79,6 @@ __device__ __forceinline__ void kv_tile(const PrepArgs<T> &a, int64_t index) {
 
     // the K rows first (HBM); each row's cos/sin (L2-resident tables) just
     // before its rotation
-    constexpr int CH = 2 * LPR;                    // chunks per row
-    constexpr int VPT = kTileTokens * CH / kBlock; // V chunks per thread
     u32x4 x0[ROWS], x1[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -184,35 +183,54 @@ __device__ __forceinline__ void kv_tile(const PrepArgs<T> &a, int64_t index) {
         }
         store_raw(out + (int64_t)d * a.seq + k * V, piece);
     }
-    const int64_t rows_here = std::min<int64_t>(kTileTokens, a.seq - s0);
-    const T *vin = a.v_in + (b * a.seq + s0) * a.v_in_tok + g * DIM;
-    u32x4 vr[VPT];
+}
+
+// One V tile: kVTokens tokens of sequence b, KV head g; 16-byte chunks copied into the
+// head-major rows (one contiguous span), kVTokens * CH / kBlock chunks per thread.
+constexpr int kVTokens = 16;
+template <typename T, int LPR>
+__device__ __forceinline__ void v_tile(const PrepArgs<T> &a, int64_t index) {
+    constexpr int V = Elem<T>::kVec;
+    constexpr int CH = 2 * LPR;
+    constexpr int DIM = CH * V;
+    constexpr int PER = (kVTokens * CH + kBlock - 1) / kBlock;
+    const int64_t vt = (a.seq + kVTokens - 1) / kVTokens;
+    const int64_t g = index % a.kv_heads, bt = index / a.kv_heads;
+    const int64_t b = bt / vt, s0 = (bt - b * vt) * kVTokens;
+    const int64_t rows = std::min<int64_t>(kVTokens, a.seq - s0);
+    T *out = a.v_out + ((b * a.kv_heads + g) * a.seq + s0) * DIM;
+    const T *in = a.v_in + (b * a.seq + s0) * a.v_in_tok + g * DIM;
+    u32x4 r[PER];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int p = threadIdx.x + i * kBlock;
-        vr[i] = p / CH < rows_here ? load_stream(vin + (int64_t)(p / CH) * a.v_in_tok + (p % CH) * V)
-                                   : u32x4{0u, 0u, 0u, 0u};
+    for (int u = 0; u < PER; ++u) {
+        const int p = threadIdx.x + u * kBlock;
+        if (p < rows * CH) r[u] = load_stream(in + (int64_t)(p / CH) * a.v_in_tok + (p % CH) * V);
     }
-    // V rows into [b, g, s, :]: the tile's rows are one contiguous span
-    T *vout = a.v_out + ((b * a.kv_heads + g) * a.seq + s0) * DIM;
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int p = threadIdx.x + i * kBlock;
-        if (p / CH < rows_here) store_raw(vout + (int64_t)p * V, vr[i]);
+    for (int u = 0; u < PER; ++u) {
+        const int p = threadIdx.x + u * kBlock;
+        if (p < rows * CH) store_raw(out + (int64_t)p * V, r[u]);
     }
 }
 
-// Q and K/V workgroups are dealt through the grid in proportion (block i is a
-// Q block when floor((i+1)*nq/n) > floor(i*nq/n)), so both roles stream from
-// the first wave of workgroups to the last instead of the K/V tiles trailing.
+// Q, K and V workgroups are dealt through the grid in proportion (block i is a
+// Q block when floor((i+1)*nq/n) > floor(i*nq/n); the others split between K
+// and V the same way), so every role streams from the first wave of workgroups
+// to the last instead of one role trailing.
 template <typename T, int LPR, int RPGQ>
 __global__ __launch_bounds__(kBlock) void attention_prepare_fast(PrepArgs<T> a) {
-    const int64_t i = blockIdx.x, n = a.q_blocks + a.k_blocks;
+    const int64_t i = blockIdx.x, n = a.q_blocks + a.k_blocks + a.v_blocks;
     const int64_t q_upto = (i + 1) * a.q_blocks / n;   // Q blocks among [0, i]
-    if (q_upto > i * a.q_blocks / n)
+    if (q_upto > i * a.q_blocks / n) {
         qk_side_contig<T, LPR, RPGQ>(a.qk, a.qk.q, q_upto - 1);
+        return;
+    }
+    const int64_t j = i - q_upto, m = a.k_blocks + a.v_blocks;
+    const int64_t k_upto = (j + 1) * a.k_blocks / m;
+    if (k_upto > j * a.k_blocks / m)
+        k_tile<T, LPR>(a, k_upto - 1);
     else
-        kv_tile<T, LPR>(a, i - q_upto);
+        v_tile<T, LPR>(a, j - k_upto);
 }
 
 // General path: one wavefront per row; rows [0, tokens*heads) are Q, then
@@ -296,7 +314,8 @@ int32_t launch_fast(PrepArgs<T> a, hipStream_t stream) {
     constexpr int64_t gpb = kBlock / LPR;
     a.q_blocks = ceil_div(a.qk.q.rows / RPGQ, gpb);
     a.k_blocks = a.batch * a.tiles * a.kv_heads;
-    const int64_t blocks = a.q_blocks + a.k_blocks;
+    a.v_blocks = a.batch * ((a.seq + kVTokens - 1) / kVTokens) * a.kv_heads;
+    const int64_t blocks = a.q_blocks + a.k_blocks + a.v_blocks;
     hipLaunchKernelGGL((attention_prepare_fast<T, LPR, RPGQ>), dim3((uint32_t)blocks),
                        dim3(kBlock), 0, stream, a);
     return launch_status();
