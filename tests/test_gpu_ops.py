@@ -999,13 +999,14 @@ def test_device_copy():
 
 # ------------------------------------------------------ attention prologue ----
 PREP_CASES = [
-    # B, S, H, KV, hd, rotary, packed [q|k|v|gate] (else q read from interleaved q||gate)
-    (8, 2048, 8, 2, 256, 64, True),     # the 0.8B-like forward: fast path, bf16 LPR 16
-    (2, 200, 8, 2, 256, 64, False),     # a partial 64-token tile at each sequence end
-    (3, 40, 4, 1, 64, 16, True),        # the plumbing shape: LPR 4 (bf16) / 8 (fp32)
-    (2, 96, 4, 2, 128, 0, True),        # no rotation
-    (1, 37, 4, 2, 64, 16, True),        # seq not a multiple of a chunk: general path
-    (2, 16, 2, 1, 24, 8, False),        # head_dim not a multiple of a chunk: general path
+    # B, S, H, KV, hd, rotary, packed [q|k|v|gate] (else q read from interleaved q||gate), offset
+    (8, 2048, 8, 2, 256, 64, True, 0),     # the 0.8B-like forward: fast path, bf16 LPR 16
+    (2, 200, 8, 2, 256, 64, False, 0),     # a partial 64-token tile at each sequence end
+    (3, 40, 4, 1, 64, 16, True, 0),        # the plumbing shape: LPR 4 (bf16) / 8 (fp32)
+    (2, 96, 4, 2, 128, 0, True, 0),        # no rotation
+    (1, 37, 4, 2, 64, 16, True, 0),        # seq not a multiple of a chunk: general path
+    (2, 16, 2, 1, 24, 8, False, 3),        # head_dim not a multiple of a chunk: general path
+    (3, 72, 8, 2, 128, 32, True, 5),       # fast path with an offset: partial K and V tiles
 ]
 
 
@@ -1014,12 +1015,11 @@ PREP_CASES = [
 def test_attention_prepare(dtype, case):
     """q, k normalised + rotated and v moved by one launch into [B, H, S, hd],
     K transposed [B, KV, hd, S] and [B, KV, S, hd], against the oracle's q/k
-    norm + RoPE per sequence (positions restart at every sequence, offset 3 in
-    the last case) and the v rows themselves (bit for bit)."""
+    norm + RoPE per sequence (positions restart at every sequence, shifted by
+    the case's offset) and the v rows themselves (bit for bit)."""
     from qdc_amd import ops
-    B, S, H, KV, hd, rd, packed = case
+    B, S, H, KV, hd, rd, packed, pos_offset = case
     T = B * S
-    pos_offset = 3 if hd == 24 else 0
     width = (2 * H + 2 * KV) * hd
     proj = host((T, width), 41, 1.0, dtype)
     qn, kn = host((hd,), 42, 0.02, dtype), host((hd,), 43, 0.02, dtype)
