@@ -48,7 +48,14 @@ With the end-to-end run, `backbone.cpu` times the oracle's backbone_hidden of
 one 2048-token sequence of the same backbone in fp32 on the host (the
 reference runs one sequence per call) and `backbone.speedup_vs_cpu` compares.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+`decision` follows the reference's own inference benchmark (backbone_last_hidden
+of one sequence of 64, 128, 256 and 512 tokens on its synthetic 4-layer model's
+shapes, host in and out, median of 21 per length, aggregate = sum of medians),
+eager and served from recorded HIP graphs, with the oracle on one host thread
+beside it and the reference's published figures for the same protocol.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-e2e]
+                       [--no-decision]
 """
 from __future__ import annotations
 
@@ -663,6 +670,101 @@ def cpu_backbone(n_tokens=None):
                        f"({len(os.sched_getaffinity(0))} cores usable)")}
 
 
+DECISION_LENGTHS = (64, 128, 256, 512)
+# The reference's published numbers for the same protocol on its own hardware
+# (benchmark/results/inference-next-15-2026-10-24.txt): aggregate of the four
+# medians, backbone_last_hidden, Julia and BLAS on one thread.
+DECISION_REFERENCE = {"cuda_rtx3060_ms": 6.421419, "cpu_xeon_e5_2699v3_1thread_ms": 115.952651,
+                      "source": "benchmark/results/inference-next-15-2026-10-24.txt"}
+
+
+def _median_ms(f, warm=4, samples=21):
+    import statistics
+    for _ in range(warm):
+        f()
+    times = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        f()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
+
+
+def decision_latency(dev, samples=21):
+    """The reference's inference benchmark protocol (benchmark/inference.jl) on
+    its synthetic model's shapes (benchmark/synthetic.jl: 4 layers, 3 DeltaNet +
+    1 full attention, hidden 256, intermediate 512, fp32): backbone_last_hidden
+    of one sequence of 64, 128, 256 and 512 tokens, ids (0..n-1) mod 256 and an
+    all-ones mask from the host, the [hidden] result back on the host; 4 warm
+    calls, then the median of 21 timed calls per length; the aggregate is the sum
+    of the four medians.  Timed eager (one launch per op) and served from
+    recorded HIP graphs (qdc_amd.graphs; recording, which also picks the faster
+    GEMM library per length, excluded, as the reference excludes its CUDA graph
+    recording).  Every graph result is checked against the eager result (1e-5
+    normwise, fp32)."""
+    import numpy as np
+    import torch
+    from qdc_amd import backbone
+    from qdc_amd.config import synthetic_inference_config
+    from qdc_amd.graphs import LastHiddenGraphs
+    from qdc_amd.weights import random_weights
+    cfg = synthetic_inference_config()
+    model = backbone.QwenBackbone.from_weights(random_weights(cfg, seed=42), cfg, dev,
+                                               torch.float32)
+    graphs = LastHiddenGraphs(model, max_graphs=len(DECISION_LENGTHS))
+    eager, graphed, libraries = {}, {}, {}
+    for n in DECISION_LENGTHS:
+        ids = np.arange(n) % min(256, cfg.vocab)
+        mask = np.ones(n, np.int64)
+        want = backbone.backbone_last_hidden(model, ids, mask)
+        got = graphs(ids, mask)
+        err = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+        if not err <= 1e-5:   # fp32: the products may come from the other GEMM library
+            raise RuntimeError(f"graph-replayed last hidden is {err:.2e} from the eager one at {n}")
+        entry = graphs.entry(n, False)
+        libraries[n] = None if entry is None else entry.library
+        eager[n] = _median_ms(lambda: backbone.backbone_last_hidden(model, ids, mask),
+                              samples=samples)
+        graphed[n] = _median_ms(lambda: graphs(ids, mask), samples=samples)
+    agg_e, agg_g = sum(eager.values()), sum(graphed.values())
+    return {"workload": "backbone_last_hidden, one sequence of 64/128/256/512 tokens, the "
+                        "reference's synthetic inference model shapes (4 layers: 3 DeltaNet + 1 "
+                        "full, hidden 256, intermediate 512), fp32, host ids in, host [hidden] out",
+            "eager_ms": {str(n): round(v, 4) for n, v in eager.items()},
+            "graph_ms": {str(n): round(v, 4) for n, v in graphed.items()},
+            "aggregate_eager_ms": round(agg_e, 4), "aggregate_graph_ms": round(agg_g, 4),
+            "graph_keys_eager": sorted(str(k) for k in graphs.eager_keys),
+            "graph_gemm_library": {str(n): v for n, v in libraries.items()},
+            "reference_published": DECISION_REFERENCE,
+            "note": "the reference's figures are from other hardware (an RTX 3060 and a Xeon "
+                    "E5-2699 v3); same protocol and model shapes, not the same machine"}
+
+
+def cpu_decision(samples=5):
+    """The oracle's forward of the same synthetic model on the host, one thread
+    (BLAS limited to one thread as the reference's `julia -t 1` run), median of
+    `samples` per length after one warm call; the last row is the result."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import forward
+    from qdc_amd.config import synthetic_inference_config
+    from qdc_amd.weights import random_weights
+    cfg = synthetic_inference_config()
+    weights = random_weights(cfg, seed=42)
+    per = {}
+    with threadpool_limits(limits=1):
+        for n in DECISION_LENGTHS:
+            ids = np.arange(n) % min(256, cfg.vocab)
+            mask = np.ones(n, np.int64)
+            per[n] = _median_ms(lambda: forward.backbone_hidden(weights, cfg.as_dict(), ids,
+                                                                mask)[-1],
+                                warm=1, samples=samples)
+    return {"ms": {str(n): round(v, 3) for n, v in per.items()},
+            "aggregate_ms": round(sum(per.values()), 3), "cores": 1, "kind": "port",
+            "sample": f"oracle backbone_hidden (numpy, fp32) on 1 thread of '{cpu_model()}', "
+                      f"median of {samples} per length"}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -778,6 +880,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma-separated kernel names (profiling runs)")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end backbone run")
+    ap.add_argument("--no-decision", action="store_true",
+                    help="skip the single-sequence last-token latency run (--no-e2e skips it too)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 4 plain 512 MiB device copies (scales the PMC byte counters)")
     args = ap.parse_args()
@@ -886,12 +990,16 @@ def main():
             k.sets, k.graph = None, None
         torch.cuda.empty_cache()
         line["backbone"] = e2e_benchmark(dev)
+    if not (args.no_e2e or args.no_decision or args.only):
+        line["decision"] = decision_latency(dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
         if "backbone" in line:
             line["backbone"]["cpu"] = cpu_backbone()
             line["backbone"]["speedup_vs_cpu"] = round(
                 line["backbone"]["tokens_per_s"] / line["backbone"]["cpu"]["tokens_per_s"], 1)
+        if "decision" in line:
+            line["decision"]["cpu"] = cpu_decision()
     print(json.dumps(line), flush=True)
 
 

@@ -13,7 +13,7 @@
 // qk_normalize_kernel! and the beta/decay broadcasts, ext/amdgpu_delta.jl:1-33, 83-113, 154-159.
 //
 // Fast path: a thread owns 4 consecutive channels for a tile of 40 (bf16) or 16
-// (fp32) consecutive tokens, loads the tile's rows and the K-1 halo rows before
+// (fp32) consecutive tokens (4 in short launches), loads the tile's rows and the K-1 halo rows before
 // it in one go, then slides a K-tap window down the tile, so each projection row
 // is read once from HBM (the halo comes from L2) and each output chunk is one
 // whole 16-byte store.  The kd/4 lanes of a key head are an aligned lane group,
@@ -59,6 +59,11 @@ __device__ __forceinline__ float softplus_f(float x) {
 // bf16 tiles of 40 tokens measured ~4% faster than 32 or 64 at the 0.8B shapes
 // (more rows in flight per wavefront against occupancy 3 instead of 4).
 template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 40 : 16; }
+// Short launches (a single sequence of a few hundred tokens) take tiles of 4
+// tokens: more workgroups on the chip and a 4-step chain per thread instead of
+// 40 (the 3 halo rows per tile come from L2).  Each token's arithmetic is the
+// same in either tile, so the outputs are bit-identical.
+constexpr int kSmallTile = 4;
 
 template <typename T> struct Raw4;  // 4 channels of one projection row
 template <> struct Raw4<bf16_t> {
@@ -76,10 +81,9 @@ template <> struct Raw4<float> {
     }
 };
 
-template <typename T, int LPH>
+template <typename T, int LPH, int kTileT>
 __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     using Raw = typename Raw4<T>::type;
-    constexpr int kTileT = tile_for<T>();
     constexpr int kRows = kTileT + kTaps - 1;  // rows t0-3 .. t0+tile-1
     // One-dimensional grid of tiles x channel blocks in plain order (the last
     // block of a tile computes the gates).  Dealing each XCD a contiguous run of
@@ -229,32 +233,53 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_general(Prologue a) {
     }
 }
 
+template <typename T, int TILE>
+int32_t launch_fast(Prologue q, int lph, hipStream_t stream) {
+    const int64_t blocks = ceil_div(q.tokens, TILE) * q.blocks_per_tile;
+    const dim3 grid((uint32_t)blocks);
+#define QDC_PRO(L)                                                                               \
+    case L:                                                                                      \
+        hipLaunchKernelGGL((delta_prologue_fast<T, L, TILE>), grid, dim3(kBlock), 0, stream, q); \
+        return launch_status();
+    switch (lph) {
+        QDC_PRO(1)
+        QDC_PRO(2)
+        QDC_PRO(4)
+        QDC_PRO(8)
+        QDC_PRO(16)
+        QDC_PRO(32)
+        QDC_PRO(64)
+        default:
+            break;
+    }
+#undef QDC_PRO
+    return kNoFastPath;
+}
+
+// Below this many workgroups with the large tiles (well under one per CU of the
+// 256) the launch takes 4-token tiles.  Measured crossover on MI355X, graph-
+// replayed: at the 0.8B DeltaNet dims (bf16, 7 workgroups per tile) 4-token
+// tiles are faster up to 512 tokens (11.0 against 14.6 us; 4.5 against 14.4 at
+// 64) and slower from 1024 (91 and 182 large-tile workgroups); at the 4-layer
+// synthetic dims (fp32, 2 per tile) faster up to 1024 tokens, slower from 2048
+// (128 and 256).
+constexpr int64_t kSmallTileBelow = 160;
+
 template <typename T>
 int32_t launch(const Prologue &p, bool fast, hipStream_t stream) {
     const int lph = p.kd / 4;
-    const int64_t fast_blocks = ceil_div(p.tokens, tile_for<T>()) * (ceil_div(p.chunks, kBlock) + 1);
+    const int64_t bpt = ceil_div(p.chunks, kBlock) + 1;
+    const int64_t big_blocks = ceil_div(p.tokens, tile_for<T>()) * bpt;
+    const bool small = big_blocks < kSmallTileBelow;
+    const int64_t fast_blocks = small ? ceil_div(p.tokens, kSmallTile) * bpt : big_blocks;
     // the fast grid is one-dimensional: fewer than 2^32 work-items
     if (fast && p.kd % 4 == 0 && p.vd % 4 == 0 && p.taps == kTaps && lph <= kWave &&
         (lph & (lph - 1)) == 0 && fast_blocks * kBlock < ((int64_t)1 << 32)) {
         Prologue q = p;
-        q.blocks_per_tile = (uint32_t)ceil_div(p.chunks, kBlock) + 1;
-        const dim3 grid((uint32_t)fast_blocks);
-#define QDC_PRO(L)                                                                               \
-    case L:                                                                                      \
-        hipLaunchKernelGGL((delta_prologue_fast<T, L>), grid, dim3(kBlock), 0, stream, q);     \
-        return launch_status();
-        switch (lph) {
-            QDC_PRO(1)
-            QDC_PRO(2)
-            QDC_PRO(4)
-            QDC_PRO(8)
-            QDC_PRO(16)
-            QDC_PRO(32)
-            QDC_PRO(64)
-            default:
-                break;
-        }
-#undef QDC_PRO
+        q.blocks_per_tile = (uint32_t)bpt;
+        const int32_t st = small ? launch_fast<T, kSmallTile>(q, lph, stream)
+                                 : launch_fast<T, tile_for<T>()>(q, lph, stream);
+        if (st != kNoFastPath) return st;
     }
     const dim3 grid((uint32_t)ceil_div(p.tokens, kBlock / kWave), (uint32_t)(2 * p.kh + 2));
     hipLaunchKernelGGL((delta_prologue_general<T>), grid, dim3(kBlock), 0, stream, p);

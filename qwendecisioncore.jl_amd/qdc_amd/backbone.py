@@ -268,7 +268,9 @@ def check_sequence(model: QwenBackbone, ids, mask) -> None:
         raise ValueError("Mask values must be zero or one.")
 
 
-def _device_inputs(model, ids, mask):
+def _host_sequence(model, ids, mask):
+    """One sequence's ids and mask as checked 1-D int64 host arrays (a ``[1, S]``
+    array is taken as its row)."""
     ids = np.asarray(ids, dtype=np.int64)
     mask = np.asarray(mask, dtype=np.int64)
     if ids.ndim == 2:
@@ -276,6 +278,11 @@ def _device_inputs(model, ids, mask):
             raise ValueError("Pass one sequence per call; batching is not implemented yet.")
         ids, mask = ids[0], mask[0]
     check_sequence(model, ids, mask)
+    return ids.reshape(-1), mask.reshape(-1)
+
+
+def _device_inputs(model, ids, mask):
+    ids, mask = _host_sequence(model, ids, mask)
     d_ids = torch.from_numpy(ids.astype(np.int32)).to(model.device).view(1, -1)
     if mask.all():  # nothing masked: the forward skips the masking work
         return d_ids, None

@@ -127,6 +127,18 @@ def plumbing_config() -> BackboneConfig:
                           intermediate=768, vocab=4096)
 
 
+def synthetic_inference_config() -> BackboneConfig:
+    """The shapes of the reference's inference benchmark model
+    (``benchmark/synthetic.jl:3-28``): 4 layers, DeltaNet x3 then full attention
+    (full at ``i % 4 == 0``, 1-based), hidden 256, intermediate 512, 4 Q / 2 KV
+    heads of 64 (rotary 16, theta 1e4), DeltaNet keys 2x128 / values 4x128,
+    vocab 256."""
+    return BackboneConfig(hidden=256, head_dim=64, heads=4, kv_heads=2, key_heads=2,
+                          value_heads=4, key_dim=128, value_dim=128,
+                          eps=float(np.float32(1e-6)), rope_theta=1e4, rotary_dim=16,
+                          layer_types=hybrid_layer_types(4), intermediate=512, vocab=256)
+
+
 def qwen35_08b_config(depth: int = 24) -> BackboneConfig:
     """Qwen3.5-0.8B-like shapes: hidden 1024, 8 Q / 2 KV heads of 256 (rotary 64),
     DeltaNet 16 key heads x 128 and 16 value heads x 128, intermediate 3584,

@@ -766,8 +766,9 @@ def test_delta_scan_chunked_matches_recurrent(B, S, KH, H, kd, vd):
 # ------------------------------------------------ DeltaNet prologue ----------
 # (B, S, KH, kd, H, vd, taps, pad): pad > 0 widens the row stride by pad elements
 PROLOGUE_CASES = [
-    (2, 1024, 16, 128, 16, 128, 4, 0),   # Qwen3.5-0.8B DeltaNet dims, fast path
-    (2, 37, 2, 128, 4, 128, 4, 0),       # sequences break inside a 16-token tile
+    (2, 1024, 16, 128, 16, 128, 4, 0),   # Qwen3.5-0.8B DeltaNet dims: 40/16-token tiles
+    (1, 200, 16, 128, 16, 128, 4, 0),    # the same dims, one short sequence: 4-token tiles
+    (2, 37, 2, 128, 4, 128, 4, 0),       # sequences break inside a (4-token) tile
     (3, 5, 1, 64, 2, 32, 4, 8),          # strided rows
     (7, 1, 2, 16, 2, 8, 4, 0),           # every token starts a sequence
     (2, 33, 1, 8, 4, 16, 4, 0),          # one lane per key head
