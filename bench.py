@@ -55,7 +55,7 @@ eager and served from recorded HIP graphs, with the oracle on one host thread
 beside it and the reference's published figures for the same protocol.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-e2e]
-                       [--no-decision]
+                       [--no-decision | --decision-only]
 """
 from __future__ import annotations
 
@@ -882,6 +882,8 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end backbone run")
     ap.add_argument("--no-decision", action="store_true",
                     help="skip the single-sequence last-token latency run (--no-e2e skips it too)")
+    ap.add_argument("--decision-only", action="store_true",
+                    help="run only the single-sequence last-token latency run (profiling runs)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 4 plain 512 MiB device copies (scales the PMC byte counters)")
     args = ap.parse_args()
@@ -895,6 +897,12 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.decision_only:
+        line = {"decision": decision_latency(dev)}
+        if not args.no_cpu:
+            line["decision"]["cpu"] = cpu_decision()
+        print(json.dumps(line), flush=True)
+        return
     if args.calibrate:
         calibrate(dev)
     kernels = build_kernels(dev) + build_forward_kernels(dev)
