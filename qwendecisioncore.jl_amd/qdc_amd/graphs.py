@@ -187,15 +187,16 @@ class LastHiddenGraphs:
         previous = backends.preferred_blas_library()
         best = None
         try:
-            for library in self.gemm_libraries or (previous,):
-                backends.preferred_blas_library(library)
-                e = self._record_one(seq_len, masked)
-                if MEMSET_NODE in e.nodes:
-                    continue
-                e.library = str(library)
-                e.replay_ms = self._replay_ms(e)
-                if best is None or e.replay_ms < best.replay_ms:
-                    best = e
+            with torch.cuda.device(self.model.device):
+                for library in self.gemm_libraries or (previous,):
+                    backends.preferred_blas_library(library)
+                    e = self._record_one(seq_len, masked)
+                    if MEMSET_NODE in e.nodes:
+                        continue
+                    e.library = str(library)
+                    e.replay_ms = self._replay_ms(e)
+                    if best is None or e.replay_ms < best.replay_ms:
+                        best = e
         finally:
             backends.preferred_blas_library(previous)
         return best
@@ -225,13 +226,14 @@ class LastHiddenGraphs:
             e = self.entry(ids.size, masked)
             if e is None:
                 return bb.backbone_last_hidden(self.model, ids, mask)
-            stream = torch.cuda.current_stream(self.model.device)
-            e.ids_host[0].numpy()[:] = ids
-            e.ids.copy_(e.ids_host, non_blocking=True)
-            if masked:
-                e.mask_host[0].numpy()[:] = mask
-                e.mask.copy_(e.mask_host, non_blocking=True)
-            e.graph.replay()
-            e.out_host.copy_(e.out.float(), non_blocking=True)
-            stream.synchronize()
-            return e.out_host.numpy().copy()
+            with torch.cuda.device(self.model.device):
+                stream = torch.cuda.current_stream(self.model.device)
+                e.ids_host[0].numpy()[:] = ids
+                e.ids.copy_(e.ids_host, non_blocking=True)
+                if masked:
+                    e.mask_host[0].numpy()[:] = mask
+                    e.mask.copy_(e.mask_host, non_blocking=True)
+                e.graph.replay()
+                e.out_host.copy_(e.out.float(), non_blocking=True)
+                stream.synchronize()
+                return e.out_host.numpy().copy()
