@@ -394,6 +394,8 @@ def attention_prepare(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm:
     shapes = ((batch, H, S, hd), (batch, KV, hd, S), (batch, KV, S, hd))
     if out is None:
         out = tuple(torch.empty(sh, dtype=q.dtype, device=q.device) for sh in shapes)
+    if len(out) != 3:
+        raise ValueError("out must be three tensors (q, K transposed, v)")
     for o, sh in zip(out, shapes):
         _device(q, o)
         if o.dtype != q.dtype or tuple(o.shape) != sh or not o.is_contiguous():

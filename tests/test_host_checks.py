@@ -49,6 +49,24 @@ def _calls():
     the library (the stub), every invalid one must raise ValueError first."""
     tables = (d(8, 4), d(8, 4))
     return [
+        ("native_gather_rms",
+         lambda **kw: ops.native_gather_rms(d(10, 16, dtype=BF16), d(4, dtype=torch.int32),
+                                            d(16, dtype=BF16), 1e-6, **kw),
+         [dict(hidden=d(4, 16, dtype=BF16)), dict(hidden=host(4, 16)),
+          dict(normed=d(4, 16)), dict(normed=host(4, 16, dtype=BF16)),
+          dict(error_flag=d(1)), dict(error_flag=host(1, dtype=torch.int32)),
+          dict(token_mask=d(4, dtype=torch.int64))]),
+        ("attention_prepare",
+         lambda **kw: ops.attention_prepare(d(8, 2, 16), d(8, 1, 16), d(8, 1, 16), d(16), d(16),
+                                            tables, 8, 1e-6, 2, **kw),
+         [dict(out=(d(2, 2, 4, 16), d(2, 1, 16, 4), d(2, 1, 4, 16, dtype=BF16))),
+          dict(out=(d(2, 2, 4, 16), host(2, 1, 16, 4), d(2, 1, 4, 16))),
+          dict(out=(d(2, 2, 4, 16), d(2, 1, 4, 16), d(2, 1, 4, 16))),
+          dict(out=(d(2, 2, 4, 16), d(2, 1, 16, 4)))]),
+        ("device_copy_rows",
+         lambda **kw: ops.device_copy_rows(kw.get("dst", d(4, 16, dtype=BF16)),
+                                           d(10, 16, dtype=BF16), d(4, dtype=torch.int32)),
+         [dict(dst=host(4, 16, dtype=BF16)), dict(dst=d(4, 8, dtype=BF16))]),
         ("native_gather",
          lambda **kw: ops.native_gather(d(10, 16, dtype=BF16), d(4, dtype=torch.int32), **kw),
          [dict(out=d(4, 16, dtype=F32)),                      # bf16 table -> bf16 out expected
