@@ -129,6 +129,26 @@ def test_graph_replays_full_size_model(dtype):
     torch.cuda.empty_cache()
 
 
+def test_graph_all_masked_and_single_token():
+    """Edge masks and lengths through the graph path (eager GEMM library: bit for
+    bit): a sequence with every token masked (no visible key in any attention
+    row), one with only its last token kept, and a single token."""
+    from qdc_amd import backbone
+    from qdc_amd.graphs import LastHiddenGraphs
+    cfg, weights, model = _synthetic_model(torch.float32, seed=13)
+    graphs = LastHiddenGraphs(model, gemm_libraries=None)
+    rng = np.random.default_rng(14)
+    for n, mask in ((40, np.zeros(40, np.int64)), (40, np.r_[np.zeros(39, np.int64), 1]),
+                    (1, np.ones(1, np.int64))):
+        ids = rng.integers(0, cfg.vocab, size=n)
+        got = graphs(ids, mask)
+        exp = backbone.backbone_last_hidden(model, ids, mask)
+        assert np.array_equal(_bits(got), _bits(exp)), (n, mask.sum())
+        ref = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask)[-1]
+        assert normwise(got, ref) <= 1e-5, (n, normwise(got, ref))
+    assert set(graphs._entries) == {(40, True), (1, False)}
+
+
 def test_graph_input_checks():
     from qdc_amd import backbone
     from qdc_amd.config import synthetic_inference_config

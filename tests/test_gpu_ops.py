@@ -1008,6 +1008,8 @@ PREP_CASES = [
     (1, 37, 4, 2, 64, 16, True, 0),        # seq not a multiple of a chunk: general path
     (2, 16, 2, 1, 24, 8, False, 3),        # head_dim not a multiple of a chunk: general path
     (3, 72, 8, 2, 128, 32, True, 5),       # fast path with an offset: partial K and V tiles
+    (5, 8, 4, 2, 64, 16, True, 0),         # shortest bf16 fast path: one 8-token K and V tile
+    (1, 4, 2, 1, 64, 16, False, 2),        # 4 tokens: fp32 fast path (bf16: general path)
 ]
 
 
