@@ -132,6 +132,10 @@ class QwenBackbone:
                                 "layer_types": cfg.layer_types})
         return cls(cfg, weights, device, dtype)
 
+    def _mm(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        """A projection whose result feeds a row kernel, in the model dtype."""
+        return a @ b
+
     def _mm32(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         """A GEMM whose result feeds the fp32 residual stream: fp32 output even
         from bf16 operands (hipBLASLt accumulates in fp32 either way)."""
@@ -185,7 +189,7 @@ class QwenBackbone:
                 h = h.view(B, S, -1)[:, -1].contiguous()
                 mixed = mixed.view(B, S, -1)[:, -1].contiguous()
             residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps)
-            gate_up = normed @ layer["gate_up"]
+            gate_up = self._mm(normed, layer["gate_up"])
             inter = gate_up.shape[1] // 2
             act = ops.native_mlp_gate(gate_up[:, :inter], gate_up[:, inter:])
             down = self._mm32(act, layer["down"])
@@ -208,7 +212,7 @@ class QwenBackbone:
         hd, H, KV = cfg.head_dim, cfg.heads, cfg.kv_heads
         G = H // KV
         T = B * S
-        proj = x @ layer["qkv"]                              # [T, q | k | v | gate]
+        proj = self._mm(x, layer["qkv"])                     # [T, q | k | v | gate]
         q_in = proj[:, :H * hd].view(T, H, hd)
         k_in = proj[:, H * hd:(H + KV) * hd].view(T, KV, hd)
         v_in = proj[:, (H + KV) * hd:(H + 2 * KV) * hd].view(T, KV, hd)
@@ -241,7 +245,7 @@ class QwenBackbone:
         T = B * S
         kw, vw = kd * kh, vd * vh
         cq = 2 * kw + vw
-        proj = x @ layer["proj"]           # [T, cq + vw + 2*vh (+ zero padding)]
+        proj = self._mm(x, layer["proj"])  # [T, cq + vw + 2*vh (+ zero padding)]
         # conv + SiLU, q/k L2 norm and the beta/decay gates in one pass
         q, k, v, beta, decay = ops.delta_prologue(proj, layer["conv"], layer["a_decay"],
                                                   layer["dt_bias"], S, kh, kd, vh, vd)
