@@ -188,7 +188,7 @@ __device__ __forceinline__ float sigmoid_ref(float x) {
     return 1.0f / (1.0f + expf(-x));
 }
 
-// One thread per 8 consecutive elements of one (token, head) row.
+// One thread per 8 elements of one (token, head) row: 4 in each half of the row.
 template <typename TG, typename TO>
 __global__ __launch_bounds__(kBlock) void gate_merge_fast(Gate a) {
     const int64_t g = (int64_t)blockIdx.x * kBlock + threadIdx.x;
@@ -199,19 +199,27 @@ __global__ __launch_bounds__(kBlock) void gate_merge_fast(Gate a) {
     const uint32_t h = th - t * a.heads.d;
     const uint32_t b = fastdiv(t, a.seq);
     const uint32_t s = t - b * a.seq.d;
-    const int64_t dim = (int64_t)a.chunks.d * 8;
-    const float *vp = a.values + (((int64_t)b * a.heads.d + h) * a.seq.d + s) * dim + c * 8;
+    const int64_t dim = (int64_t)a.chunks.d * 8, half = dim / 2;
+    // elements [4c, 4c+4) and [dim/2 + 4c, dim/2 + 4c + 4): every load and store
+    // instruction of a wavefront then covers contiguous spans
+    const float *vp = a.values + (((int64_t)b * a.heads.d + h) * a.seq.d + s) * dim + c * 4;
     const TG *gp = reinterpret_cast<const TG *>(a.gate) + (int64_t)t * a.gate_tok +
-                   (int64_t)h * a.gate_head + c * 8;
-    const Frag<float, 8> vf = stream_frag<float, 8>(vp);
-    const Frag<TG, 8> gf = stream_frag<TG, 8>(gp);
-    float v[8], gv[8];
-    unpack(vf, v);
-    unpack(gf, gv);
+                   (int64_t)h * a.gate_head + c * 4;
+    const Frag<float, 4> vf0 = stream_frag<float, 4>(vp), vf1 = stream_frag<float, 4>(vp + half);
+    const Frag<TG, 4> gf0 = stream_frag<TG, 4>(gp), gf1 = stream_frag<TG, 4>(gp + half);
+    TO *op = reinterpret_cast<TO *>(a.out) + (int64_t)t * a.out_tok + (int64_t)h * dim + c * 4;
+    float v0[4], v1[4], g0[4], g1[4];
+    unpack(vf0, v0);
+    unpack(vf1, v1);
+    unpack(gf0, g0);
+    unpack(gf1, g1);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = v[j] * sigmoid_ref(gv[j]);
-    TO *op = reinterpret_cast<TO *>(a.out) + (int64_t)t * a.out_tok + (int64_t)h * dim + c * 8;
-    store_frag<8>(op, v);
+    for (int j = 0; j < 4; ++j) {
+        v0[j] = v0[j] * sigmoid_ref(g0[j]);
+        v1[j] = v1[j] * sigmoid_ref(g1[j]);
+    }
+    store_frag<4>(op, v0);
+    store_frag<4>(op + half, v1);
 }
 
 template <typename TG, typename TO>
