@@ -28,7 +28,8 @@
 namespace qdc {
 namespace {
 
-constexpr int kMaxRowChunks = 8;  // fast path: up to 8 chunks of 4 keys per lane (2048 keys)
+constexpr int kMaxRowChunks = 8;  // chunks of 4 keys per lane of one wavefront (2048 keys)
+constexpr int kMaxRowWaves = 16;  // wavefronts per row in one workgroup (32768 keys)
 
 template <int CTRL> __device__ __forceinline__ float dpp_max_step(float v) {
     return fmaxf(v, dpp<CTRL>(v));
@@ -134,6 +135,93 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_fast(Softmax a) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int64_t k0 = ((int64_t)c * kWave + lane) * 4;
+        if (k0 >= a.keys) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = none ? uniform : (k0 + e < visible ? v[c][e] * inv_total : 0.0f);
+        store4<TO>(dst + k0, o);
+    }
+}
+
+// Rows longer than one wavefront's registers (more than 2048 keys): WPR
+// wavefronts per row, the row's 16-byte chunks dealt round-robin over them (so
+// the causally visible keys spread evenly), each wavefront reducing its share
+// with DPP and lane swaps and the WPR partial maxima and sums meeting in LDS.
+// Every score is read once and every probability written once, as in
+// softmax_rows_fast; workgroups of max(4, WPR) wavefronts.  Wavefronts of rows
+// past the end skip their loads and stores but reach both barriers.
+template <typename TO, int CPL, int WPR>
+__global__ __launch_bounds__(WPR > 4 ? WPR * kWave : kBlock) void softmax_rows_waves(Softmax a) {
+    constexpr int NW = WPR > 4 ? WPR : kBlock / kWave;  // wavefronts per workgroup
+    constexpr int RPB = NW / WPR;                       // rows per workgroup
+    __shared__ float part_max[NW], part_sum[NW];
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int part = wave % WPR, first = wave - part;   // this row's wavefronts: [first, first+WPR)
+    const int64_t row = (int64_t)blockIdx.x * RPB + wave / WPR;
+    const bool valid = row < a.rows;
+    const int64_t r = valid ? row : 0;
+    const uint32_t qi = (uint32_t)r - fastdiv((uint32_t)r, a.queries) * a.queries.d;
+    const uint32_t b = fastdiv((uint32_t)r, a.per_batch);
+    const int64_t visible = valid ? min(a.keys, a.q_offset + (int64_t)qi + 1) : 0;
+    const float *src = a.scores + r * a.keys;
+    const int32_t *mrow = a.mask ? a.mask + (int64_t)b * a.keys : nullptr;
+
+    float v[CPL][4];
+    u32x4 raw[CPL];
+    int4 mk[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int64_t k0 = ((int64_t)(c * WPR + part) * kWave + lane) * 4;
+        raw[c] = u32x4{0u, 0u, 0u, 0u};
+        mk[c] = int4{1, 1, 1, 1};
+        if (k0 < visible) {
+            raw[c] = load_stream(src + k0);
+            if (mrow) mk[c] = *reinterpret_cast<const int4 *>(mrow + k0);
+        }
+    }
+    float peak = -FLT_MAX;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int64_t k0 = ((int64_t)(c * WPR + part) * kWave + lane) * 4;
+        const int mm[4] = {mk[c].x, mk[c].y, mk[c].z, mk[c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool on = k0 + e < visible && mm[e] != 0;
+            v[c][e] = on ? __uint_as_float(raw[c][e]) * a.scale : -FLT_MAX;
+            peak = fmaxf(peak, v[c][e]);
+        }
+    }
+    peak = wave_max(peak);
+    if (lane == 0) part_max[wave] = peak;
+    __syncthreads();
+    peak = part_max[first];
+#pragma unroll
+    for (int j = 1; j < WPR; ++j) peak = fmaxf(peak, part_max[first + j]);
+    const bool none = peak == -FLT_MAX;  // no visible unmasked key: every key gets 1/keys
+    float total = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int64_t k0 = ((int64_t)(c * WPR + part) * kWave + lane) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[c][e] = k0 < visible ? exp_shifted(v[c][e], peak) : 0.0f;
+            total += v[c][e];
+        }
+    }
+    total = group_sum<kWave>(total);
+    if (lane == 0) part_sum[wave] = total;
+    __syncthreads();
+    total = part_sum[first];
+#pragma unroll
+    for (int j = 1; j < WPR; ++j) total += part_sum[first + j];
+    if (!valid) return;
+    const float inv_total = 1.0f / total;
+    TO *dst = reinterpret_cast<TO *>(a.probs) + r * a.keys;
+    const float uniform = 1.0f / (float)a.keys;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int64_t k0 = ((int64_t)(c * WPR + part) * kWave + lane) * 4;
         if (k0 >= a.keys) continue;
         float o[4];
 #pragma unroll
@@ -275,24 +363,41 @@ extern "C" int32_t qdc_attention_softmax(void *probs, int32_t probs_dtype, const
     a.scale = scale;
     const dim3 grid((uint32_t)ceil_div(rows, kBlock / kWave));
     const int64_t chunks = ceil_div(keys, 4 * kWave);  // chunks of 4 keys per lane
+    // wavefronts per row beyond one: each keeps at most kMaxRowChunks chunks per lane;
+    // the grid's work-items (rows * wpr * 64) stay below 2^32
+    int64_t wpr = 1;
+    while (wpr < kMaxRowWaves && chunks > wpr * kMaxRowChunks) wpr *= 2;
     const bool fast = keys % 4 == 0 && aligned16(scores) && aligned16(probs) &&
-                      (!mask || aligned16(mask)) && chunks <= kMaxRowChunks;
+                      (!mask || aligned16(mask)) && chunks <= wpr * kMaxRowChunks &&
+                      rows * wpr < ((int64_t)1 << 26);
 #define QDC_SM(TO, CPL)                                                                      \
     hipLaunchKernelGGL((softmax_rows_fast<TO, CPL>), grid, dim3(kBlock), 0, stream, a);     \
     return launch_status();
+#define QDC_SMW(TO, W)                                                                       \
+    if (wpr == W) {                                                                          \
+        constexpr int64_t nw = W > 4 ? W : kBlock / kWave;                                   \
+        hipLaunchKernelGGL((softmax_rows_waves<TO, kMaxRowChunks, W>),                      \
+                           dim3((uint32_t)ceil_div(rows, nw / W)), dim3(nw * kWave), 0,      \
+                           stream, a);                                                       \
+        return launch_status();                                                              \
+    }
 #define QDC_SM_ALL(TO)                                                                       \
     if (fast) {                                                                              \
         if (chunks <= 1) { QDC_SM(TO, 1) }                                                   \
         if (chunks <= 2) { QDC_SM(TO, 2) }                                                   \
         if (chunks <= 4) { QDC_SM(TO, 4) }                                                   \
         if (chunks <= 8) { QDC_SM(TO, 8) }                                                   \
-        QDC_SM(TO, 16)                                                                       \
+        QDC_SMW(TO, 2)                                                                       \
+        QDC_SMW(TO, 4)                                                                       \
+        QDC_SMW(TO, 8)                                                                       \
+        QDC_SMW(TO, 16)                                                                      \
     }                                                                                        \
     hipLaunchKernelGGL((softmax_rows_general<TO>), grid, dim3(kBlock), 0, stream, a);       \
     return launch_status();
     if (probs_dtype == QDC_BF16) { QDC_SM_ALL(bf16_t) }
     QDC_SM_ALL(float)
 #undef QDC_SM_ALL
+#undef QDC_SMW
 #undef QDC_SM
 }
 

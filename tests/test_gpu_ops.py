@@ -853,7 +853,13 @@ SOFTMAX_CASES = [
     (1, 3, 37, 37, 0, "rand"),
     (2, 2, 5, 8, 0, "dead"),
     (1, 2, 16, 100, 84, "rand"),     # a chunk of queries at the end of a 100-key context
-    (1, 1, 7, 2560, 2553, "none"),   # more keys than the register path holds: general kernel
+    (1, 1, 7, 2560, 2553, "none"),   # more keys than one wavefront holds: 2 per row
+    (1, 2, 40, 4096, 4056, "rand"),  # 2 wavefronts per row
+    (2, 1, 20, 8192, 0, "dead"),     # 4 per row, rows with no visible key
+    (1, 1, 12, 20000, 19988, "rand"),  # 16 per row (1024-thread workgroups), a partial chunk span
+    (1, 1, 6, 32768, 32762, "none"),   # the longest rows of the register path
+    (1, 1, 3, 33000, 32997, "none"),   # longer rows: general kernel
+    (1, 1, 5, 2561, 2556, "none"),   # long rows with keys % 4 != 0: general kernel
     (1, 2, 9, 13, 4, "rand"),        # keys % 4 != 0: general kernel
 ]
 
@@ -891,16 +897,16 @@ def test_attention_softmax(out_dtype, case):
         assert np.all(got[hidden & ~np.broadcast_to(dead, got.shape)] == 0)
 
 
-def test_attention_softmax_in_place():
+@pytest.mark.parametrize("case", [(2, 4, 64, 64, 0, "rand"), (1, 2, 8, 4096, 4088, "rand")])
+def test_attention_softmax_in_place(case):
     from oracle import forward
     from qdc_amd import ops
-    case = (2, 4, 64, 64, 0, "rand")
     scores, mask = _softmax_inputs(case)
     d = dev(scores, torch.float32)
-    out = ops.attention_softmax(d, dev(mask, torch.int32), 0.0625, out=d)
+    out = ops.attention_softmax(d, dev(mask, torch.int32), 0.0625, case[4], out=d)
     assert out.data_ptr() == d.data_ptr()
-    report("softmax in place", back(d), forward.attention_softmax(scores, mask, 0.0625),
-           torch.float32)
+    report(f"softmax in place {case}", back(d),
+           forward.attention_softmax(scores, mask, 0.0625, case[4]), torch.float32)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
