@@ -19,7 +19,8 @@
 // dependent instruction; streamed inputs use nontemporal loads.  The row
 // stays in registers: HBM sees each input byte read once and each output byte
 // written once.  The sum of squares is reduced across the LPR lanes (DPP inside
-// 16-lane rows, lane swaps across them); 64/LPR rows share a wavefront, 4
+// 16-lane rows, lane swaps across them, and through LDS across the 2 or 4
+// wavefronts of a row wider than 64 lanes); 64/LPR rows share a wavefront, 4
 // wavefronts a workgroup.
 //
 // General path (any width, stride or alignment): one wavefront per row, scalar
@@ -112,7 +113,19 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
             for (int j = 0; j < V; ++j) ss += v[c][j] * v[c][j];
         }
     }
-    ss = group_sum<LPR>(ss);
+    if constexpr (LPR <= kWave) {
+        ss = group_sum<LPR>(ss);
+    } else {  // a row over LPR / 64 wavefronts: their partial sums meet in LDS
+        constexpr int WPR = LPR / kWave;
+        __shared__ float part[kBlock / kWave];
+        const int wave = threadIdx.x / kWave, first = wave - wave % WPR;
+        ss = group_sum<kWave>(ss);
+        if (threadIdx.x % kWave == 0) part[wave] = ss;
+        __syncthreads();  // reached by every thread: inactive rows return below
+        ss = part[first];
+#pragma unroll
+        for (int j = 1; j < WPR; ++j) ss += part[first + j];
+    }
     if (!active) return;
     const float s = rms_scale(ss, width, eps);
 
@@ -206,9 +219,14 @@ int32_t launch_fast(const Args &a, hipStream_t stream) {
 // Fast-path shapes by G = groups per row: a lane holds 2 groups for rows of up
 // to 64 groups and 4 groups for 128- and 256-group rows (8 for plain all-bf16
 // 128-group rows; the splits that measured fastest on MI355X, 32 x 8 and
-// 16 x 16 were not faster for the 256-group fp32-to-bf16 rows); wider rows use
-// all 64 lanes with G/64 groups each.  kNoFastPath when no instantiation
-// matches.
+// 16 x 16 were not faster for the 256-group fp32-to-bf16 rows); rows of 192,
+// 320, 384 and 448 groups take 64 lanes with 3-7 groups each; wider rows 2
+// wavefronts (512-1536 groups: fp32 rows of
+// 2048-6144 elements, 4-12 groups per lane) or 4 (2048-4096 groups, 8-16 per
+// lane).  Measured on MI355X against one 64-lane wavefront per row with G/64
+// groups per lane: 2-7% faster at 512-768 groups and 13-15% at 1024 (16 groups
+// per lane took 256 VGPRs); 12-32 groups per lane in one wavefront took
+// 200-256 VGPRs, with spills.  kNoFastPath when no instantiation matches.
 template <typename TX, typename TM, typename TO, Mode M, bool C>
 int32_t dispatch_fast(const Args &a, hipStream_t stream) {
     constexpr int V = group_elems<TX, TM, TO>();
@@ -237,10 +255,16 @@ int32_t dispatch_fast(const Args &a, hipStream_t stream) {
         QDC_FAST(64, 5)
         QDC_FAST(64, 6)
         QDC_FAST(64, 7)
-        QDC_FAST(64, 8)
-        QDC_FAST(64, 10)
-        QDC_FAST(64, 12)
-        QDC_FAST(64, 16)
+        QDC_FAST(128, 4)
+        QDC_FAST(128, 5)
+        QDC_FAST(128, 6)
+        QDC_FAST(128, 8)
+        QDC_FAST(128, 10)
+        QDC_FAST(128, 12)
+        QDC_FAST(256, 8)
+        QDC_FAST(256, 10)
+        QDC_FAST(256, 12)
+        QDC_FAST(256, 16)
         default:
             return kNoFastPath;
     }

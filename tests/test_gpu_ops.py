@@ -57,7 +57,10 @@ DTYPES = [torch.float32, torch.bfloat16]
 # ------------------------------------------------------------------ RMSNorm --
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,width", [(8192, 1024), (81920, 256), (17, 7), (1, 1), (3, 1000),
-                                        (33, 2560), (5, 4096), (257, 128), (2, 8), (9, 64)])
+                                        (33, 2560), (5, 4096), (257, 128), (2, 8), (9, 64),
+                                        # rows over 2 or 4 wavefronts (fp32 from 2048;
+                                        # bf16 from 4096)
+                                        (6, 2048), (9, 5120), (4, 8192), (3, 10240), (2, 16384)])
 @pytest.mark.parametrize("centered", [True, False])
 def test_rmsnorm(dtype, rows, width, centered):
     from qdc_amd import ops
@@ -86,7 +89,8 @@ def test_rmsnorm_strided_misaligned_inplace_empty(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,width", [(8192, 1024), (16384, 1024), (17, 7), (65, 256), (3, 3000)])
+@pytest.mark.parametrize("rows,width", [(8192, 1024), (16384, 1024), (17, 7), (65, 256), (3, 3000),
+                                        (5, 5120)])
 def test_residual_rmsnorm(dtype, rows, width):
     from qdc_amd import ops
     x = host((rows, width), 5, 1.0, dtype)
@@ -336,7 +340,8 @@ def test_device_copy_rows():
 
 
 # ------------------------------------------- fp32 residual stream mixes ------
-@pytest.mark.parametrize("rows,width", [(16384, 1024), (33, 256), (5, 1000)])
+@pytest.mark.parametrize("rows,width", [(16384, 1024), (33, 256), (5, 1000), (7, 5120),
+                                        (3, 12288)])
 def test_rmsnorm_fp32_to_bf16(rows, width):
     """fp32 rows normalised into a bf16 output with a bf16 weight."""
     from qdc_amd import ops
@@ -350,7 +355,8 @@ def test_rmsnorm_fp32_to_bf16(rows, width):
 @pytest.mark.parametrize("mixed_dtype,out_dtype", [(torch.bfloat16, torch.bfloat16),
                                                     (torch.bfloat16, torch.float32),
                                                     (torch.float32, torch.bfloat16)])
-@pytest.mark.parametrize("rows,width", [(16384, 1024), (65, 256), (3, 3000)])
+@pytest.mark.parametrize("rows,width", [(16384, 1024), (65, 256), (3, 3000), (9, 6144),
+                                        (4, 8192)])
 def test_residual_rmsnorm_fp32_stream(mixed_dtype, out_dtype, rows, width):
     """fp32 residual stream + bf16 or fp32 addend -> fp32 residual, normalised
     output in the weight's dtype (bf16 for the next GEMM, fp32 for the final norm)."""
@@ -395,7 +401,7 @@ def _exact_rows(width):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("width", [1024, 1000, 7])
+@pytest.mark.parametrize("width", [1024, 1000, 7, 4096, 5120])
 def test_norm_special_rows_bit_exact(dtype, width):
     """Zero, overflowing, inf, NaN, denormal and exactly-summable rows through
     the plain, residual and gated norms: bit for bit (NaN-aware) equal to the
@@ -449,7 +455,7 @@ def test_qk_norm_rope_special_rows_bit_exact(dtype, hd, rd):
 @pytest.mark.parametrize("x_dtype,out_dtype", [(torch.float32, torch.float32),
                                                 (torch.bfloat16, torch.bfloat16),
                                                 (torch.float32, torch.bfloat16)])
-@pytest.mark.parametrize("rows,width", [(16384, 1024), (65, 256), (33, 1000), (3, 7)])
+@pytest.mark.parametrize("rows,width", [(16384, 1024), (65, 256), (33, 1000), (3, 7), (9, 5120)])
 def test_masked_norms(x_dtype, out_dtype, rows, width):
     """The DeltaNet input mask (src/backbone.jl:286) fused into the norms that
     produce that input.  Each masked row is the unmasked kernel's row times its
