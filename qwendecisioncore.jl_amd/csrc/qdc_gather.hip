@@ -363,8 +363,10 @@ int32_t launch_gather_rms(float *hidden, TN *normed, const TT *table, const int3
             QDC_GR(32, 2)
             QDC_GR(64, 2)
             QDC_GR(64, 4)
+            QDC_GR(64, 5)
             QDC_GR(64, 6)
             QDC_GR(64, 8)
+            QDC_GR(64, 10)
             QDC_GR(64, 12)
             QDC_GR(64, 16)
             default:

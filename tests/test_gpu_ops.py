@@ -1092,7 +1092,8 @@ def test_attention_prepare_checks():
                                                     (torch.float32, torch.bfloat16)])
 @pytest.mark.parametrize("vocab,width,n", [(248320, 1024, 16384), (4096, 256, 129), (64, 8, 65),
                                            (100, 12, 33), (50, 1000, 7), (30, 4096, 5),
-                                           (60, 512, 70), (40, 2048, 9)])
+                                           (60, 512, 70), (40, 2048, 9), (45, 2560, 11),
+                                           (35, 1280, 6)])
 def test_gather_rms(table_dtype, norm_dtype, vocab, width, n):
     """hidden = the gathered rows widened to fp32 bit for bit; normed = their
     zero-centred RMSNorm (oracle, fp32 1e-5 / bf16 1e-2), masked rows times
