@@ -339,6 +339,35 @@ def test_device_copy_rows():
                              torch.zeros(3, dtype=torch.int32, device=DEV), repeat=2)
 
 
+# Every fast-path row shape of the RMSNorm family (groups per row G = lanes x
+# groups per lane; 4 elements per group when any tensor is fp32, 8 when all are
+# bf16), once per type mix, against the oracle: a wrong dispatch entry or a
+# broken multi-wavefront reduction shows at its own width.
+RMS_FAST_GROUPS = [1, 2, 4, 8, 16, 32, 64, 128, 192, 256, 320, 384, 448, 512, 640, 768, 1024,
+                   1280, 1536, 2048, 2560, 3072, 4096]
+
+
+@pytest.mark.parametrize("groups", RMS_FAST_GROUPS)
+@pytest.mark.parametrize("mix", ["f32", "bf16", "f32->bf16", "residual f32+bf16->bf16"])
+def test_rmsnorm_every_fast_shape(groups, mix):
+    from qdc_amd import ops
+    bf, f32 = torch.bfloat16, torch.float32
+    width = groups * (8 if mix == "bf16" else 4)
+    rows = 5
+    x = host((rows, width), 71, 1.0, bf if mix == "bf16" else f32)
+    out_dtype = f32 if mix == "f32" else bf
+    w = host((width,), 72, 0.02, out_dtype)
+    if mix.startswith("residual"):
+        m = host((rows, width), 73, 1.0, bf)
+        res, got = ops.native_residual_rms(dev(x, f32), dev(m, bf), dev(w, bf), 1e-6)
+        exp_res, exp = O.residual_rms(x, m, w, 1e-6)
+        assert np.array_equal(back(res), exp_res)
+    else:
+        got = ops.native_rms(dev(x, bf if mix == "bf16" else f32), dev(w, out_dtype), 1e-6)
+        exp = O.rms(x, w, 1e-6)
+    report(f"rms {mix} G={groups} width={width}", back(got), exp, out_dtype)
+
+
 # ------------------------------------------- fp32 residual stream mixes ------
 @pytest.mark.parametrize("rows,width", [(16384, 1024), (33, 256), (5, 1000), (7, 5120),
                                         (3, 12288)])
