@@ -606,27 +606,33 @@ def e2e_benchmark(dev, steps=3, warmup=1):
     from qdc_amd.weights import random_device_weights
     cfg = qwen35_08b_config()
     weights = random_device_weights(cfg, seed=0, device=dev, dtype=torch.bfloat16)
-    model = backbone.QwenBackbone.from_weights(weights, cfg, dev, torch.bfloat16)
-    del weights
-    torch.cuda.empty_cache()
     g = torch.Generator(device=dev)
     g.manual_seed(2)
     ids = torch.randint(0, cfg.vocab, (E2E_BATCH, E2E_SEQ), generator=g, device=dev,
                         dtype=torch.int32)
     mask = None  # no padding: every token is kept (the forward then does no masking work)
-    for _ in range(warmup):
-        out = model.forward(ids, mask)
-    torch.cuda.synchronize()
-    if not torch.isfinite(out).all():
-        raise RuntimeError("non-finite backbone output")
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        model.forward(ids, mask)
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    del model
+
+    def forward_ms(split):
+        model = backbone.QwenBackbone.from_weights(weights, cfg, dev, torch.bfloat16,
+                                                   split_gemm_inputs=split)
+        for _ in range(warmup):
+            out = model.forward(ids, mask)
+        torch.cuda.synchronize()
+        if not torch.isfinite(out).all():
+            raise RuntimeError("non-finite backbone output")
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            model.forward(ids, mask)
+        end.record()
+        torch.cuda.synchronize()
+        del model, out
+        torch.cuda.empty_cache()
+        return start.elapsed_time(end) / steps
+
+    ms = forward_ms(False)
+    split_ms = {mode: forward_ms(mode) for mode in ("all", "mlp")}
+    del weights
     torch.cuda.empty_cache()
     # this library's kernels of one forward, replayed from graphs on buffers of
     # the forward's shapes: the fused row kernels, then the widened kernels
@@ -642,6 +648,15 @@ def e2e_benchmark(dev, steps=3, warmup=1):
             "fused_kernel_time_share": round(fused_ms / ms, 4),
             "widened_kernels_ms": round(widened_ms, 3),
             "widened_kernel_time_share": round(widened_ms / ms, 4),
+            "split_gemm_inputs": {
+                "note": "the same weights and tokens with GEMM inputs written by their "
+                        "producing kernels as two bf16 terms (hi + lo, the GEMMs' inner "
+                        "dimension doubled) and fp32 MLP gate/up -- every GEMM input ('all') "
+                        "or the MLP's two ('mlp'): the bf16-weight modes that meet the 1e-2 "
+                        "end-to-end bar against the fp32 oracle at 24 layers",
+                **{mode: {"ms_per_forward": round(v, 3),
+                          "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (v / 1e3), 1)}
+                   for mode, v in split_ms.items()}},
             "steps": steps, "warmup": warmup}
 
 

@@ -10,6 +10,19 @@
  *    call's tensors; the RMSNorm entry points take one per tensor role so an
  *    fp32 residual stream can feed bf16 activations.  Arithmetic is fp32; bf16
  *    results are rounded to nearest even.  RoPE tables are always fp32.
+ *  - QDC_BF16X2 is an output type only (the split form of a GEMM input): each
+ *    fp32 result v is written as two bf16 terms, hi = bf16(v) and
+ *    lo = bf16(v - hi) (lo = 0 when hi is not finite), so hi + lo keeps about
+ *    16 significant bits.  Element e of such an output takes the bf16 slots
+ *    8*(e/4) + e%4 (hi) and 8*(e/4) + 4 + e%4 (lo): every aligned group of 4
+ *    elements is one 16-byte piece [4 hi | 4 lo], 4 bytes per element, and
+ *    strides stay in elements.  A row of K such elements is a bf16 row of 2K
+ *    values; multiplied by a bf16 weight whose K rows are repeated in the same
+ *    pattern (rows 8g+j and 8g+4+j both hold row 4g+j) it gives
+ *    sum((hi + lo) * w).  Rows must hold whole groups: widths and output row
+ *    strides a multiple of 4 (QDC_ERR_SHAPE otherwise).  Tensors read beside a
+ *    split output in its dtype role (norm weights, the gated norm's z) are
+ *    bf16.  Supported where each entry point says so.
  *  - The library never allocates or frees memory, keeps no pointer after
  *    return, has no mutable global state and never synchronises: work is
  *    enqueued on `stream` (0 = the null stream of the current device) and the
@@ -37,7 +50,8 @@ extern "C" {
 
 typedef enum {
     QDC_F32 = 0,
-    QDC_BF16 = 1
+    QDC_BF16 = 1,
+    QDC_BF16X2 = 2  /* output only: two bf16 terms per fp32 value */
 } qdc_dtype;
 
 typedef enum {
@@ -73,8 +87,9 @@ int32_t qdc_embedding_gather(void *out, int32_t out_dtype, const void *table, in
  * over the table rows: hidden[t, :] = table[ids[t], :] (fp32, the residual
  * stream; bf16 table entries widened exactly by <<16) and normed[t, :] =
  * zero-centred RMSNorm(hidden[t, :]) with `weight` (normed_dtype, as the
- * weight), times token_mask[t] when token_mask is not NULL (the DeltaNet input
- * mask when the first layer is a DeltaNet layer, as qdc_rmsnorm_masked).
+ * weight; QDC_BF16X2 with a bf16 weight), times token_mask[t] when
+ * token_mask is not NULL (the DeltaNet input mask when the first layer is a
+ * DeltaNet layer, as qdc_rmsnorm_masked).
  * Replaces native_gather (ext/amdgpu_workspace.jl:206-236) followed by the
  * first layer's native_rms (src/backbone.jl:364; ext/amdgpu_workspace.jl:
  * 113-149), which reads the gathered rows back.  Ids as qdc_embedding_gather
@@ -103,8 +118,9 @@ int32_t qdc_check_ids(const int64_t *ids, int64_t n_ids, int64_t vocab);
  * (rows = tokens*heads, width = head_dim) and, with centered = 0, the plain
  * DeltaNet output norm.  Row r reads x + r*ld_x and writes out + r*ld_out.
  * x_dtype is the type of x; out_dtype that of out and weight.  Supported:
- * f32->f32, bf16->bf16 and f32->bf16 (an fp32 residual stream feeding bf16
- * GEMMs).  out may equal x when the type and stride agree.
+ * f32->f32, bf16->bf16, f32->bf16 (an fp32 residual stream feeding bf16
+ * GEMMs) and f32->bf16x2 (bf16 weight).  out may equal x when the type and
+ * stride agree (not for a split output).
  */
 int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows, int64_t width,
                     int64_t ld_x, int64_t ld_out, float eps, int32_t centered, int32_t x_dtype,
@@ -118,7 +134,8 @@ int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows, 
  * weight, the residual add of native_layer (src/backbone.jl:358-366) fused
  * with that next norm.  residual_dtype types x and residual, mixed_dtype
  * mixed, out_dtype out and weight.  Supported: all bf16, or an f32 residual
- * stream with an f32 or bf16 addend and an f32 or bf16 output.  The sum is formed and
+ * stream with an f32 or bf16 addend and an f32 or bf16 output, or with an f32
+ * addend and a bf16x2 output (bf16 weight).  The sum is formed and
  * normalised in fp32.  residual may equal x (or mixed of the same type); out
  * may equal x or mixed of the same type; out and residual must differ.
  */
@@ -253,12 +270,14 @@ int32_t qdc_rope_tables(float *cos_table, float *sin_table, int64_t n_pos, int64
  * cpu_delta_gate_output! ext/QwenDecisionCoreLoopVectorizationExt.jl:373-390).
  * Row (t, h) reads x + t*x_tok + h*width and z + t*z_tok + h*width (z may sit
  * inside the packed projection) and writes out + t*out_tok + h*width.
- * out may equal x.
+ * dtype types x, z and weight; out_dtype equals dtype, or is QDC_BF16X2 with
+ * dtype QDC_BF16 (the out-projection input in the split form).  out may equal
+ * x when their types and strides agree.
  */
 int32_t qdc_gated_rmsnorm(void *out, const void *x, const void *z, const void *weight,
                           int64_t tokens, int64_t heads, int64_t width, int64_t x_tok,
                           int64_t z_tok, int64_t out_tok, float eps, int32_t dtype,
-                          hipStream_t stream);
+                          int32_t out_dtype, hipStream_t stream);
 
 /*
  * SwiGLU: out[t, i] = silu(gate[t, i]) * up[t, i] for i < width.
@@ -266,12 +285,14 @@ int32_t qdc_gated_rmsnorm(void *out, const void *x, const void *z, const void *w
  * src/backbone.jl:352-355; CPU cpu_portable_gate!
  * ext/QwenDecisionCoreLoopVectorizationExt.jl:189-215).  For the packed
  * gate||up GEMM output pass gate = packed, up = packed + width,
- * ld_gate = ld_up = 2*width; out is the down-projection input.
- * out may equal gate or up when its stride equals theirs.
+ * ld_gate = ld_up = 2*width; out is the down-projection input.  dtype types
+ * gate and up; out_dtype equals dtype, or is QDC_BF16X2 with dtype QDC_F32
+ * (the down-projection input in the split form).  out may equal gate or up
+ * when its type and stride equal theirs.
  */
 int32_t qdc_swiglu(void *out, const void *gate, const void *up, int64_t tokens, int64_t width,
                    int64_t ld_gate, int64_t ld_up, int64_t ld_out, int32_t dtype,
-                   hipStream_t stream);
+                   int32_t out_dtype, hipStream_t stream);
 
 /*
  * Gated delta rule recurrence of the DeltaNet layers -- the "existing path"
@@ -328,7 +349,8 @@ int32_t qdc_attention_softmax(void *probs, int32_t probs_dtype, const float *sco
  * Output-gate merge: out[t, h*head_dim + r] = values[b, h, s, r] *
  * sigmoid(gate[t*gate_tok + h*gate_head + r]) for t = b*seq + s; values fp32
  * [batch, heads, seq, head_dim] contiguous (the PV GEMM output), gate and out
- * in gate_dtype / out_dtype with the given token and head strides (elements).
+ * in gate_dtype / out_dtype with the given token and head strides (elements);
+ * out_dtype may be QDC_BF16X2 (the out-projection input in the split form).
  * Replaces merge_gate_kernel! (ext/amdgpu_attention.jl:90-106, launch :168-176;
  * generic src/backbone.jl:258-259).
  */

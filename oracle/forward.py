@@ -9,13 +9,21 @@ the ``language_model.`` prefix removed (``layers.0.mlp.gate_proj.weight`` ...),
 laid out as stored (PyTorch ``[out, in]``), which is the reference's Julia
 ``(in, out)`` matrix in the same memory.
 
-``bf16=True`` runs the same algorithm with bf16 storage (RNE,
+``bf16=True`` (``storage="bf16"``) runs the same algorithm with bf16 storage (RNE,
 ``src/safetensors.jl:37-42``) of the activations a bf16 device pipeline keeps in
 bf16: the normalised GEMM inputs, the outputs of the input-side projections
 (q||gate, k, v, qkv, z, a, b, gate, up), the normed+rotated q/k, the attention
 probabilities, the merged attention output, the DeltaNet recurrence and gated-norm outputs and the SwiGLU
 output.  The residual stream and the outputs of the residual-side projections
 (o_proj, out_proj, down_proj) stay fp32.  Arithmetic stays fp32 throughout.
+
+``storage="bf16x2"`` is the split-GEMM-input pipeline: every GEMM input (the
+normalised rows, the merged attention output, the gated-norm output and the
+SwiGLU output) is stored as two bf16 terms (``qdc_oracle.round_split``), the MLP
+gate/up projections stay fp32, and the attention and DeltaNet projections, the
+normed+rotated q/k, the probabilities and the recurrence output are bf16.
+``storage="bf16x2_mlp"`` splits only the two MLP inputs (the post-attention
+norm and the SwiGLU output); the other GEMM inputs are bf16.
 """
 from __future__ import annotations
 
@@ -79,28 +87,46 @@ def _linear(x, w):
     return (x @ w.T).astype(F32)
 
 
-def _store(x, bf16):
-    """Storage rounding of an activation: bf16 RNE when ``bf16``, else fp32."""
-    return ops.round_bf16(x) if bf16 else np.asarray(x, F32)
+STORAGE = ("f32", "bf16", "bf16x2", "bf16x2_mlp")
+
+
+def _storage(bf16, storage) -> str:
+    st = storage or ("bf16" if bf16 else "f32")
+    if st not in STORAGE:
+        raise ValueError(f"storage must be one of {STORAGE}")
+    return st
+
+
+def _store(x, st, role="act"):
+    """Storage rounding of an activation of ``role`` under storage policy ``st``:
+    ``mlp_in`` (an MLP GEMM input), ``gemm_in`` (another GEMM input), ``mlp_proj``
+    (the MLP gate/up projections) or ``act`` (any other stored activation)."""
+    split = st.startswith("bf16x2")
+    if st == "f32" or (split and role == "mlp_proj"):
+        return np.asarray(x, F32)
+    if (split and role == "mlp_in") or (st == "bf16x2" and role == "gemm_in"):
+        return ops.round_split(x)
+    return ops.round_bf16(x)
 
 
 def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, tables,
-                   bf16: bool = False, trace: dict | None = None):
+                   bf16: bool = False, trace: dict | None = None, storage: str | None = None):
     """``full_attention`` (``src/backbone.jl:224-262``) on ``x [T, hidden]``.
 
     ``trace``, when given, receives the intermediates under the names of the
     stages (``qgate``, ``k_proj``, ``v``, ``q``, ``k``, ``scores``, ``probs``,
     ``values``, ``merged``, ``mixed``), each as stored."""
+    st = _storage(bf16, storage)
     T = x.shape[0]
     hd, H, KV = cfg["head_dim"], cfg["heads"], cfg["kv_heads"]
-    qgate = _store(_linear(x, W[p + "self_attn.q_proj.weight"]), bf16).reshape(T, H, 2 * hd)
+    qgate = _store(_linear(x, W[p + "self_attn.q_proj.weight"]), st).reshape(T, H, 2 * hd)
     cos, sin = tables
     q = _store(ops.qk_norm_rope(qgate[:, :, :hd], W[p + "self_attn.q_norm.weight"], cos, sin,
-                                cfg["rotary_dim"], cfg["eps"]), bf16)
-    kp = _store(_linear(x, W[p + "self_attn.k_proj.weight"]), bf16).reshape(T, KV, hd)
+                                cfg["rotary_dim"], cfg["eps"]), st)
+    kp = _store(_linear(x, W[p + "self_attn.k_proj.weight"]), st).reshape(T, KV, hd)
     k = _store(ops.qk_norm_rope(kp, W[p + "self_attn.k_norm.weight"], cos, sin, cfg["rotary_dim"],
-                                cfg["eps"]), bf16)
-    v = _store(_linear(x, W[p + "self_attn.v_proj.weight"]), bf16).reshape(T, KV, hd)
+                                cfg["eps"]), st)
+    v = _store(_linear(x, W[p + "self_attn.v_proj.weight"]), st).reshape(T, KV, hd)
     # AMDGPU form (ext/amdgpu_attention.jl:148-176): scores of every head, the
     # masked softmax with scale inv(sqrt(dim)), the PV product, the gate merge;
     # kv head of query head h is h // (H // KV) (src/backbone.jl:249-251)
@@ -110,9 +136,9 @@ def full_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict, 
     vh = np.repeat(v.transpose(1, 0, 2), groups, axis=0)
     scores = (qh @ kh.transpose(0, 2, 1)).astype(F32)           # [H, query, key]
     probs = _store(attention_softmax(scores[None], mask[None], F32(1) / np.sqrt(F32(hd)))[0],
-                   bf16)
+                   st)
     values = (probs @ vh).astype(F32)                           # [H, query, hd]
-    merged = _store(attention_gate(values[None], qgate[:, :, hd:]), bf16)
+    merged = _store(attention_gate(values[None], qgate[:, :, hd:]), st, "gemm_in")
     mixed = _linear(merged, W[p + "self_attn.o_proj.weight"])
     if trace is not None:
         trace.update(qgate=qgate, k_proj=kp, v=v, q=q, k=k, scores=scores, probs=probs,
@@ -161,7 +187,7 @@ def causal_depthwise(x: np.ndarray, w: np.ndarray) -> np.ndarray:
 
 
 def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
-                    bf16: bool = False, trace: dict | None = None):
+                    bf16: bool = False, trace: dict | None = None, storage: str | None = None):
     """Gated DeltaNet, recurrent form of the CPU default path.
 
     ``cpu_delta_prepare`` (``src/backbone_cpu.jl:465-499``) and
@@ -171,21 +197,23 @@ def delta_attention(W: dict, p: str, x: np.ndarray, mask: np.ndarray, cfg: dict,
     ``trace``, when given, receives the intermediates (``masked``, ``qkv``,
     ``z``, ``a``, ``b``, ``q``, ``k``, ``v``, ``beta``, ``decay``,
     ``recurrence`` (fp32), ``result`` (stored), ``gated``, ``mixed``)."""
+    st = _storage(bf16, storage)
     T = x.shape[0]
     kd, kh, vd, vh = cfg["key_dim"], cfg["key_heads"], cfg["value_dim"], cfg["value_heads"]
     masked = (x * mask.astype(F32)[:, None]).astype(F32)
-    qkv = _store(_linear(masked, W[p + "linear_attn.in_proj_qkv.weight"]), bf16)
+    qkv = _store(_linear(masked, W[p + "linear_attn.in_proj_qkv.weight"]), st)
     conv = W[p + "linear_attn.conv1d.weight"]
     conv = conv.reshape(conv.shape[0], conv.shape[-1])
-    z = _store(_linear(masked, W[p + "linear_attn.in_proj_z.weight"]), bf16).reshape(T, vh, vd)
-    b_raw = _store(_linear(masked, W[p + "linear_attn.in_proj_b.weight"]), bf16)
-    a_raw = _store(_linear(masked, W[p + "linear_attn.in_proj_a.weight"]), bf16)
+    z = _store(_linear(masked, W[p + "linear_attn.in_proj_z.weight"]), st).reshape(T, vh, vd)
+    b_raw = _store(_linear(masked, W[p + "linear_attn.in_proj_b.weight"]), st)
+    a_raw = _store(_linear(masked, W[p + "linear_attn.in_proj_a.weight"]), st)
     a_decay = (F32(-1) * np.exp(W[p + "linear_attn.A_log"].astype(F32))).astype(F32)
     q, k, v, beta, decay = delta_prologue(qkv, conv, a_raw, b_raw, a_decay,
                                           W[p + "linear_attn.dt_bias"], kh, kd, vh, vd)
     recurrence = delta_recurrence(q, k, v, beta, decay)
-    result = _store(recurrence, bf16)
-    out = _store(ops.gated_rms(result, z, W[p + "linear_attn.norm.weight"], cfg["eps"]), bf16)
+    result = _store(recurrence, st)
+    out = _store(ops.gated_rms(result, z, W[p + "linear_attn.norm.weight"], cfg["eps"]), st,
+                 "gemm_in")
     mixed = _linear(out.reshape(T, vh * vd), W[p + "linear_attn.out_proj.weight"])
     if trace is not None:
         trace.update(masked=masked, qkv=qkv, z=z, a=a_raw, b=b_raw, q=q, k=k, v=v, beta=beta,
@@ -260,40 +288,42 @@ def check_sequence(ids, mask, vocab):
 
 
 def backbone_layer(W: dict, cfg: dict, i: int, h: np.ndarray, normed: np.ndarray,
-                   mask: np.ndarray, tables, bf16: bool = False, trace: dict | None = None):
+                   mask: np.ndarray, tables, bf16: bool = False, trace: dict | None = None,
+                   storage: str | None = None):
     """Layer ``i`` of ``native_hidden_states`` (``native_layer``,
     ``src/backbone.jl:358-388``) from the residual stream ``h`` and its input
     norm ``normed``: returns the next ``(h, normed)``, where ``normed`` is the next
     layer's input norm (the final norm after the last layer) fused with the MLP
     residual add.  ``trace`` also receives ``residual``, ``post_normed``, ``gate``,
     ``up``, ``act`` and ``down`` besides the attention intermediates."""
+    st = _storage(bf16, storage)
     eps = cfg["eps"]
     kinds = cfg["layer_types"]
     p = f"layers.{i}."
     if kinds[i] == "full_attention":
-        mixed = full_attention(W, p, normed, mask, cfg, tables, bf16, trace)
+        mixed = full_attention(W, p, normed, mask, cfg, tables, trace=trace, storage=st)
     elif kinds[i] == "linear_attention":
-        mixed = delta_attention(W, p, normed, mask, cfg, bf16, trace)
+        mixed = delta_attention(W, p, normed, mask, cfg, trace=trace, storage=st)
     else:
         raise ValueError(f"Unsupported layer type {kinds[i]}.")
     residual, post = ops.residual_rms(h, mixed, W[p + "post_attention_layernorm.weight"], eps)
-    post = _store(post, bf16)
-    gate = _store(_linear(post, W[p + "mlp.gate_proj.weight"]), bf16)
-    up = _store(_linear(post, W[p + "mlp.up_proj.weight"]), bf16)
-    act = _store(ops.swiglu(gate, up), bf16)
+    post = _store(post, st, "mlp_in")
+    gate = _store(_linear(post, W[p + "mlp.gate_proj.weight"]), st, "mlp_proj")
+    up = _store(_linear(post, W[p + "mlp.up_proj.weight"]), st, "mlp_proj")
+    act = _store(ops.swiglu(gate, up), st, "mlp_in")
     down = _linear(act, W[p + "mlp.down_proj.weight"])
     last = i + 1 == len(kinds)
     nxt = W["norm.weight"] if last else W[f"layers.{i + 1}.input_layernorm.weight"]
     # native_residual_add! (src/backbone.jl:358-361), then the next RMSNorm
     h, normed = ops.residual_rms(residual, down, nxt, eps)
     if not last:
-        normed = _store(normed, bf16)
+        normed = _store(normed, st, "gemm_in")
     if trace is not None:
         trace.update(residual=residual, post_normed=post, gate=gate, up=up, act=act, down=down)
     return h, normed
 
 
-def embed(W: dict, cfg: dict, ids, mask, bf16: bool = False):
+def embed(W: dict, cfg: dict, ids, mask, bf16: bool = False, storage: str | None = None):
     """Checked ids, the gathered residual stream and the first input norm:
     ``(ids, mask, h, normed, tables)`` (``src/backbone.jl:433-446``)."""
     embed_table = W["embed_tokens.weight"]
@@ -304,17 +334,21 @@ def embed(W: dict, cfg: dict, ids, mask, bf16: bool = False):
     h = ops.gather(embed_table, ids)
     tables = ops.rope_tables(T, cfg["rotary_dim"], cfg["rope_theta"]) if cfg["rotary_dim"] else (
         np.zeros((T, 0), F32), np.zeros((T, 0), F32))
-    normed = _store(ops.rms(h, W["layers.0.input_layernorm.weight"], cfg["eps"]), bf16)
+    normed = _store(ops.rms(h, W["layers.0.input_layernorm.weight"], cfg["eps"]),
+                    _storage(bf16, storage), "gemm_in")
     return ids, mask, h, normed, tables
 
 
-def backbone_hidden(W: dict, cfg: dict, ids, mask, bf16: bool = False) -> np.ndarray:
+def backbone_hidden(W: dict, cfg: dict, ids, mask, bf16: bool = False,
+                    storage: str | None = None) -> np.ndarray:
     """``backbone_hidden`` (``src/backbone.jl:433-460``) -> ``[T, hidden]`` fp32.
 
     The residual add of each layer is computed together with the next RMSNorm
     (the final norm after the last layer); ``bf16`` selects bf16 storage of
-    the activations listed in the module docstring."""
-    ids, mask, h, normed, tables = embed(W, cfg, ids, mask, bf16)
+    the activations listed in the module docstring (``storage`` selects any of
+    the policies there)."""
+    st = _storage(bf16, storage)
+    ids, mask, h, normed, tables = embed(W, cfg, ids, mask, storage=st)
     for i in range(len(cfg["layer_types"])):
-        h, normed = backbone_layer(W, cfg, i, h, normed, mask, tables, bf16)
+        h, normed = backbone_layer(W, cfg, i, h, normed, mask, tables, storage=st)
     return normed

@@ -91,6 +91,39 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     return bf16_to_f32(f32_to_bf16(x))
 
 
+def split_bf16(x: np.ndarray) -> np.ndarray:
+    """The two-term bf16 form of fp32 values (the library's ``QDC_BF16X2`` output;
+    no counterpart in the reference, whose GPU path is fp32 only): ``hi = bf16(x)``
+    and ``lo = bf16(x - hi)``, both RNE as :func:`f32_to_bf16`, ``lo = 0`` where
+    ``hi`` is not finite.  Returns uint16 bit patterns ``[..., 2K]`` for ``[..., K]``
+    (K a multiple of 4), every aligned group of 4 elements laid out ``[4 hi | 4 lo]``."""
+    x = _f32(x)
+    K = x.shape[-1]
+    if K % 4:
+        raise ValueError("the split form needs whole groups of 4 elements")
+    hi_bits = f32_to_bf16(x)
+    hi = bf16_to_f32(hi_bits)
+    with np.errstate(invalid="ignore"):
+        rest = np.where(np.isfinite(hi), x - hi, np.float32(0)).astype(np.float32)
+    lo_bits = f32_to_bf16(rest)
+    lead = x.shape[:-1]
+    pieces = np.stack([hi_bits.reshape(*lead, K // 4, 4), lo_bits.reshape(*lead, K // 4, 4)], -2)
+    return pieces.reshape(*lead, 2 * K)
+
+
+def join_split(bits: np.ndarray) -> np.ndarray:
+    """fp32 ``hi + lo`` of split bit patterns ``[..., 2K]`` -> ``[..., K]``."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    lead, K2 = bits.shape[:-1], bits.shape[-1]
+    g = bf16_to_f32(bits).reshape(*lead, K2 // 8, 2, 4)
+    return (g[..., 0, :] + g[..., 1, :]).astype(np.float32).reshape(*lead, K2 // 2)
+
+
+def round_split(x: np.ndarray) -> np.ndarray:
+    """fp32 values as the split form stores them (``hi + lo``)."""
+    return join_split(split_bf16(x))
+
+
 def gather(table: np.ndarray, ids: np.ndarray) -> np.ndarray:
     """``src/backbone.jl:56-64``: row copy, any element type.  ValueError on a bad id."""
     table = np.ascontiguousarray(table)

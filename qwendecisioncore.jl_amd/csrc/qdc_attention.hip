@@ -324,8 +324,8 @@ __global__ __launch_bounds__(kBlock) void gate_merge_general(Gate a) {
     const float v = a.values[(((int64_t)b * a.heads.d + h) * a.seq.d + s) * dim + r];
     const float gv = to_f32(reinterpret_cast<const TG *>(
         a.gate)[(int64_t)t * a.gate_tok + (int64_t)h * a.gate_head + r]);
-    reinterpret_cast<TO *>(a.out)[(int64_t)t * a.out_tok + (int64_t)h * dim + r] =
-        from_f32<TO>(v * sigmoid_ref(gv));
+    put_elem(reinterpret_cast<TO *>(a.out), (int64_t)t * a.out_tok + (int64_t)h * dim + r,
+             v * sigmoid_ref(gv));
 }
 
 }  // namespace
@@ -406,8 +406,10 @@ extern "C" int32_t qdc_attention_gate(void *out, int32_t out_dtype, const float 
                                       int64_t seq, int64_t heads, int64_t head_dim,
                                       int64_t gate_tok, int64_t gate_head, int64_t out_tok,
                                       hipStream_t stream) {
-    if (!valid_dtype(out_dtype) || !valid_dtype(gate_dtype)) return QDC_ERR_DTYPE;
+    const bool split = out_dtype == QDC_BF16X2;
+    if (!(valid_dtype(out_dtype) || split) || !valid_dtype(gate_dtype)) return QDC_ERR_DTYPE;
     if (batch < 0 || seq < 0 || heads <= 0 || head_dim <= 0) return QDC_ERR_SHAPE;
+    if (split && !split_rows_ok(head_dim, out_tok)) return QDC_ERR_SHAPE;
     const int64_t tokens = batch * seq;
     if (tokens == 0) return QDC_OK;
     if (gate_head < head_dim || gate_tok < (heads - 1) * gate_head + head_dim ||
@@ -444,9 +446,11 @@ extern "C" int32_t qdc_attention_gate(void *out, int32_t out_dtype, const float 
         hipLaunchKernelGGL((gate_merge_general<TG, TO>), grid, dim3(kBlock), 0, stream, a);  \
     return launch_status();
     if (gate_dtype == QDC_BF16) {
+        if (split) { QDC_GATE(bf16_t, split_t) }
         if (out_dtype == QDC_BF16) { QDC_GATE(bf16_t, bf16_t) }
         QDC_GATE(bf16_t, float)
     }
+    if (split) { QDC_GATE(float, split_t) }
     if (out_dtype == QDC_BF16) { QDC_GATE(float, bf16_t) }
     QDC_GATE(float, float)
 #undef QDC_GATE

@@ -170,6 +170,67 @@ template <int V> __device__ __forceinline__ void store_frag(bf16_t *p, const flo
     }
 }
 
+// ------------------------------------------------------ two-term bf16 ----
+// The split output form (QDC_BF16X2): an fp32 value v is written as two bf16
+// terms, hi = bf16(v) and lo = bf16(v - hi) (both round to nearest even), so
+// hi + lo keeps about 16 significant bits (|v - (hi + lo)| <= 2^-17 |v| for
+// normal v: |v - hi| <= 2^-8 |v| and lo rounds that rest to 8 bits).  A
+// non-finite hi (inf, NaN, or v beyond the bf16 range) gets lo = 0.  Element e
+// of a split tensor takes bf16 slots 8*(e/4) + e%4 (hi) and 8*(e/4) + 4 + e%4
+// (lo): each aligned group of 4 elements is one 16-byte piece [4 hi | 4 lo], so
+// a split element has the 4-byte footprint of an fp32 one and every address
+// computation of an fp32 output applies unchanged.  A GEMM reads a split row
+// of K elements as 2K bf16 values against a weight whose K rows are repeated
+// in the same pattern: sum(hi*w + lo*w) = sum((hi + lo)*w) with bf16 operands.
+struct split_t {
+    uint32_t bits;
+};
+
+// Tensors a kernel reads beside a split output (norm weights, gates) are bf16.
+template <typename T> struct AuxOf {
+    typedef T type;
+};
+template <> struct AuxOf<split_t> {
+    typedef bf16_t type;
+};
+template <typename T> using Aux = typename AuxOf<T>::type;
+
+__device__ __forceinline__ void split2(float v, float &hi, float &lo) {
+    hi = to_f32(from_f32<bf16_t>(v));
+    lo = (__float_as_uint(hi) & 0x7f800000u) == 0x7f800000u ? 0.0f : v - hi;  // exact
+}
+
+// One aligned group of 4 values as its 16-byte split piece.
+__device__ __forceinline__ u32x4 pack_split4(const float *v) {
+    float h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) split2(v[j], h[j], l[j]);
+    return u32x4{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(l[0], l[1]),
+                 pack_bf16x2(l[2], l[3])};
+}
+
+template <int V> __device__ __forceinline__ void store_frag(split_t *p, const float (&v)[V]) {
+    static_assert(V % 4 == 0, "split stores cover whole groups of 4 elements");
+#pragma unroll
+    for (int i = 0; i < V / 4; ++i) store_raw(p + 4 * i, pack_split4(v + 4 * i));
+}
+__device__ __forceinline__ void store_chunk(split_t *p, const float (&v)[4]) {
+    store_raw(p, pack_split4(v));
+}
+
+// One element at element index e of an output (the general kernels' store).
+__device__ __forceinline__ void put_elem(float *p, int64_t e, float v) { p[e] = v; }
+__device__ __forceinline__ void put_elem(bf16_t *p, int64_t e, float v) {
+    p[e] = from_f32<bf16_t>(v);
+}
+__device__ __forceinline__ void put_elem(split_t *p, int64_t e, float v) {
+    float hi, lo;
+    split2(v, hi, lo);
+    bf16_t *b = reinterpret_cast<bf16_t *>(p) + 8 * (e >> 2) + (e & 3);
+    b[0] = from_f32<bf16_t>(hi);
+    b[4] = from_f32<bf16_t>(lo);
+}
+
 // ------------------------------------------------------------- reductions --
 // Sum over aligned groups of N lanes (N a power of two <= 64) of a wavefront;
 // every lane of a group ends with the bit-identical sum (each step adds a pair
@@ -248,8 +309,13 @@ constexpr int32_t kNoFastPath = INT32_MIN;
 
 // --------------------------------------------------------- host helpers ---
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+// Bytes per element; a QDC_BF16X2 element is two bf16 terms.
 static inline int64_t elem_size(int32_t dtype) { return dtype == QDC_BF16 ? 2 : 4; }
 static inline bool valid_dtype(int32_t dtype) { return dtype == QDC_F32 || dtype == QDC_BF16; }
+// A split output's rows must start on a group of 4 elements and hold whole groups.
+static inline bool split_rows_ok(int64_t width, int64_t row_stride) {
+    return width % 4 == 0 && row_stride % 4 == 0;
+}
 
 // Launch status: a positive hipError_t when the launch failed, else 0.
 static inline int32_t launch_status() {

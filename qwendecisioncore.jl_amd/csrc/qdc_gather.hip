@@ -170,8 +170,8 @@ __global__ __launch_bounds__(kBlock) void gather_general(TO *__restrict__ out,
 template <typename TT, typename TN, int LPR, int CPL>
 __global__ __launch_bounds__(kBlock) void gather_rms_fast(
     float *__restrict__ hidden, TN *__restrict__ normed, const TT *__restrict__ table,
-    const int32_t *__restrict__ ids, const TN *__restrict__ w, const int32_t *__restrict__ keep,
-    int64_t n, int64_t vocab, float eps, int32_t *error_flag) {
+    const int32_t *__restrict__ ids, const Aux<TN> *__restrict__ w,
+    const int32_t *__restrict__ keep, int64_t n, int64_t vocab, float eps, int32_t *error_flag) {
     constexpr int V = 4;
     constexpr int W = LPR * CPL * V;  // row width
     constexpr int RPB = kBlock / LPR;
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(kBlock) void gather_rms_fast(
     const bool valid = active && id >= 0 && id < vocab;
     if (active && !valid && lane == 0 && error_flag) atomicOr(error_flag, 1);
     Frag<TT, V> xr[CPL];
-    Frag<TN, V> wr[CPL];
+    Frag<Aux<TN>, V> wr[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         if (valid) {
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kBlock) void gather_rms_fast(
         }
     }
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) wr[c] = load_frag<TN, V>(w + (c * LPR + lane) * V);
+    for (int c = 0; c < CPL; ++c) wr[c] = load_frag<Aux<TN>, V>(w + (c * LPR + lane) * V);
     const float keep_row = (active && keep) ? (float)keep[row] : 1.0f;
     float v[CPL][V];
     float ss = 0.0f;
@@ -293,8 +293,9 @@ __global__ __launch_bounds__(kBlock) void gather_rms_bf16(
 template <typename TT, typename TN>
 __global__ __launch_bounds__(kBlock) void gather_rms_general(
     float *__restrict__ hidden, TN *__restrict__ normed, const TT *__restrict__ table,
-    const int32_t *__restrict__ ids, const TN *__restrict__ w, const int32_t *__restrict__ keep,
-    int64_t n, int64_t vocab, int64_t width, float eps, int32_t *error_flag) {
+    const int32_t *__restrict__ ids, const Aux<TN> *__restrict__ w,
+    const int32_t *__restrict__ keep, int64_t n, int64_t vocab, int64_t width, float eps,
+    int32_t *error_flag) {
     const int lane = threadIdx.x % kWave;
     const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
     if (row >= n) return;  // uniform per wavefront
@@ -315,13 +316,13 @@ __global__ __launch_bounds__(kBlock) void gather_rms_general(
     for (int64_t i = lane; i < width; i += kWave) {
         float o = (h[i] * s) * (1.0f + to_f32(w[i]));
         if (keep) o = o * keep_row;
-        normed[row * width + i] = from_f32<TN>(o);
+        put_elem(normed, row * width + i, o);
     }
 }
 
 template <typename TT, typename TN, int LPR, int CPL>
 int32_t launch_gather_rms_fast(float *hidden, TN *normed, const TT *table, const int32_t *ids,
-                               const TN *w, const int32_t *keep, int64_t n, int64_t vocab,
+                               const Aux<TN> *w, const int32_t *keep, int64_t n, int64_t vocab,
                                float eps, int32_t *error_flag, hipStream_t stream) {
     hipLaunchKernelGGL((gather_rms_fast<TT, TN, LPR, CPL>),
                        dim3((uint32_t)ceil_div(n, kBlock / LPR)), dim3(kBlock), 0, stream, hidden,
@@ -333,7 +334,7 @@ int32_t launch_gather_rms_fast(float *hidden, TN *normed, const TT *table, const
 // up to 64 groups (a power of two), else 64 lanes of G/64 groups.
 template <typename TT, typename TN>
 int32_t launch_gather_rms(float *hidden, TN *normed, const TT *table, const int32_t *ids,
-                          const TN *w, const int32_t *keep, int64_t n, int64_t vocab,
+                          const Aux<TN> *w, const int32_t *keep, int64_t n, int64_t vocab,
                           int64_t width, float eps, bool fast, int32_t *error_flag,
                           hipStream_t stream) {
     if constexpr (sizeof(TT) == 2 && sizeof(TN) == 2) {
@@ -463,16 +464,19 @@ extern "C" int32_t qdc_embedding_gather_rmsnorm(void *hidden, void *normed, cons
                                                 const int32_t *token_mask, int64_t n_ids,
                                                 int64_t vocab, int64_t width, float eps,
                                                 int32_t *error_flag, hipStream_t stream) {
-    if (!valid_dtype(table_dtype) || !valid_dtype(normed_dtype)) return QDC_ERR_DTYPE;
+    const bool split = normed_dtype == QDC_BF16X2;  // with a bf16 weight
+    if (!valid_dtype(table_dtype) || !(valid_dtype(normed_dtype) || split)) return QDC_ERR_DTYPE;
     if (n_ids < 0 || vocab < 0 || width < 0) return QDC_ERR_SHAPE;
     if (n_ids == 0 || width == 0) return QDC_OK;
     if (vocab == 0) return QDC_ERR_RANGE;
     if (n_ids >= ((int64_t)1 << 26)) return QDC_ERR_SHAPE;  // wavefront-per-row grid limit
     if (!hidden || !normed || !table || !ids || !weight) return QDC_ERR_NULL;
+    if (split && !split_rows_ok(width, width)) return QDC_ERR_SHAPE;
     const int64_t ti = elem_size(table_dtype), tn = elem_size(normed_dtype);
+    const int64_t tw = split ? 2 : tn;  // weight element bytes
     const int64_t hb = n_ids * width * 4, nb = n_ids * width * tn;
     const void *ins[4] = {table, ids, weight, token_mask};
-    const int64_t in_bytes[4] = {vocab * width * ti, n_ids * 4, width * tn,
+    const int64_t in_bytes[4] = {vocab * width * ti, n_ids * 4, width * tw,
                                  token_mask ? n_ids * 4 : 0};
     for (int i = 0; i < 4; ++i)
         if (overlaps(hidden, hb, ins[i], in_bytes[i]) || overlaps(normed, nb, ins[i], in_bytes[i]))
@@ -483,6 +487,14 @@ extern "C" int32_t qdc_embedding_gather_rmsnorm(void *hidden, void *normed, cons
     const bool fast = aligned16(hidden) && aligned16(table) && aligned16(normed) &&
                       aligned16(weight) && (width * ti) % 16 == 0 && (width * tn) % 16 == 0;
     float *h = static_cast<float *>(hidden);
+    if (split && table_dtype == QDC_BF16)
+        return launch_gather_rms(h, (split_t *)normed, (const bf16_t *)table, ids,
+                                 (const bf16_t *)weight, token_mask, n_ids, vocab, width, eps,
+                                 fast, error_flag, stream);
+    if (split)
+        return launch_gather_rms(h, (split_t *)normed, (const float *)table, ids,
+                                 (const bf16_t *)weight, token_mask, n_ids, vocab, width, eps,
+                                 fast, error_flag, stream);
     if (table_dtype == QDC_BF16 && normed_dtype == QDC_BF16)
         return launch_gather_rms(h, (bf16_t *)normed, (const bf16_t *)table, ids,
                                  (const bf16_t *)weight, token_mask, n_ids, vocab, width, eps,

@@ -55,8 +55,8 @@ template <typename TX, typename TM, typename TO> constexpr int group_elems() {
 
 template <typename TX, typename TM, typename TO, int LPR, int CPL, Mode M, bool CENTERED>
 __global__ __launch_bounds__(kBlock) void rms_rows_fast(
-    TO *out, TX *res_out, const TX *x, const TM *mixed, const TO *__restrict__ z,
-    const TO *__restrict__ w, const int32_t *__restrict__ keep, int64_t rows, RowMap map,
+    TO *out, TX *res_out, const TX *x, const TM *mixed, const Aux<TO> *__restrict__ z,
+    const Aux<TO> *__restrict__ w, const int32_t *__restrict__ keep, int64_t rows, RowMap map,
     float width, float eps) {
     constexpr int V = group_elems<TX, TM, TO>();
     constexpr int RPB = kBlock / LPR;  // rows per workgroup
@@ -76,8 +76,8 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
     // Issue every load of the row before the first dependent instruction.
     Frag<TX, V> xr[CPL];
     Frag<TM, V> mr[M == Mode::kResidual ? CPL : 1];
-    Frag<TO, V> zr[M == Mode::kGated ? CPL : 1];
-    Frag<TO, V> wr[CPL];
+    Frag<Aux<TO>, V> zr[M == Mode::kGated ? CPL : 1];
+    Frag<Aux<TO>, V> wr[CPL];
     if (active) {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) xr[c] = stream_frag<TX, V>(x + xo + (c * LPR + lane) * V);
@@ -88,10 +88,11 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
         }
         if constexpr (M == Mode::kGated) {
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) zr[c] = stream_frag<TO, V>(z + zo + (c * LPR + lane) * V);
+            for (int c = 0; c < CPL; ++c)
+                zr[c] = stream_frag<Aux<TO>, V>(z + zo + (c * LPR + lane) * V);
         }
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) wr[c] = load_frag<TO, V>(w + (c * LPR + lane) * V);
+        for (int c = 0; c < CPL; ++c) wr[c] = load_frag<Aux<TO>, V>(w + (c * LPR + lane) * V);
     }
     int32_t keep_row = 1;
     if (active && keep) keep_row = keep[row];
@@ -154,8 +155,8 @@ __global__ __launch_bounds__(kBlock) void rms_rows_fast(
 // One wavefront per row, any width/stride/alignment.
 template <typename TX, typename TM, typename TO, Mode M, bool CENTERED>
 __global__ __launch_bounds__(kBlock) void rms_rows_general(
-    TO *out, TX *res_out, const TX *x, const TM *mixed, const TO *__restrict__ z,
-    const TO *__restrict__ w, const int32_t *__restrict__ keep, int64_t rows, RowMap map,
+    TO *out, TX *res_out, const TX *x, const TM *mixed, const Aux<TO> *__restrict__ z,
+    const Aux<TO> *__restrict__ w, const int32_t *__restrict__ keep, int64_t rows, RowMap map,
     int64_t width, float eps) {
     const int lane = threadIdx.x % kWave;
     const int64_t row = (int64_t)blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(kBlock) void rms_rows_general(
             o = (v * s) * (CENTERED ? (1.0f + wv) : wv);
             if (keep) o = o * keep_row;
         }
-        out[oo + i] = from_f32<TO>(o);
+        put_elem(out, oo + i, o);
     }
 }
 
@@ -211,8 +212,8 @@ int32_t launch_fast(const Args &a, hipStream_t stream) {
     const int64_t blocks = ceil_div(a.rows, kBlock / LPR);
     hipLaunchKernelGGL((rms_rows_fast<TX, TM, TO, LPR, CPL, M, C>), dim3((uint32_t)blocks),
                        dim3(kBlock), 0, stream, (TO *)a.out, (TX *)a.res, (const TX *)a.x,
-                       (const TM *)a.mixed, (const TO *)a.z, (const TO *)a.w, a.keep, a.rows,
-                       a.map, (float)a.width, a.eps);
+                       (const TM *)a.mixed, (const Aux<TO> *)a.z, (const Aux<TO> *)a.w, a.keep,
+                       a.rows, a.map, (float)a.width, a.eps);
     return launch_status();
 }
 
@@ -280,7 +281,8 @@ int32_t run(const Args &a, hipStream_t stream) {
     const int64_t blocks = ceil_div(a.rows, kBlock / kWave);
     hipLaunchKernelGGL((rms_rows_general<TX, TM, TO, M, C>), dim3((uint32_t)blocks), dim3(kBlock),
                        0, stream, (TO *)a.out, (TX *)a.res, (const TX *)a.x, (const TM *)a.mixed,
-                       (const TO *)a.z, (const TO *)a.w, a.keep, a.rows, a.map, a.width, a.eps);
+                       (const Aux<TO> *)a.z, (const Aux<TO> *)a.w, a.keep, a.rows, a.map, a.width,
+                       a.eps);
     return launch_status();
 }
 
@@ -298,12 +300,15 @@ bool all16(std::initializer_list<const void *> ptrs) {
 int32_t rmsnorm(void *out, const void *x, const void *weight, const int32_t *keep, bool masked,
                 int64_t rows, int64_t width, int64_t ld_x, int64_t ld_out, float eps,
                 int32_t centered, int32_t x_dtype, int32_t out_dtype, hipStream_t stream) {
-    if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return QDC_ERR_DTYPE;
-    if (x_dtype == QDC_BF16 && out_dtype == QDC_F32) return QDC_ERR_DTYPE;
+    const bool split = out_dtype == QDC_BF16X2;  // fp32 rows, bf16 weight
+    if (!valid_dtype(x_dtype) || !(valid_dtype(out_dtype) || split)) return QDC_ERR_DTYPE;
+    if (x_dtype == QDC_BF16 && out_dtype != QDC_BF16) return QDC_ERR_DTYPE;
     if (rows < 0 || width < 0 || rows >= kMaxRows) return QDC_ERR_SHAPE;
     if (rows == 0 || width == 0) return QDC_OK;
     if (!out || !x || !weight || (masked && !keep)) return QDC_ERR_NULL;
     if (ld_x < width || ld_out < width) return QDC_ERR_SHAPE;
+    if (split && !split_rows_ok(width, ld_out)) return QDC_ERR_SHAPE;
+    if (split && out == x) return QDC_ERR_ALIAS;
     const int64_t ex = elem_size(x_dtype), eo = elem_size(out_dtype);
     const int64_t span_x = ((rows - 1) * ld_x + width) * ex;
     const int64_t span_o = ((rows - 1) * ld_out + width) * eo;
@@ -312,15 +317,18 @@ int32_t rmsnorm(void *out, const void *x, const void *weight, const int32_t *kee
         return QDC_ERR_ALIAS;
     if (masked && overlaps(out, span_o, keep, rows * (int64_t)sizeof(int32_t)))
         return QDC_ERR_ALIAS;
+    if (overlaps(out, span_o, weight, width * (split ? 2 : eo))) return QDC_ERR_ALIAS;
     Args a{out, nullptr, x, nullptr, nullptr, weight, rows, width,
            RowMap{make_fastdiv(1), ld_x, 0, 0, 0, ld_out, 0}, eps,
            all16({out, x, weight}) && (ld_x * ex) % 16 == 0 && (ld_out * eo) % 16 == 0};
     a.keep = masked ? keep : nullptr;
     if (centered) {
+        if (split) return run<float, float, split_t, Mode::kPlain, true>(a, stream);
         if (x_dtype == QDC_BF16) return run<bf16_t, bf16_t, bf16_t, Mode::kPlain, true>(a, stream);
         if (out_dtype == QDC_BF16) return run<float, float, bf16_t, Mode::kPlain, true>(a, stream);
         return run<float, float, float, Mode::kPlain, true>(a, stream);
     }
+    if (split) return run<float, float, split_t, Mode::kPlain, false>(a, stream);
     if (x_dtype == QDC_BF16) return run<bf16_t, bf16_t, bf16_t, Mode::kPlain, false>(a, stream);
     if (out_dtype == QDC_BF16) return run<float, float, bf16_t, Mode::kPlain, false>(a, stream);
     return run<float, float, float, Mode::kPlain, false>(a, stream);
@@ -331,7 +339,11 @@ int32_t residual_rmsnorm(void *residual, void *out, const void *x, const void *m
                          const void *weight, const int32_t *keep, bool masked, int64_t rows,
                          int64_t width, float eps, int32_t residual_dtype, int32_t mixed_dtype,
                          int32_t out_dtype, hipStream_t stream) {
-    if (!valid_dtype(residual_dtype) || !valid_dtype(mixed_dtype) || !valid_dtype(out_dtype))
+    // the split output takes an fp32 residual stream and an fp32 addend
+    const bool split = out_dtype == QDC_BF16X2;
+    if (split && (residual_dtype != QDC_F32 || mixed_dtype != QDC_F32)) return QDC_ERR_DTYPE;
+    if (!valid_dtype(residual_dtype) || !valid_dtype(mixed_dtype) ||
+        !(valid_dtype(out_dtype) || split))
         return QDC_ERR_DTYPE;
     const bool all_f32 =
         residual_dtype == QDC_F32 && mixed_dtype == QDC_F32 && out_dtype == QDC_F32;
@@ -343,6 +355,7 @@ int32_t residual_rmsnorm(void *residual, void *out, const void *x, const void *m
     if (rows < 0 || width < 0 || rows >= kMaxRows) return QDC_ERR_SHAPE;
     if (rows == 0 || width == 0) return QDC_OK;
     if (!residual || !out || !x || !mixed || !weight || (masked && !keep)) return QDC_ERR_NULL;
+    if (split && !split_rows_ok(width, width)) return QDC_ERR_SHAPE;
     const int64_t br = rows * width * elem_size(residual_dtype);
     const int64_t bm = rows * width * elem_size(mixed_dtype);
     const int64_t bo = rows * width * elem_size(out_dtype);
@@ -357,10 +370,13 @@ int32_t residual_rmsnorm(void *residual, void *out, const void *x, const void *m
     const int64_t bk = rows * (int64_t)sizeof(int32_t);
     if (masked && (overlaps(out, bo, keep, bk) || overlaps(residual, br, keep, bk)))
         return QDC_ERR_ALIAS;
+    const int64_t bw = width * (split ? 2 : elem_size(out_dtype));
+    if (overlaps(out, bo, weight, bw) || overlaps(residual, br, weight, bw)) return QDC_ERR_ALIAS;
     Args a{out, residual, x, mixed, nullptr, weight, rows, width,
            RowMap{make_fastdiv(1), width, 0, 0, 0, width, 0}, eps,
            all16({residual, out, x, mixed, weight})};
     a.keep = masked ? keep : nullptr;
+    if (split) return run<float, float, split_t, Mode::kResidual, true>(a, stream);
     if (all_f32) return run<float, float, float, Mode::kResidual, true>(a, stream);
     if (all_bf16) return run<bf16_t, bf16_t, bf16_t, Mode::kResidual, true>(a, stream);
     if (mixed_dtype == QDC_F32) return run<float, float, bf16_t, Mode::kResidual, true>(a, stream);
@@ -411,27 +427,32 @@ extern "C" int32_t qdc_residual_rmsnorm_masked(void *residual, void *out, const 
 extern "C" int32_t qdc_gated_rmsnorm(void *out, const void *x, const void *z, const void *weight,
                                      int64_t tokens, int64_t heads, int64_t width, int64_t x_tok,
                                      int64_t z_tok, int64_t out_tok, float eps, int32_t dtype,
-                                     hipStream_t stream) {
-    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
+                                     int32_t out_dtype, hipStream_t stream) {
+    // out in dtype, or bf16 x, z and weight with the split output
+    const bool split = dtype == QDC_BF16 && out_dtype == QDC_BF16X2;
+    if (!valid_dtype(dtype) || !(out_dtype == dtype || split)) return QDC_ERR_DTYPE;
     if (tokens < 0 || heads < 0 || width < 0) return QDC_ERR_SHAPE;
     if (tokens == 0 || heads == 0 || width == 0) return QDC_OK;
     if (!out || !x || !z || !weight) return QDC_ERR_NULL;
     if (tokens * heads >= kMaxRows || heads >= kMaxRows) return QDC_ERR_SHAPE;
     if (x_tok < heads * width || z_tok < heads * width || out_tok < heads * width)
         return QDC_ERR_SHAPE;
-    const int64_t es = elem_size(dtype);
-    const int64_t span_o = ((tokens - 1) * out_tok + heads * width) * es;
-    if (out != x && overlaps(out, span_o, x, ((tokens - 1) * x_tok + heads * width) * es))
+    if (split && !split_rows_ok(width, out_tok)) return QDC_ERR_SHAPE;
+    const int64_t es = elem_size(dtype), eo = elem_size(out_dtype);
+    const int64_t span_o = ((tokens - 1) * out_tok + heads * width) * eo;
+    const int64_t span_x = ((tokens - 1) * x_tok + heads * width) * es;
+    if (out == x ? (out_tok != x_tok || eo != es) : overlaps(out, span_o, x, span_x))
         return QDC_ERR_ALIAS;
-    if (out == x && out_tok != x_tok) return QDC_ERR_ALIAS;
     if (overlaps(out, span_o, z, ((tokens - 1) * z_tok + heads * width) * es))
         return QDC_ERR_ALIAS;
+    if (overlaps(out, span_o, weight, width * es)) return QDC_ERR_ALIAS;
     const Args a{out, nullptr, x, nullptr, z, weight, tokens * heads, width,
                  RowMap{make_fastdiv((uint32_t)heads), x_tok, width, z_tok, width, out_tok, width},
                  eps,
                  all16({out, x, z, weight}) && (width * es) % 16 == 0 &&
                      (x_tok * es) % 16 == 0 && (z_tok * es) % 16 == 0 &&
-                     (out_tok * es) % 16 == 0};
+                     (out_tok * eo) % 16 == 0};
+    if (split) return run<bf16_t, bf16_t, split_t, Mode::kGated, false>(a, stream);
     if (dtype == QDC_BF16) return run<bf16_t, bf16_t, bf16_t, Mode::kGated, false>(a, stream);
     return run<float, float, float, Mode::kGated, false>(a, stream);
 }

@@ -1,5 +1,8 @@
 // qdc_swiglu.hip -- SwiGLU out = silu(gate) * up for gfx950.
 //
+// Types: TI is gate and up, TO the output (the same type, or the split
+// two-term bf16 form of fp32 values).
+//
 // Fast path: the [tokens, width] output is cut into 16-byte chunks numbered
 // row-major; each thread handles kUnroll chunks spaced one workgroup apart,
 // issuing all gate/up loads before any arithmetic.  Token/column of a chunk
@@ -15,12 +18,12 @@ namespace {
 
 constexpr int kUnroll = 1;
 
-template <typename T>
-__global__ __launch_bounds__(kBlock) void swiglu_fast(T *out, const T *gate, const T *up,
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void swiglu_fast(TO *out, const TI *gate, const TI *up,
                                                       uint32_t total_chunks, FastDiv per_row,
                                                       int64_t ld_gate, int64_t ld_up,
                                                       int64_t ld_out) {
-    constexpr int V = Elem<T>::kVec;
+    constexpr int V = Elem<TI>::kVec;
     const uint32_t base = blockIdx.x * (uint32_t)(kBlock * kUnroll) + threadIdx.x;
     float g[kUnroll][V], u[kUnroll][V];
     int64_t oo[kUnroll];
@@ -47,8 +50,8 @@ __global__ __launch_bounds__(kBlock) void swiglu_fast(T *out, const T *gate, con
 }
 
 // Element-wise, any width/stride/alignment.
-template <typename T>
-__global__ __launch_bounds__(kBlock) void swiglu_general(T *out, const T *gate, const T *up,
+template <typename TI, typename TO>
+__global__ __launch_bounds__(kBlock) void swiglu_general(TO *out, const TI *gate, const TI *up,
                                                          int64_t tokens, int64_t width,
                                                          int64_t ld_gate, int64_t ld_up,
                                                          int64_t ld_out) {
@@ -58,25 +61,25 @@ __global__ __launch_bounds__(kBlock) void swiglu_general(T *out, const T *gate, 
         const int64_t t = i / width, c = i - t * width;
         const float g = to_f32(gate[t * ld_gate + c]);
         const float u = to_f32(up[t * ld_up + c]);
-        out[t * ld_out + c] = from_f32<T>(silu(g) * u);
+        put_elem(out, t * ld_out + c, silu(g) * u);
     }
 }
 
-template <typename T>
+template <typename TI, typename TO>
 int32_t launch(void *out, const void *gate, const void *up, int64_t tokens, int64_t width,
                int64_t ld_gate, int64_t ld_up, int64_t ld_out, bool fast, hipStream_t stream) {
-    constexpr int V = Elem<T>::kVec;
+    constexpr int V = Elem<TI>::kVec;
     const int64_t chunks = tokens * (width / V);
     if (fast && width % V == 0 && chunks < ((int64_t)1 << 31)) {
         const int64_t blocks = ceil_div(chunks, kBlock * kUnroll);
-        hipLaunchKernelGGL((swiglu_fast<T>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
-                           (T *)out, (const T *)gate, (const T *)up, (uint32_t)chunks,
+        hipLaunchKernelGGL((swiglu_fast<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0,
+                           stream, (TO *)out, (const TI *)gate, (const TI *)up, (uint32_t)chunks,
                            make_fastdiv((uint32_t)(width / V)), ld_gate, ld_up, ld_out);
     } else {
         const int64_t blocks = std::min<int64_t>(ceil_div(tokens * width, kBlock), 1 << 20);
-        hipLaunchKernelGGL((swiglu_general<T>), dim3((uint32_t)blocks), dim3(kBlock), 0, stream,
-                           (T *)out, (const T *)gate, (const T *)up, tokens, width, ld_gate, ld_up,
-                           ld_out);
+        hipLaunchKernelGGL((swiglu_general<TI, TO>), dim3((uint32_t)blocks), dim3(kBlock), 0,
+                           stream, (TO *)out, (const TI *)gate, (const TI *)up, tokens, width,
+                           ld_gate, ld_up, ld_out);
     }
     return launch_status();
 }
@@ -88,26 +91,34 @@ using namespace qdc;
 
 extern "C" int32_t qdc_swiglu(void *out, const void *gate, const void *up, int64_t tokens,
                               int64_t width, int64_t ld_gate, int64_t ld_up, int64_t ld_out,
-                              int32_t dtype, hipStream_t stream) {
-    if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
+                              int32_t dtype, int32_t out_dtype, hipStream_t stream) {
+    // out in dtype, or fp32 gate and up with the split output
+    const bool split = dtype == QDC_F32 && out_dtype == QDC_BF16X2;
+    if (!valid_dtype(dtype) || !(out_dtype == dtype || split)) return QDC_ERR_DTYPE;
     if (tokens < 0 || width < 0) return QDC_ERR_SHAPE;
     if (tokens == 0 || width == 0) return QDC_OK;
     if (!out || !gate || !up) return QDC_ERR_NULL;
     if (ld_gate < width || ld_up < width || ld_out < width) return QDC_ERR_SHAPE;
     if (width >= ((int64_t)1 << 31)) return QDC_ERR_SHAPE;
-    const int64_t es = elem_size(dtype);
-    const int64_t span_o = ((tokens - 1) * ld_out + width) * es;
-    // In place is allowed only element-for-element (same base and stride).
-    if (!(out == gate && ld_out == ld_gate) &&
+    if (split && !split_rows_ok(width, ld_out)) return QDC_ERR_SHAPE;
+    const int64_t es = elem_size(dtype), eo = elem_size(out_dtype);
+    const int64_t span_o = ((tokens - 1) * ld_out + width) * eo;
+    // In place is allowed only element-for-element (same base, stride and type).
+    if (!(out == gate && ld_out == ld_gate && !split) &&
         overlaps(out, span_o, gate, ((tokens - 1) * ld_gate + width) * es))
         return QDC_ERR_ALIAS;
-    if (!(out == up && ld_out == ld_up) &&
+    if (!(out == up && ld_out == ld_up && !split) &&
         overlaps(out, span_o, up, ((tokens - 1) * ld_up + width) * es))
         return QDC_ERR_ALIAS;
     const bool fast = aligned16(out) && aligned16(gate) && aligned16(up) &&
                       (ld_gate * es) % 16 == 0 && (ld_up * es) % 16 == 0 &&
-                      (ld_out * es) % 16 == 0;
+                      (ld_out * eo) % 16 == 0;
+    if (split)
+        return launch<float, split_t>(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, fast,
+                                      stream);
     if (dtype == QDC_BF16)
-        return launch<bf16_t>(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, fast, stream);
-    return launch<float>(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, fast, stream);
+        return launch<bf16_t, bf16_t>(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, fast,
+                                      stream);
+    return launch<float, float>(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, fast,
+                                stream);
 }

@@ -34,6 +34,7 @@ import Libdl
 
 const QDC_F32 = Int32(0)
 const QDC_BF16 = Int32(1)
+const QDC_BF16X2 = Int32(2)  # output only: two bf16 terms per fp32 value
 
 # ---------------------------------------------------------------- library --
 # Loaded on first use, as src/cpu_mkl.jl:18-66 loads MKL: a missing library is
@@ -169,17 +170,18 @@ qdc_rope_tables(cos_table, sin_table, n_pos, rotary_dim, theta) =
           cos_table, sin_table, n_pos, rotary_dim, theta)
 
 qdc_gated_rmsnorm(out, x, z, weight, tokens, heads, width, x_tok, z_tok, out_tok, eps, dtype,
-                  stream) =
+                  out_dtype, stream) =
     ccall(qdc_sym(:qdc_gated_rmsnorm), Int32,
           (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64,
-           Int64, Float32, Int32, Ptr{Cvoid}),
-          out, x, z, weight, tokens, heads, width, x_tok, z_tok, out_tok, eps, dtype, stream)
+           Int64, Float32, Int32, Int32, Ptr{Cvoid}),
+          out, x, z, weight, tokens, heads, width, x_tok, z_tok, out_tok, eps, dtype, out_dtype,
+          stream)
 
-qdc_swiglu(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, dtype, stream) =
+qdc_swiglu(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, dtype, out_dtype, stream) =
     ccall(qdc_sym(:qdc_swiglu), Int32,
-          (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64, Int32,
+          (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64, Int32, Int32,
            Ptr{Cvoid}),
-          out, gate, up, tokens, width, ld_gate, ld_up, ld_out, dtype, stream)
+          out, gate, up, tokens, width, ld_gate, ld_up, ld_out, dtype, out_dtype, stream)
 
 qdc_delta_scan(out, out_dtype, q, k, v, beta, decay, batch, seq, heads, key_heads, key_dim,
                value_dim, stream) =
@@ -286,7 +288,8 @@ function QwenDecisionCore.native_mlp(mlp::PackedMLP, x::AMDGPU.ROCArray{Float32,
     width, tokens = size(projected, 1) ÷ 2, size(x, 2)
     gated = scratch(Float32, (width, tokens))
     qdc_check(qdc_swiglu(qdc_ptr(gated), qdc_ptr(projected), qdc_ptr(projected) + 4width, tokens,
-                         width, 2width, 2width, width, QDC_F32, qdc_stream()), "native_mlp")
+                         width, 2width, 2width, width, QDC_F32, QDC_F32, qdc_stream()),
+              "native_mlp")
     return QwenDecisionCore.native_linear(mlp.down, gated)
 end
 
@@ -370,7 +373,7 @@ function amdgpu_delta_attention(attention, x::AMDGPU.ROCArray{Float32,2,ROCBuffe
     gated = scratch(Float32, (vd * vh, tokens))
     qdc_check(qdc_gated_rmsnorm(qdc_ptr(gated), qdc_ptr(result), qdc_ptr(projected) + 4qkv_width,
                                 qdc_ptr(attention.norm), tokens, vh, vd, vd * vh, ld, vd * vh,
-                                Float32(cfg.eps), QDC_F32, qdc_stream()), "gated_rms")
+                                Float32(cfg.eps), QDC_F32, QDC_F32, qdc_stream()), "gated_rms")
     return QwenDecisionCore.native_linear(attention.out, gated)
 end
 

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libqdc_hip.so")
 
 QDC_F32 = 0
 QDC_BF16 = 1
+QDC_BF16X2 = 2  # output only: two bf16 terms per fp32 value
 
 STATUS = {0: "QDC_OK", -1: "QDC_ERR_NULL", -2: "QDC_ERR_SHAPE", -3: "QDC_ERR_DTYPE",
           -4: "QDC_ERR_RANGE", -5: "QDC_ERR_ALIAS"}
@@ -45,8 +46,8 @@ SIGNATURES = {
     "qdc_attention_prepare": (_i32, [_vp] * 10 + [_i64] * 12 + [_f32, _i32, _vp]),
     "qdc_rope_tables": (_i32, [_vp, _vp, _i64, _i64, _f32]),
     "qdc_gated_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
-                                 _i32, _vp]),
-    "qdc_swiglu": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _vp]),
+                                 _i32, _i32, _vp]),
+    "qdc_swiglu": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     "qdc_delta_scan": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                               _i64, _vp]),
     "qdc_delta_prologue": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _vp,

@@ -27,6 +27,18 @@ and SwiGLU reading the packed gate||up GEMM output.  GEMMs and the two attention
 products run through PyTorch-ROCm (hipBLASLt), with fp32 results; attention
 scores and probabilities are fp32 (probabilities stored in the model dtype for
 the PV product).
+
+``split_gemm_inputs=True`` (or ``"all"``; bf16 models) stores every GEMM input
+-- the normalised rows, the SwiGLU output, the merged attention output and the
+gated norm output -- in the split two-term bf16 form written by the kernels
+that produce them (``ops.BF16X2``), against projection weights whose input rows
+are repeated in the same pattern (``ops.split_weight``): the GEMMs stay bf16 x
+bf16 with fp32 accumulation and twice the inner dimension, while their inputs
+keep about 16 significant bits.  The MLP gate/up projection then writes fp32
+for SwiGLU; the attention and DeltaNet projections, q/k, the probabilities and
+the recurrence output stay bf16.  ``split_gemm_inputs="mlp"`` splits only the
+two MLP inputs (the post-attention norm and the SwiGLU output), where bf16
+rounding is amplified most, and leaves the other GEMMs at their bf16 size.
 """
 from __future__ import annotations
 
@@ -43,12 +55,25 @@ class QwenBackbone:
     """A Qwen3.5 hybrid backbone resident on one GPU."""
 
     def __init__(self, cfg: BackboneConfig, weights: dict, device="cuda:0",
-                 dtype: torch.dtype = torch.float32):
+                 dtype: torch.dtype = torch.float32, split_gemm_inputs=False):
         """``dtype`` is the storage type of weights and GEMM activations; the
-        residual stream and the returned hidden states are fp32 either way."""
+        residual stream and the returned hidden states are fp32 either way.
+        ``split_gemm_inputs`` (bfloat16 only: False, True / ``"all"``, or
+        ``"mlp"``) selects the split GEMM inputs described in the module
+        docstring."""
         if dtype not in (torch.float32, torch.bfloat16):
             raise ValueError("dtype must be float32 or bfloat16")
+        modes = {False: None, None: None, "none": None, True: "all", "all": "all", "mlp": "mlp"}
+        if split_gemm_inputs not in modes:
+            raise ValueError("split_gemm_inputs must be False, True, 'all' or 'mlp'")
+        self.split = modes[split_gemm_inputs]
+        if self.split and dtype != torch.bfloat16:
+            raise ValueError("split GEMM inputs are a bfloat16 mode")
         self.cfg, self.dtype = cfg, dtype
+        # out_dtype of the kernels that write GEMM inputs: the MLP's two inputs,
+        # and every other GEMM input
+        self.mlp_in = ops.BF16X2 if self.split else None
+        self.gemm_in = ops.BF16X2 if self.split == "all" else None
         self.device = torch.device(device)
         self._tables = {}
 
@@ -56,12 +81,16 @@ class QwenBackbone:
             t = x if isinstance(x, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(x))
             return t.to(self.device).to(dt or dtype).contiguous()
 
-        def lin(*names, pad_to=1):  # packed, transposed [in, out] for y = x @ W
+        def gemm_weight(w, split):  # [out, in] -> [in, out] (input rows repeated when split)
+            w = w.t().contiguous()
+            return ops.split_weight(w) if split else w
+
+        def lin(*names, pad_to=1, mlp=False):  # packed, transposed [in, out] for y = x @ W
             w = torch.cat([dev(weights[n]) for n in names], 0)
             extra = -w.shape[0] % pad_to
             if extra:  # zero output columns: the GEMM runs a tile-aligned width
                 w = torch.cat([w, w.new_zeros((extra, w.shape[1]))], 0)
-            return w.t().contiguous()
+            return gemm_weight(w, self.mlp_in if mlp else self.gemm_in)
 
         self.embedding = dev(weights["embed_tokens.weight"])
         # the last residual add is fused with the final norm, which writes fp32
@@ -73,8 +102,8 @@ class QwenBackbone:
                 "kind": kind,
                 "input_norm": dev(weights[p + "input_layernorm.weight"]),
                 "post_norm": dev(weights[p + "post_attention_layernorm.weight"]),
-                "gate_up": lin(p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"),
-                "down": lin(p + "mlp.down_proj.weight"),
+                "gate_up": lin(p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight", mlp=True),
+                "down": lin(p + "mlp.down_proj.weight", mlp=True),
             }
             if kind == "full_attention":
                 a = p + "self_attn."
@@ -84,10 +113,11 @@ class QwenBackbone:
                 # and the gate merge reads the gate block whole
                 hd, H = cfg.head_dim, cfg.heads
                 qg = dev(weights[a + "q_proj.weight"]).reshape(H, 2, hd, -1)
-                layer.update(qkv=torch.cat([qg[:, 0].reshape(H * hd, -1),
-                                            dev(weights[a + "k_proj.weight"]),
-                                            dev(weights[a + "v_proj.weight"]),
-                                            qg[:, 1].reshape(H * hd, -1)], 0).t().contiguous(),
+                layer.update(qkv=gemm_weight(torch.cat([qg[:, 0].reshape(H * hd, -1),
+                                                        dev(weights[a + "k_proj.weight"]),
+                                                        dev(weights[a + "v_proj.weight"]),
+                                                        qg[:, 1].reshape(H * hd, -1)], 0),
+                                             self.gemm_in),
                              out=lin(a + "o_proj.weight"), q_norm=dev(weights[a + "q_norm.weight"]),
                              k_norm=dev(weights[a + "k_norm.weight"]))
             elif kind == "linear_attention":
@@ -115,12 +145,14 @@ class QwenBackbone:
 
     @classmethod
     def from_weights(cls, weights: dict, cfg: BackboneConfig, device="cuda:0",
-                     dtype: torch.dtype = torch.float32) -> "QwenBackbone":
-        return cls(cfg, weights, device, dtype)
+                     dtype: torch.dtype = torch.float32,
+                     split_gemm_inputs: bool = False) -> "QwenBackbone":
+        return cls(cfg, weights, device, dtype, split_gemm_inputs)
 
     @classmethod
     def from_directory(cls, directory: str, device="cuda:0",
-                       dtype: torch.dtype = torch.float32) -> "QwenBackbone":
+                       dtype: torch.dtype = torch.float32,
+                       split_gemm_inputs: bool = False) -> "QwenBackbone":
         """A local safetensors checkpoint directory (no network access).  Tensors
         load straight onto ``device`` in their stored dtype; with ``dtype=bfloat16``
         a BF16 checkpoint is never widened to fp32 (the packed projection weights
@@ -130,7 +162,7 @@ class QwenBackbone:
         cfg = BackboneConfig(**{**cfg.as_dict(), "vocab": weights["embed_tokens.weight"].shape[0],
                                 "intermediate": weights["layers.0.mlp.gate_proj.weight"].shape[0],
                                 "layer_types": cfg.layer_types})
-        return cls(cfg, weights, device, dtype)
+        return cls(cfg, weights, device, dtype, split_gemm_inputs)
 
     def _mm(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         """A projection whose result feeds a row kernel, in the model dtype."""
@@ -178,7 +210,8 @@ class QwenBackbone:
         # fp32 (a bf16 table widens exactly) and its normalised rows in one pass
         h, normed = ops.native_gather_rms(self.embedding, ids.reshape(-1).contiguous(),
                                           self.layers[0]["input_norm"], cfg.eps,
-                                          token_mask=delta_keep(0), error_flag=error_flag)
+                                          token_mask=delta_keep(0), error_flag=error_flag,
+                                          normed_dtype=self.gemm_in)
         for i, layer in enumerate(self.layers):
             if layer["kind"] == "full_attention":
                 mixed = self._full_attention(layer, normed, mask32, B, S)
@@ -188,15 +221,20 @@ class QwenBackbone:
             if last and last_only:  # the MLP and the final norm of the last rows only
                 h = h.view(B, S, -1)[:, -1].contiguous()
                 mixed = mixed.view(B, S, -1)[:, -1].contiguous()
-            residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps)
-            gate_up = self._mm(normed, layer["gate_up"])
+            residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps,
+                                                       out_dtype=self.mlp_in)
+            # split inputs: fp32 gate/up for SwiGLU (bf16 there costs ~6x the
+            # end-to-end error of the whole split pipeline)
+            gate_up = (self._mm32 if self.split else self._mm)(normed, layer["gate_up"])
             inter = gate_up.shape[1] // 2
-            act = ops.native_mlp_gate(gate_up[:, :inter], gate_up[:, inter:])
+            act = ops.native_mlp_gate(gate_up[:, :inter], gate_up[:, inter:],
+                                      out_dtype=self.mlp_in)
             down = self._mm32(act, layer["down"])
             nxt = self.final_norm if last else self.layers[i + 1]["input_norm"]
             # residual add of the MLP fused with the next RMSNorm
             h, normed = ops.native_residual_rms(residual, down, nxt, cfg.eps,
-                                                token_mask=None if last else delta_keep(i + 1))
+                                                token_mask=None if last else delta_keep(i + 1),
+                                                out_dtype=None if last else self.gemm_in)
         return normed
 
     def _full_attention(self, layer, x, mask32, B, S):
@@ -226,7 +264,8 @@ class QwenBackbone:
                                       out=scores.view(B, H, S, S) if self.dtype == torch.float32
                                       else None)
         values = self._bmm32(probs.view(B * KV, G * S, S), v.view(B * KV, S, hd))  # [B, H, S, hd]
-        merged = ops.attention_gate(values.view(B, H, S, hd), gate, out_dtype=self.dtype)
+        merged = ops.attention_gate(values.view(B, H, S, hd), gate,
+                                    out_dtype=self.gemm_in or self.dtype)
         return self._mm32(merged, layer["out"])
 
     def _bmm32(self, a, b):
@@ -254,8 +293,9 @@ class QwenBackbone:
         # recurrence straight into the model dtype the gated norm reads
         result = ops.delta_scan(q, k, v, beta, decay, self.dtype)
         z = proj[:, cq:cq + vw].view(T, vh, vd)
-        out = ops.native_gated_rms(result.view(T, vh, vd), z, layer["norm"], cfg.eps)
-        return self._mm32(out.view(T, vw), layer["out"])
+        out = ops.native_gated_rms(result.view(T, vh, vd), z, layer["norm"], cfg.eps,
+                                   out_dtype=self.gemm_in)
+        return self._mm32(out.view(T, -1), layer["out"])
 
 
 # ---------------------------------------------------------------- API -------

@@ -15,7 +15,12 @@ path (the generic functions the AMDGPU extension overrides):
 ==========================  ====================================================
 
 Tensors are row-major ``[rows, width]`` (the reference's column-major
-``(width, rows)``).  Every call enqueues one kernel of ``libqdc_hip.so`` on the
+``(width, rows)``).  The producers of GEMM inputs (the norms, SwiGLU and the
+attention gate merge) also write the split two-term bf16 form, ``out_dtype=BF16X2``:
+each fp32 result ``v`` as ``hi = bf16(v)`` and ``lo = bf16(v - hi)``, every aligned
+group of 4 elements a 16-byte piece ``[4 hi | 4 lo]``, so a ``[rows, K]`` result
+is a bf16 tensor ``[rows, 2K]``; :func:`split_weight` repeats a GEMM weight's rows
+in the same pattern and :func:`join_split` reads ``hi + lo`` back.  Every call enqueues one kernel of ``libqdc_hip.so`` on the
 tensor device's current PyTorch stream; torch supplies device memory and the
 stream only.  dtype is float32 or bfloat16 (fp32 arithmetic either way).
 Argument errors raise ``ValueError`` before anything is enqueued, as the
@@ -34,6 +39,33 @@ from . import _lib
 from ._lib import check, lib
 
 _DTYPES = {torch.float32: _lib.QDC_F32, torch.bfloat16: _lib.QDC_BF16}
+BF16X2 = "bf16x2"  # out_dtype of the split two-term bf16 form
+
+
+def _is_split(out_dtype) -> bool:
+    if isinstance(out_dtype, str):
+        if out_dtype != BF16X2:
+            raise ValueError(f"unknown out_dtype {out_dtype!r}; expected a torch dtype or BF16X2")
+        return True
+    return False
+
+
+def split_weight(weight: torch.Tensor) -> torch.Tensor:
+    """A GEMM weight ``[K, N]`` (``y = x @ weight``) as ``[2K, N]`` for split
+    inputs: rows ``8g + j`` and ``8g + 4 + j`` both hold row ``4g + j``, so
+    ``x2 @ split_weight(w)`` = ``(hi + lo) @ w`` for the split form ``x2`` of ``x``."""
+    K, N = weight.shape
+    if K % 4:
+        raise ValueError("the split form needs a multiple of 4 input rows")
+    return weight.reshape(K // 4, 1, 4, N).expand(K // 4, 2, 4, N).reshape(2 * K, N).contiguous()
+
+
+def join_split(x: torch.Tensor) -> torch.Tensor:
+    """fp32 ``hi + lo`` of a split tensor (bf16, last axis ``2K``) -> ``[..., K]``."""
+    if x.dtype != torch.bfloat16 or x.shape[-1] % 8:
+        raise ValueError("a split tensor is bf16 with a last axis of whole 8-value pieces")
+    g = x.reshape(*x.shape[:-1], x.shape[-1] // 8, 2, 4).float()
+    return (g[..., 0, :] + g[..., 1, :]).reshape(*x.shape[:-1], x.shape[-1] // 2)
 
 
 def _dtype_code(*tensors) -> int:
@@ -123,12 +155,14 @@ def native_gather(embedding: torch.Tensor, ids, out: torch.Tensor | None = None,
 def native_gather_rms(embedding: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor,
                       eps: float, token_mask: torch.Tensor | None = None,
                       error_flag: torch.Tensor | None = None, hidden: torch.Tensor | None = None,
-                      normed: torch.Tensor | None = None):
+                      normed: torch.Tensor | None = None, normed_dtype=None):
     """The gather fused with the first layer's input norm: returns ``(hidden,
     normed)``, ``hidden [n, width]`` fp32 = the gathered rows (the residual
-    stream) and ``normed`` = their zero-centred RMSNorm in the weight's dtype,
-    times ``token_mask`` when given.  ``ids`` a contiguous device int32 vector;
-    an id outside the vocabulary gives zero rows and sets ``error_flag``."""
+    stream) and ``normed`` = their zero-centred RMSNorm in the weight's dtype
+    (or, with ``normed_dtype=BF16X2`` and a bf16 weight, the split form
+    ``[n, 2*width]``), times ``token_mask`` when given.  ``ids`` a contiguous
+    device int32 vector; an id outside the vocabulary gives zero rows and sets
+    ``error_flag``."""
     _device(embedding, ids, weight)
     if ids.dtype != torch.int32 or not ids.is_contiguous() or ids.dim() != 1:
         raise ValueError("ids must be a contiguous int32 device vector")
@@ -138,16 +172,21 @@ def native_gather_rms(embedding: torch.Tensor, ids: torch.Tensor, weight: torch.
     if weight.dtype not in _DTYPES or weight.numel() != width or not weight.is_contiguous():
         raise ValueError("weight must be a contiguous float32/bfloat16 vector of the row width")
     n = ids.numel()
+    split = _is_split(normed_dtype)
+    if split and weight.dtype != torch.bfloat16:
+        raise ValueError("the split output takes a bfloat16 weight")
+    nshape = (n, 2 * width) if split else (n, width)
     if hidden is None:
         hidden = torch.empty((n, width), dtype=torch.float32, device=embedding.device)
     if normed is None:
-        normed = torch.empty((n, width), dtype=weight.dtype, device=embedding.device)
+        normed = torch.empty(nshape, dtype=weight.dtype, device=embedding.device)
     _device(embedding, hidden, normed)
     if (hidden.dtype != torch.float32 or hidden.shape != (n, width)
             or not hidden.is_contiguous()):
         raise ValueError("hidden must be a contiguous float32 [n_ids, width] tensor")
-    if normed.dtype != weight.dtype or normed.shape != (n, width) or not normed.is_contiguous():
-        raise ValueError("normed must be a contiguous [n_ids, width] tensor of the weight's dtype")
+    if normed.dtype != weight.dtype or normed.shape != nshape or not normed.is_contiguous():
+        raise ValueError("normed must be a contiguous [n_ids, width] tensor of the weight's dtype "
+                         "([n_ids, 2*width] bfloat16 for the split form)")
     keep = _row_mask(token_mask, n, embedding)
     flag = 0
     if error_flag is not None:
@@ -158,7 +197,7 @@ def native_gather_rms(embedding: torch.Tensor, ids: torch.Tensor, weight: torch.
     check(lib().qdc_embedding_gather_rmsnorm(hidden.data_ptr(), normed.data_ptr(),
                                              embedding.data_ptr(), _DTYPES[embedding.dtype],
                                              ids.data_ptr(), weight.data_ptr(),
-                                             _DTYPES[weight.dtype],
+                                             _lib.QDC_BF16X2 if split else _DTYPES[weight.dtype],
                                              0 if keep is None else keep.data_ptr(), n, vocab,
                                              width, eps, flag, _stream(embedding)),
           "native_gather_rms")
@@ -179,11 +218,13 @@ def _row_mask(token_mask: torch.Tensor | None, rows: int, like: torch.Tensor):
 
 def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool = True,
                out: torch.Tensor | None = None,
-               token_mask: torch.Tensor | None = None) -> torch.Tensor:
+               token_mask: torch.Tensor | None = None, out_dtype=None) -> torch.Tensor:
     """RMSNorm over the last axis: ``(x*s)*(1+w)`` (centred) or ``(x*s)*w``.
 
     The output takes the weight's dtype, so an fp32 ``x`` with a bf16 weight
-    gives a bf16 result (an fp32 residual stream feeding bf16 GEMMs).  With a
+    gives a bf16 result (an fp32 residual stream feeding bf16 GEMMs);
+    ``out_dtype=BF16X2`` (fp32 ``x``, bf16 weight) writes the split form, a
+    bf16 tensor with a last axis of ``2*width``.  With a
     ``token_mask`` (device int32, one 0/1 entry per row) each output row is
     multiplied by its entry before rounding: the DeltaNet input mask of
     ``src/backbone.jl:286`` fused into the norm that produces that input."""
@@ -193,33 +234,43 @@ def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool
     rows, width, ld_x = _rows_view(x)
     if weight.numel() != width or not weight.is_contiguous():
         raise ValueError("weight must be a contiguous vector of the row width")
+    split = _is_split(out_dtype)
+    if split and (x.dtype != torch.float32 or weight.dtype != torch.bfloat16):
+        raise ValueError("the split output takes float32 rows and a bfloat16 weight")
+    oshape = x.shape[:-1] + (2 * width,) if split else x.shape
     if out is None:
-        out = torch.empty(x.shape, dtype=weight.dtype, device=x.device)
+        out = torch.empty(oshape, dtype=weight.dtype, device=x.device)
     _device(x, out)
-    if out.shape != x.shape or out.dtype != weight.dtype:
-        raise ValueError("out must have the shape of x and the dtype of weight")
+    if out.shape != oshape or out.dtype != weight.dtype:
+        raise ValueError("out must have the shape of x and the dtype of weight (the split "
+                         "form: bfloat16, last axis 2*width)")
     _, _, ld_out = _rows_view(out)
+    if split:
+        ld_out //= 2  # the C ABI counts split elements
+    code = _lib.QDC_BF16X2 if split else _DTYPES[weight.dtype]
     keep = _row_mask(token_mask, rows, x)
     if keep is None:
         check(lib().qdc_rmsnorm(out.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, width,
                                 ld_x, ld_out, eps, int(bool(centered)), _DTYPES[x.dtype],
-                                _DTYPES[weight.dtype], _stream(x)), "native_rms")
+                                code, _stream(x)), "native_rms")
     else:
         check(lib().qdc_rmsnorm_masked(out.data_ptr(), x.data_ptr(), weight.data_ptr(),
                                        keep.data_ptr(), rows, width, ld_x, ld_out, eps,
                                        int(bool(centered)), _DTYPES[x.dtype],
-                                       _DTYPES[weight.dtype], _stream(x)), "native_rms")
+                                       code, _stream(x)), "native_rms")
     return out
 
 
 def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tensor, eps: float,
                         residual: torch.Tensor | None = None,
                         out: torch.Tensor | None = None,
-                        token_mask: torch.Tensor | None = None):
+                        token_mask: torch.Tensor | None = None, out_dtype=None):
     """``residual = x + mixed``; returns ``(residual, rms(residual))`` in one pass.
 
     ``residual`` has x's dtype, the normalised output the weight's dtype;
-    ``mixed`` may be bf16 while x is fp32 (fp32 residual stream).  A
+    ``mixed`` may be bf16 while x is fp32 (fp32 residual stream).
+    ``out_dtype=BF16X2`` (fp32 ``x`` and ``mixed``, bf16 weight) writes the
+    normalised rows in the split form (last axis ``2*width``).  A
     ``token_mask`` masks the normalised rows as in ``native_rms``; the residual
     is never masked."""
     _device(x, mixed, weight)
@@ -232,35 +283,43 @@ def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tens
     rows = x.numel() // width if width else 0
     if weight.numel() != width:
         raise ValueError("weight must be a vector of the row width")
+    split = _is_split(out_dtype)
+    if split and (x.dtype != torch.float32 or mixed.dtype != torch.float32
+                  or weight.dtype != torch.bfloat16):
+        raise ValueError("the split output takes float32 x and mixed and a bfloat16 weight")
+    oshape = x.shape[:-1] + (2 * width,) if split else x.shape
     residual = torch.empty_like(x) if residual is None else residual
-    out = torch.empty(x.shape, dtype=weight.dtype, device=x.device) if out is None else out
+    out = torch.empty(oshape, dtype=weight.dtype, device=x.device) if out is None else out
     _device(x, residual, out)
     if residual.shape != x.shape or not residual.is_contiguous() or residual.dtype != x.dtype:
         raise ValueError("residual must be a contiguous tensor like x")
-    if out.shape != x.shape or not out.is_contiguous() or out.dtype != weight.dtype:
-        raise ValueError("out must be contiguous, shaped like x, of the weight's dtype")
+    if out.shape != oshape or not out.is_contiguous() or out.dtype != weight.dtype:
+        raise ValueError("out must be contiguous, shaped like x, of the weight's dtype (the "
+                         "split form: bfloat16, last axis 2*width)")
+    code = _lib.QDC_BF16X2 if split else _DTYPES[weight.dtype]
     keep = _row_mask(token_mask, rows, x)
     if keep is None:
         check(lib().qdc_residual_rmsnorm(residual.data_ptr(), out.data_ptr(), x.data_ptr(),
                                          mixed.data_ptr(), weight.data_ptr(), rows, width, eps,
-                                         _DTYPES[x.dtype], _DTYPES[mixed.dtype],
-                                         _DTYPES[weight.dtype], _stream(x)), "native_residual_rms")
+                                         _DTYPES[x.dtype], _DTYPES[mixed.dtype], code,
+                                         _stream(x)), "native_residual_rms")
     else:
         check(lib().qdc_residual_rmsnorm_masked(residual.data_ptr(), out.data_ptr(), x.data_ptr(),
                                                 mixed.data_ptr(), weight.data_ptr(),
                                                 keep.data_ptr(), rows, width, eps,
-                                                _DTYPES[x.dtype], _DTYPES[mixed.dtype],
-                                                _DTYPES[weight.dtype], _stream(x)),
+                                                _DTYPES[x.dtype], _DTYPES[mixed.dtype], code,
+                                                _stream(x)),
               "native_residual_rms")
     return residual, out
 
 
 def native_gated_rms(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None, out_dtype=None) -> torch.Tensor:
     """``((x*s)*w)*silu(z)`` per ``[tokens, heads, width]`` row, not centred.
 
     ``z`` may be a strided view (heads contiguous inside each token), e.g. the
-    z block of a packed projection."""
+    z block of a packed projection.  ``out_dtype=BF16X2`` (bf16 ``x``, ``z`` and
+    weight) writes the split form ``[tokens, heads, 2*width]``."""
     _device(x, z, weight)
     code = _dtype_code(x, z, weight)
     if x.dim() != 3 or z.shape != x.shape:
@@ -269,17 +328,25 @@ def native_gated_rms(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps
     for t in (x, z):
         if t.stride(2) != 1 or (heads > 1 and t.stride(1) != width):
             raise ValueError("heads must be contiguous within a token")
+    split = _is_split(out_dtype)
+    if split and x.dtype != torch.bfloat16:
+        raise ValueError("the split output takes bfloat16 x, z and weight")
+    ow = 2 * width if split else width
     if out is None:
-        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        out = torch.empty((tokens, heads, ow), dtype=x.dtype, device=x.device)
     _device(x, out)
     if out.dtype != x.dtype:
         raise ValueError(f"out must have the dtype of x ({x.dtype}), got {out.dtype}")
-    if out.shape != x.shape or out.stride(2) != 1 or (heads > 1 and out.stride(1) != width):
-        raise ValueError("out must be [tokens, heads, width] with contiguous heads")
-    tok = lambda t: t.stride(0) if tokens > 1 else heads * width  # noqa: E731
+    if out.shape != (tokens, heads, ow) or out.stride(2) != 1 or (
+            heads > 1 and out.stride(1) != ow):
+        raise ValueError("out must be [tokens, heads, width] with contiguous heads "
+                         "([tokens, heads, 2*width] for the split form)")
+    tok = lambda t: t.stride(0) if tokens > 1 else heads * t.shape[2]  # noqa: E731
+    out_tok = tok(out) // 2 if split else tok(out)  # the C ABI counts split elements
     check(lib().qdc_gated_rmsnorm(out.data_ptr(), x.data_ptr(), z.data_ptr(), weight.data_ptr(),
-                                  tokens, heads, width, tok(x), tok(z), tok(out), eps, code,
-                                  _stream(x)), "native_gated_rms")
+                                  tokens, heads, width, tok(x), tok(z), out_tok, eps, code,
+                                  _lib.QDC_BF16X2 if split else code, _stream(x)),
+          "native_gated_rms")
     return out
 
 
@@ -416,12 +483,13 @@ def attention_prepare(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm:
 
 # ----------------------------------------------------------------- SwiGLU ---
 def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, out_dtype=None) -> torch.Tensor:
     """``silu(gate) * up`` on ``[tokens, width]`` views (contiguous rows).
 
     ``native_mlp_gate!`` writes into ``gate``; here ``out=gate`` does the same
     (allowed when the strides agree).  For the packed gate||up GEMM output pass
-    ``packed[:, :I]`` and ``packed[:, I:]``."""
+    ``packed[:, :I]`` and ``packed[:, I:]``.  ``out_dtype=BF16X2`` (fp32 gate
+    and up) writes the split form ``[tokens, 2*width]``."""
     _device(gate, up)
     code = _dtype_code(gate, up)
     if gate.dim() != 2 or up.shape != gate.shape:
@@ -430,16 +498,23 @@ def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
     for t in (gate, up):
         if width > 1 and t.stride(1) != 1:
             raise ValueError("rows must be contiguous")
+    split = _is_split(out_dtype)
+    if split and gate.dtype != torch.float32:
+        raise ValueError("the split output takes float32 gate and up")
+    odt, ow = (torch.bfloat16, 2 * width) if split else (gate.dtype, width)
     if out is None:
-        out = torch.empty((tokens, width), dtype=gate.dtype, device=gate.device)
+        out = torch.empty((tokens, ow), dtype=odt, device=gate.device)
     _device(gate, out)
-    if out.dtype != gate.dtype:
-        raise ValueError(f"out must have the dtype of gate ({gate.dtype}), got {out.dtype}")
-    if out.shape != gate.shape or (width > 1 and out.stride(1) != 1):
-        raise ValueError("out must be [tokens, width] with contiguous rows")
-    ld = lambda t: t.stride(0) if tokens > 1 else width  # noqa: E731
+    if out.dtype != odt:
+        raise ValueError(f"out must be {odt}, got {out.dtype}")
+    if out.shape != (tokens, ow) or (ow > 1 and out.stride(1) != 1):
+        raise ValueError("out must be [tokens, width] with contiguous rows "
+                         "([tokens, 2*width] bfloat16 for the split form)")
+    ld = lambda t: t.stride(0) if tokens > 1 else t.shape[1]  # noqa: E731
+    ld_out = ld(out) // 2 if split else ld(out)  # the C ABI counts split elements
     check(lib().qdc_swiglu(out.data_ptr(), gate.data_ptr(), up.data_ptr(), tokens, width,
-                           ld(gate), ld(up), ld(out), code, _stream(gate)), "native_mlp_gate")
+                           ld(gate), ld(up), ld_out, code, _lib.QDC_BF16X2 if split else code,
+                           _stream(gate)), "native_mlp_gate")
     return out
 
 
@@ -538,21 +613,31 @@ def attention_gate(values: torch.Tensor, gate: torch.Tensor, out_dtype=None,
     """Output-gate merge ``out[t, h*hd + r] = values[b, h, s, r] * sigmoid(gate[t, h, r])``
     for ``t = b*S + s``: ``values`` fp32 ``[B, H, S, hd]`` contiguous (the PV
     product), ``gate`` a ``[B*S, H, hd]`` view with unit element stride (the gate
-    half of the q||gate projection).  Returns ``[B*S, H*hd]``."""
+    half of the q||gate projection).  Returns ``[B*S, H*hd]`` in ``out_dtype``
+    (default: the gate's), or with ``out_dtype=BF16X2`` the split form
+    ``[B*S, 2*H*hd]`` (bf16)."""
     _device(values, gate)
     if values.dtype != torch.float32 or values.dim() != 4 or not values.is_contiguous():
         raise ValueError("values must be a contiguous float32 [B, H, S, hd] tensor")
     B, H, S, hd = values.shape
     if gate.dtype not in _DTYPES or gate.shape != (B * S, H, hd) or gate.stride(2) != 1:
         raise ValueError("gate must be a [B*S, H, hd] view with unit element stride")
+    split = _is_split(out_dtype)
+    odt = torch.bfloat16 if split else (out_dtype or gate.dtype)
+    oshape = (B * S, (2 if split else 1) * H * hd)
     if out is None:
-        out = torch.empty((B * S, H * hd), dtype=out_dtype or gate.dtype, device=values.device)
+        out = torch.empty(oshape, dtype=odt, device=values.device)
     _device(values, out)
-    if out.dtype not in _DTYPES or out.shape != (B * S, H * hd) or out.stride(1) != 1:
-        raise ValueError("out must be [B*S, H*hd] with unit element stride")
-    tok = out.stride(0) if B * S > 1 else H * hd
+    if (out.dtype not in _DTYPES or (split and out.dtype != odt) or out.shape != oshape
+            or out.stride(1) != 1):
+        raise ValueError("out must be [B*S, H*hd] with unit element stride "
+                         "([B*S, 2*H*hd] bfloat16 for the split form)")
+    tok = out.stride(0) if B * S > 1 else oshape[1]
+    if split:
+        tok //= 2  # the C ABI counts split elements
     gtok = gate.stride(0) if B * S > 1 else H * gate.stride(1)
-    check(lib().qdc_attention_gate(out.data_ptr(), _DTYPES[out.dtype], values.data_ptr(),
+    code = _lib.QDC_BF16X2 if split else _DTYPES[out.dtype]
+    check(lib().qdc_attention_gate(out.data_ptr(), code, values.data_ptr(),
                                    gate.data_ptr(), _DTYPES[gate.dtype], B, S, H, hd, gtok,
                                    gate.stride(1) if H > 1 else hd, tok, _stream(values)),
           "attention_gate")

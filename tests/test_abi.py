@@ -15,7 +15,7 @@ from oracle import qdc_oracle as O
 from qdc_amd import _lib
 
 HEADER = os.path.join(ROOT, "include", "qdc_hip.h")
-F32, BF16 = _lib.QDC_F32, _lib.QDC_BF16
+F32, BF16, X2 = _lib.QDC_F32, _lib.QDC_BF16, _lib.QDC_BF16X2
 NULL_S = None
 FAKE = 0x10000  # a non-null, 16-byte aligned address never dereferenced by validation
 
@@ -81,6 +81,13 @@ def test_rmsnorm_validation():
     assert rms(FAKE, FAKE, FAKE, 4, 8, 8, 8, 1e-6, 1, F32, BF16) == -5  # in place, other type
     # up to a wavefront per row in a grid of fewer than 2^32 work-items: rows < 2^26
     assert rms(FAKE, FAKE * 2, FAKE, 1 << 26, 8, 8, 8, 1e-6, 1, F32, F32) == -2
+    assert rms(FAKE, FAKE * 2, FAKE, 4, 8, 8, 8, 1e-6, 1, F32, F32) == -5  # out on the weight
+    # the split output: fp32 rows only, whole groups of 4, never in place
+    assert rms(FAKE, FAKE * 2, FAKE * 3, 4, 8, 8, 8, 1e-6, 1, BF16, X2) == -3
+    assert rms(FAKE, FAKE * 2, FAKE * 3, 4, 6, 6, 6, 1e-6, 1, F32, X2) == -2
+    assert rms(FAKE, FAKE * 2, FAKE * 3, 4, 8, 8, 10, 1e-6, 1, F32, X2) == -2
+    assert rms(FAKE, FAKE, FAKE * 3, 4, 8, 8, 8, 1e-6, 1, F32, X2) == -5
+    assert rms(FAKE, FAKE * 2, FAKE * 3, 0, 8, 8, 8, 1e-6, 1, F32, X2) == 0
 
 
 def test_residual_validation():
@@ -96,6 +103,13 @@ def test_residual_validation():
     assert f(A, B, C, B, W, 4, 8, 1e-6, F32, BF16, F32) == -5  # out on mixed of another type
     assert f(A, B, C, D, W, 0, 8, 1e-6, F32, F32, F32) == 0
     assert f(A, B, C, D, W, 1 << 26, 8, 1e-6, F32, F32, F32) == -2  # rows < 2^26
+    assert f(A, B, C, D, A + 8, 4, 8, 1e-6, F32, F32, F32) == -5  # weight inside residual
+    # the split output: fp32 residual and addend, whole groups of 4, not in place
+    assert f(A, B, C, D, W, 4, 8, 1e-6, F32, BF16, X2) == -3
+    assert f(A, B, C, D, W, 4, 8, 1e-6, BF16, BF16, X2) == -3
+    assert f(A, B, C, D, W, 4, 6, 1e-6, F32, F32, X2) == -2
+    assert f(A, C, C, D, W, 4, 8, 1e-6, F32, F32, X2) == -5  # out on x
+    assert f(A, B, C, D, W, 0, 8, 1e-6, F32, F32, X2) == 0
 
 
 def test_masked_norm_validation():
@@ -121,21 +135,37 @@ def test_masked_norm_validation():
 
 def test_gated_validation():
     lib = _lib.lib()
-    f = lambda *a: lib.qdc_gated_rmsnorm(*a, None)  # noqa: E731
+    g = lambda *a: lib.qdc_gated_rmsnorm(*a, None)  # noqa: E731
+    f = lambda *a: g(*a, a[-1])  # noqa: E731  (out in the input dtype)
     A, X, Z, W = FAKE, FAKE * 2, FAKE * 3, FAKE * 4
     assert f(A, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, 3) == -3
     assert f(A, X, Z, W, 4, 2, 8, 8, 16, 16, 1e-6, F32) == -2  # token stride < heads*width
     assert f(A, X, None, W, 4, 2, 8, 16, 16, 16, 1e-6, F32) == -1
     assert f(Z, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, F32) == -5  # out on z
+    assert f(W, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, F32) == -5  # out on the weight
     assert f(A, X, Z, W, 0, 2, 8, 16, 16, 16, 1e-6, F32) == 0
     assert f(A, X, Z, W, 1 << 25, 2, 8, 16, 16, 16, 1e-6, F32) == -2  # tokens * heads < 2^26
+    # the split output: bf16 inputs only, whole groups of 4 per row
+    assert g(A, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, F32, X2) == -3
+    assert g(A, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, BF16, F32) == -3
+    assert g(A, X, Z, W, 4, 2, 6, 12, 12, 12, 1e-6, BF16, X2) == -2  # width 6
+    assert g(A, X, Z, W, 4, 2, 8, 16, 16, 18, 1e-6, BF16, X2) == -2  # token stride 18
+    assert g(X, X, Z, W, 4, 2, 8, 16, 16, 16, 1e-6, BF16, X2) == -5  # in place, other type
+    assert g(A, X, Z, W, 0, 2, 8, 16, 16, 16, 1e-6, BF16, X2) == 0
 
 
 def test_swiglu_validation():
     lib = _lib.lib()
-    f = lambda *a: lib.qdc_swiglu(*a, None)  # noqa: E731
+    g = lambda *a: lib.qdc_swiglu(*a, None)  # noqa: E731
+    f = lambda *a: g(*a, a[-1])  # noqa: E731  (out in the input dtype)
     O_, G, U = FAKE, FAKE * 2, FAKE * 3
     assert f(O_, G, U, 4, 8, 8, 8, 8, 5) == -3
+    assert g(O_, G, U, 4, 8, 8, 8, 8, F32, BF16) == -3  # no f32 -> bf16
+    assert g(O_, G, U, 4, 8, 8, 8, 8, BF16, X2) == -3  # split output from f32 only
+    assert g(O_, G, U, 4, 6, 6, 6, 6, F32, X2) == -2  # width 6: not whole groups
+    assert g(O_, G, U, 4, 8, 16, 16, 10, F32, X2) == -2  # output stride 10
+    assert g(G, G, U, 4, 8, 8, 8, 8, F32, X2) == -5  # in place, other type
+    assert g(O_, G, U, 0, 8, 8, 8, 8, F32, X2) == 0
     assert f(O_, G, U, 4, 8, 4, 8, 8, F32) == -2
     assert f(O_, None, U, 4, 8, 8, 8, 8, F32) == -1
     assert f(G + 4, G, U, 4, 8, 8, 8, 8, F32) == -5
@@ -327,6 +357,26 @@ def test_attention_gate_validation():
     assert ga(None, F32, None, None, F32, 0, 4, 2, 8, 32, 16, 16) == 0
     assert ga(FAKE + 65536 + 32, F32, FAKE + 65536, FAKE + 131072, F32, 1, 4, 2, 8, 32, 16,
               16) == -5
+    # the split output: whole groups of 4 per (token, head) row
+    assert ga(FAKE, X2, FAKE + 65536, FAKE + 131072, BF16, 1, 4, 2, 6, 24, 12, 12) == -2
+    assert ga(FAKE, X2, FAKE + 65536, FAKE + 131072, BF16, 1, 4, 2, 8, 32, 16, 18) == -2
+    assert ga(None, X2, None, None, BF16, 0, 4, 2, 8, 32, 16, 16) == 0
+
+
+def test_gather_rmsnorm_validation():
+    lib = _lib.lib()
+    # hidden, normed, table, table dtype, ids, weight, normed dtype, mask, n, vocab, width, eps
+    gr = lambda *a: lib.qdc_embedding_gather_rmsnorm(*a, None, None)  # noqa: E731
+    H, N, T, I, W = (FAKE * i for i in range(1, 6))
+    assert gr(H, N, T, 7, I, W, F32, None, 4, 16, 8, 1e-6) == -3
+    assert gr(H, N, T, BF16, I, W, 7, None, 4, 16, 8, 1e-6) == -3
+    assert gr(H, N, T, BF16, None, W, BF16, None, 4, 16, 8, 1e-6) == -1
+    assert gr(H, N, T, BF16, I, W, BF16, None, 4, 0, 8, 1e-6) == -4
+    assert gr(H, H + 32, T, BF16, I, W, BF16, None, 4, 16, 8, 1e-6) == -5
+    assert gr(H, N, T, BF16, I, N + 4, BF16, None, 4, 16, 8, 1e-6) == -5  # weight in normed
+    assert gr(H, N, T, BF16, I, W, X2, None, 4, 16, 6, 1e-6) == -2  # split: width 6
+    assert gr(H, N, T, BF16, I, H + 32, X2, None, 4, 16, 8, 1e-6) == -5
+    assert gr(H, N, T, BF16, I, W, X2, None, 0, 16, 8, 1e-6) == 0
 
 
 def test_copy_validation():

@@ -112,6 +112,33 @@ def _calls():
         ("attention_gate",
          lambda **kw: ops.attention_gate(d(1, 2, 4, 8), d(4, 2, 8, dtype=BF16), **kw),
          [dict(out=host(4, 16, dtype=BF16)), dict(out=d(4, 16, dtype=torch.float16))]),
+        # split two-term bf16 outputs: bf16 buffers with twice the last axis
+        ("native_gather_rms split",
+         lambda **kw: ops.native_gather_rms(d(10, 16, dtype=BF16), d(4, dtype=torch.int32),
+                                            d(16, dtype=BF16), 1e-6, normed_dtype=ops.BF16X2,
+                                            **kw),
+         [dict(normed=d(4, 16, dtype=BF16)), dict(normed=d(4, 32)),
+          dict(normed=host(4, 32, dtype=BF16))]),
+        ("native_rms split",
+         lambda **kw: ops.native_rms(d(8, 64), d(64, dtype=BF16), 1e-6, out_dtype=ops.BF16X2,
+                                     **kw),
+         [dict(out=d(8, 64, dtype=BF16)), dict(out=d(8, 128)), dict(out=host(8, 128, dtype=BF16))]),
+        ("native_residual_rms split",
+         lambda **kw: ops.native_residual_rms(d(8, 64), d(8, 64), d(64, dtype=BF16), 1e-6,
+                                              out_dtype=ops.BF16X2, **kw),
+         [dict(out=d(8, 64, dtype=BF16)), dict(out=d(8, 128)), dict(out=host(8, 128, dtype=BF16))]),
+        ("native_gated_rms split",
+         lambda **kw: ops.native_gated_rms(d(4, 2, 16, dtype=BF16), d(4, 2, 16, dtype=BF16),
+                                           d(16, dtype=BF16), 1e-6, out_dtype=ops.BF16X2, **kw),
+         [dict(out=d(4, 2, 16, dtype=BF16)), dict(out=d(4, 2, 32)),
+          dict(out=host(4, 2, 32, dtype=BF16))]),
+        ("native_mlp_gate split",
+         lambda **kw: ops.native_mlp_gate(d(4, 16), d(4, 16), out_dtype=ops.BF16X2, **kw),
+         [dict(out=d(4, 16, dtype=BF16)), dict(out=d(4, 32)), dict(out=host(4, 32, dtype=BF16))]),
+        ("attention_gate split",
+         lambda **kw: ops.attention_gate(d(1, 2, 4, 8), d(4, 2, 8, dtype=BF16),
+                                         out_dtype=ops.BF16X2, **kw),
+         [dict(out=d(4, 16, dtype=BF16)), dict(out=d(4, 32)), dict(out=host(4, 32, dtype=BF16))]),
     ]
 
 
@@ -129,3 +156,53 @@ def test_host_tensors_rejected(no_launch):
         ops.native_rms(host(8, 64), host(64), 1e-6)
     with pytest.raises(ValueError):
         ops.native_mlp_gate(d(4, 16), host(4, 16))
+
+
+def test_split_argument_checks(no_launch):
+    """The split output takes the input types its kernels implement; anything
+    else raises before the library is reached."""
+    X2 = ops.BF16X2
+    with pytest.raises(ValueError, match="unknown out_dtype"):
+        ops.native_rms(d(8, 64), d(64, dtype=BF16), 1e-6, out_dtype="bf16x3")
+    with pytest.raises(ValueError):
+        ops.native_rms(d(8, 64), d(64), 1e-6, out_dtype=X2)                # fp32 weight
+    with pytest.raises(ValueError):
+        ops.native_rms(d(8, 64, dtype=BF16), d(64, dtype=BF16), 1e-6, out_dtype=X2)
+    with pytest.raises(ValueError):
+        ops.native_residual_rms(d(8, 64), d(8, 64, dtype=BF16), d(64, dtype=BF16), 1e-6,
+                                out_dtype=X2)                              # bf16 addend
+    with pytest.raises(ValueError):
+        ops.native_gated_rms(d(4, 2, 16), d(4, 2, 16), d(16), 1e-6, out_dtype=X2)
+    with pytest.raises(ValueError):
+        ops.native_mlp_gate(d(4, 16, dtype=BF16), d(4, 16, dtype=BF16), out_dtype=X2)
+    with pytest.raises(ValueError):
+        ops.native_gather_rms(d(10, 16, dtype=BF16), d(4, dtype=torch.int32), d(16), 1e-6,
+                              normed_dtype=X2)                             # fp32 weight
+
+
+def test_split_weight_and_join_on_cpu():
+    """split_weight repeats each input row into its hi and lo slots, and
+    join_split adds the two terms back, on plain CPU tensors."""
+    w = torch.arange(8 * 3, dtype=torch.float32).reshape(8, 3).to(BF16)
+    w2 = ops.split_weight(w)
+    assert w2.shape == (16, 3)
+    for g in range(2):
+        for j in range(4):
+            assert torch.equal(w2[8 * g + j], w[4 * g + j])
+            assert torch.equal(w2[8 * g + 4 + j], w[4 * g + j])
+    with pytest.raises(ValueError):
+        ops.split_weight(torch.zeros(6, 3, dtype=BF16))
+    x = torch.tensor([[1.0, 2.0, 3.0, 4.0, 0.5, 0.25, -1.0, 0.0]], dtype=BF16)
+    assert torch.equal(ops.join_split(x), torch.tensor([[1.5, 2.25, 2.0, 4.0]]))
+    with pytest.raises(ValueError):
+        ops.join_split(torch.zeros(1, 8))
+    # the product identity the layout exists for: [hi | lo] pieces times the
+    # repeated rows equal (hi + lo) times the rows
+    hi = torch.tensor([[1.0, -2.0, 0.5, 3.0, 8.0, 1.0, -1.0, 2.0]]).to(BF16)
+    lo = torch.tensor([[2.0 ** -9, 0.0, -(2.0 ** -12), 2.0 ** -8, 0.0, 2.0 ** -10, 0.0,
+                        -(2.0 ** -9)]]).to(BF16)
+    xs = torch.cat([hi.view(1, 2, 4), lo.view(1, 2, 4)], 2).reshape(1, 16)
+    wk = torch.randn(8, 5).to(BF16)
+    got = xs.float() @ ops.split_weight(wk).float()
+    exp = (hi.float() + lo.float()) @ wk.float()
+    assert torch.allclose(got, exp, rtol=0, atol=1e-6)

@@ -107,6 +107,60 @@ def test_bf16_known_answers():
     assert np.array_equal(O.f32_to_bf16(wide[finite]), allbits[finite])
 
 
+def test_split_bf16_pinned():
+    """The two-term bf16 form (hi = bf16(x), lo = bf16(x - hi)) by its defining
+    properties: a known answer with the piece layout, the unique decomposition
+    of any a + b with bf16 a and |b| below half an ulp of a, the 2^-17 bound,
+    and the non-finite and signed-zero cases."""
+    # 1 + 2^-8 + 2^-12 rounds up to 1 + 2^-7; the rest, -15 * 2^-12, is a bf16 value
+    x = np.float32([1 + 2.0 ** -8 + 2.0 ** -12, 1.0, -3.0, 0.5, 2.0, 0.0, 3 * 2.0 ** -10, -7.25])
+    b = O.split_bf16(x)
+    assert b.shape == (16,)
+    assert b[:4].tolist() == [0x3F81, 0x3F80, 0xC040, 0x3F00]            # hi of elements 0..3
+    assert O.bf16_to_f32(b[4:8]).tolist() == [-15 * 2.0 ** -12, 0.0, 0.0, 0.0]  # their lo
+    assert b[8:12].tolist() == O.f32_to_bf16(x[4:]).tolist()             # hi of elements 4..7
+    assert np.array_equal(O.join_split(b), x)
+    # unique decomposition: a + b (exact in fp32) splits back into (a, b) bit for bit
+    rng = np.random.default_rng(5)
+    n = 200000
+    a = O.round_bf16(rng.standard_normal(n).astype(np.float32) *
+                     np.exp2(rng.integers(-60, 60, n)).astype(np.float32))
+    ulp = np.exp2(np.floor(np.log2(np.abs(a))) - 7).astype(np.float32)
+    # |b| in [2^-8, 0.499] ulps of a: a + b spans at most 24 bits, so it is exact
+    mag = rng.uniform(2.0 ** -8, 0.499, n) * rng.choice([-1.0, 1.0], n)
+    lo = O.round_bf16((mag * ulp).astype(np.float32))
+    # (below a power of two the next binade's half ulp is smaller: keep a off them)
+    keep = np.frexp(a)[0] != np.float32(np.sign(a) * 0.5)
+    a, lo = a[keep], lo[keep]
+    a, lo = a[:len(a) // 8 * 8], lo[:len(a) // 8 * 8]
+    xs = (a + lo).astype(np.float32)
+    assert np.array_equal(xs.astype(np.float64), a.astype(np.float64) + lo.astype(np.float64))
+    g = O.split_bf16(xs.reshape(-1, 8)).reshape(-1, 2, 4)
+    assert np.array_equal(O.bf16_to_f32(g[:, 0]).reshape(-1), a)
+    assert np.array_equal(O.bf16_to_f32(g[:, 1]).reshape(-1), lo)
+    # any normal fp32 value: hi is bf16(x) and |x - (hi + lo)| <= 2^-17 |x| (|x - hi| is
+    # at most half a bf16 ulp, 2^-8 |x|, and lo rounds that rest to 8 bits)
+    y = (rng.standard_normal(n) * np.exp2(rng.integers(-100, 100, n))).astype(np.float32)
+    g = O.split_bf16(y.reshape(-1, 8)).reshape(-1, 2, 4)
+    assert np.array_equal(g[:, 0].reshape(-1), O.f32_to_bf16(y))
+    err = np.abs(O.round_split(y).astype(np.float64) - y) / np.abs(y)
+    assert err.max() <= 2.0 ** -17 and err.max() > 2.0 ** -18
+    # non-finite hi (inf, NaN, FLT_MAX rounding up to inf) gets lo = +0; -0 splits to (-0, +0)
+    sp = np.float32([np.inf, -np.inf, np.nan, np.finfo(np.float32).max, -0.0, 1e-40, 0, 0])
+    with np.errstate(invalid="ignore"):
+        g = O.split_bf16(sp).reshape(2, 2, 4)
+    hi, lo = O.bf16_to_f32(g[:, 0]).reshape(-1), g[:, 1].reshape(-1)
+    assert hi[0] == np.inf and hi[1] == -np.inf and np.isnan(hi[2]) and hi[3] == np.inf
+    assert lo[:4].tolist() == [0, 0, 0, 0]
+    assert g[1, 0, 0] == 0x8000 and lo[4] == 0x0000
+    # a denormal: hi = bf16(x), lo = bf16(x - hi)
+    h5 = O.bf16_to_f32(g[1, 0, 1:2])
+    assert g[1, 0, 1] == O.f32_to_bf16(sp[5:6])[0]
+    assert lo[5] == O.f32_to_bf16((sp[5:6] - h5).astype(np.float32))[0]
+    with pytest.raises(ValueError):
+        O.split_bf16(np.zeros(6, np.float32))
+
+
 def test_transformers_rms(transformers_golden):
     for width in (7, 256, 1024):
         got = O.rms(ramp(np.sin, (17, width)), ramp(np.cos, (width,), 0.1), 1e-6)
