@@ -70,6 +70,12 @@ class QwenBackbone:
         if self.split and dtype != torch.bfloat16:
             raise ValueError("split GEMM inputs are a bfloat16 mode")
         self.cfg, self.dtype = cfg, dtype
+        # a split row holds whole groups of 4 elements
+        widths = {"mlp": (cfg.hidden, cfg.intermediate),
+                  "all": (cfg.hidden, cfg.intermediate, cfg.head_dim, cfg.value_dim)}
+        if self.split and any(w % 4 for w in widths[self.split]):
+            raise ValueError(f"split GEMM inputs ({self.split!r}) need the widths "
+                             f"{widths[self.split]} to be multiples of 4")
         # out_dtype of the kernels that write GEMM inputs: the MLP's two inputs,
         # and every other GEMM input
         self.mlp_in = ops.BF16X2 if self.split else None

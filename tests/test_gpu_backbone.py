@@ -592,3 +592,15 @@ def test_bf16_checkpoint_directory(native_fixture, tmp_path):
     exp = forward.backbone_hidden(weights, native_fixture["cfg"], ids[0], mask[0])
     got = backbone.backbone_hidden(wide, ids[0], mask[0])
     assert normwise(got, exp) <= 1e-5, normwise(got, exp)
+    # split MLP inputs from the same directory: the in-memory split build bit for bit,
+    # within 1e-2 of fp32; every GEMM input split needs widths of whole 4-element
+    # groups, which the fixture's value heads (2 wide) are not
+    split_dir = backbone.QwenBackbone.from_directory(str(tmp_path), "cuda:0", torch.bfloat16,
+                                                     split_gemm_inputs="mlp")
+    a = backbone.backbone_hidden(split_dir, ids[0], mask[0])
+    assert np.array_equal(a, backbone.backbone_hidden(model_for(weights, cfg, torch.bfloat16,
+                                                                split="mlp"), ids[0], mask[0]))
+    assert normwise(a, exp) <= 1e-2
+    with pytest.raises(ValueError, match="multiples of 4"):
+        backbone.QwenBackbone.from_directory(str(tmp_path), "cuda:0", torch.bfloat16,
+                                             split_gemm_inputs=True)

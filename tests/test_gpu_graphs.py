@@ -66,7 +66,7 @@ def _check_replays(model, graphs, cfg, lengths, reps, seed, oracle_weights=None,
           + f"; eager keys {sorted(graphs.eager_keys)}", flush=True)
 
 
-def _synthetic_model(dtype, seed=11):
+def _synthetic_model(dtype, seed=11, split=False):
     from qdc_amd import backbone
     from qdc_amd.config import synthetic_inference_config
     from qdc_amd.weights import random_weights
@@ -75,7 +75,8 @@ def _synthetic_model(dtype, seed=11):
     if dtype == torch.bfloat16:
         from oracle import qdc_oracle as O
         weights = {k: O.round_bf16(v) for k, v in weights.items()}
-    return cfg, weights, backbone.QwenBackbone.from_weights(weights, cfg, "cuda:0", dtype)
+    return cfg, weights, backbone.QwenBackbone.from_weights(weights, cfg, "cuda:0", dtype,
+                                                            split_gemm_inputs=split)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -88,6 +89,21 @@ def test_graph_replays_match_eager(dtype):
     _check_replays(model, graphs, cfg, (64, 128, 37, 512), 3, 5,
                    oracle_weights=weights if dtype == torch.float32 else None)
     assert len(graphs._entries) <= 3
+
+
+@pytest.mark.parametrize("split", ["all", "mlp"])
+def test_graph_replays_split_gemm_inputs(split):
+    """bf16 weights with split GEMM inputs: the split-output kernels recorded and
+    replayed bit for bit against eager, and the replay within 1e-2 of the fp32
+    oracle."""
+    from qdc_amd.graphs import LastHiddenGraphs
+    cfg, weights, model = _synthetic_model(torch.bfloat16, seed=13, split=split)
+    graphs = LastHiddenGraphs(model, max_graphs=2, gemm_libraries=None)
+    _check_replays(model, graphs, cfg, (64, 200), 3, 6)
+    rng = np.random.default_rng(7)
+    ids, mask = rng.integers(0, cfg.vocab, size=96), np.ones(96, np.int64)
+    ref = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask)[-1]
+    assert normwise(graphs(ids, mask), ref) <= 1e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

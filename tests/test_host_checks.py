@@ -206,3 +206,22 @@ def test_split_weight_and_join_on_cpu():
     got = xs.float() @ ops.split_weight(wk).float()
     exp = (hi.float() + lo.float()) @ wk.float()
     assert torch.allclose(got, exp, rtol=0, atol=1e-6)
+
+
+def test_backbone_split_mode_checks():
+    """The split GEMM-input modes are bf16-only, named, and need rows of whole
+    4-element groups; all of it is checked before any weight is touched."""
+    import dataclasses
+
+    from qdc_amd import backbone
+    from qdc_amd.config import plumbing_config
+    cfg = plumbing_config()
+    with pytest.raises(ValueError, match="bfloat16"):
+        backbone.QwenBackbone(cfg, {}, "cpu", torch.float32, split_gemm_inputs=True)
+    with pytest.raises(ValueError, match="split_gemm_inputs"):
+        backbone.QwenBackbone(cfg, {}, "cpu", torch.bfloat16, split_gemm_inputs="attention")
+    odd = dataclasses.replace(cfg, value_dim=6)
+    with pytest.raises(ValueError, match="multiples of 4"):
+        backbone.QwenBackbone(odd, {}, "cpu", torch.bfloat16, split_gemm_inputs="all")
+    with pytest.raises(KeyError):  # "mlp" does not split the 6-wide value rows: it proceeds
+        backbone.QwenBackbone(odd, {}, "cpu", torch.bfloat16, split_gemm_inputs="mlp")
