@@ -363,6 +363,46 @@ def build_forward_kernels(dev):
         lambda i: (randn((T, 2 * I), bf), torch.empty((T, I), dtype=bf, device=dev)),
         lambda s: ops.native_mlp_gate(s[0][:, :I], s[0][:, I:], out=s[1]), [T, I], "bfloat16",
         group="forward", launches=n_layers))
+    # the split GEMM-input variants (bf16 weights, split_gemm_inputs="all"): each
+    # output element is two bf16 terms (4 bytes); `launches` counts them per
+    # forward in that mode ("mlp" launches the residual norm 24 times and SwiGLU)
+    X2 = ops.BF16X2
+    ks.append(Kernel(
+        "fwd_gather_rms_split", "gather_rms_fast", T * Hd * (2 + 4 + 4) + T * 4 + Hd * 2,
+        lambda i: (torch.randint(0, cfg.vocab, (T,), generator=g, device=dev, dtype=torch.int32),
+                   torch.empty((T, Hd), dtype=f32, device=dev),
+                   torch.empty((T, 2 * Hd), dtype=bf, device=dev)),
+        lambda s: ops.native_gather_rms(table, s[0], wb, 1e-6, hidden=s[1], normed=s[2],
+                                        normed_dtype=X2),
+        [T, Hd], "bfloat16->float32,bf16x2", group="split", launches=1,
+        ceiling=row_copy_ceiling(dev, g, table, T, 4)))
+    ks.append(Kernel(
+        "fwd_residual_rms_f32_split", "rms_rows_fast", T * Hd * (4 + 4 + 4 + 4) + Hd * 2,
+        lambda i: (randn((T, Hd), f32), randn((T, Hd), f32),
+                   torch.empty((T, Hd), dtype=f32, device=dev),
+                   torch.empty((T, 2 * Hd), dtype=bf, device=dev)),
+        lambda s: ops.native_residual_rms(s[0], s[1], wb, 1e-6, residual=s[2], out=s[3],
+                                          out_dtype=X2),
+        [T, Hd], "float32->float32,bf16x2", group="split", launches=2 * n_layers - 1))
+    ks.append(Kernel(
+        "fwd_gated_rms_split", "rms_rows_fast", T * vh * vd * (2 + 2 + 4) + vd * 2,
+        lambda i: (randn((T, vh, vd), bf), randn((T, pw), bf),
+                   torch.empty((T, vh, 2 * vd), dtype=bf, device=dev)),
+        lambda s: ops.native_gated_rms(s[0], s[1][:, cq:cq + vh * vd].view(T, vh, vd), wg, 1e-6,
+                                       out=s[2], out_dtype=X2),
+        [T, vh, vd], "bfloat16->bf16x2", group="split", launches=n_delta))
+    ks.append(Kernel(
+        "fwd_gate_merge_split", "gate_merge_fast", T * nh * hd * (4 + 2 + 4),
+        lambda i: (randn((B, nh, S, hd), f32), randn((T, qkv_w), bf),
+                   torch.empty((T, 2 * nh * hd), dtype=bf, device=dev)),
+        lambda s: ops.attention_gate(s[0], s[1][:, hd * (nh + 2 * kv):].view(T, nh, hd),
+                                     out_dtype=X2, out=s[2]),
+        [B, S, nh, hd], "float32,bfloat16->bf16x2", group="split", launches=n_full))
+    ks.append(Kernel(
+        "fwd_swiglu_f32_split", "swiglu_fast", T * I * (4 + 4 + 4),
+        lambda i: (randn((T, 2 * I), f32), torch.empty((T, 2 * I), dtype=bf, device=dev)),
+        lambda s: ops.native_mlp_gate(s[0][:, :I], s[0][:, I:], out=s[1], out_dtype=X2),
+        [T, I], "float32->bf16x2", group="split", launches=n_layers))
     return ks
 
 
@@ -935,8 +975,9 @@ def main():
     hot = [k for k in kernels if k.group == "hot"] or kernels
     fwd = [k for k in kernels if k.group == "forward"]
     alone = [k for k in kernels if k.group == "standalone"]
-    ceilings = copy_ceilings(dev, hot + [k for k in fwd + alone if k not in hot], args.steps,
-                             args.warmup)
+    split = [k for k in kernels if k.group == "split"]
+    ceilings = copy_ceilings(dev, hot + [k for k in fwd + alone + split if k not in hot],
+                             args.steps, args.warmup)
     floors = empty_floors(hot, args.steps, args.warmup)
     hot_ms = sum(k.avg_ms for k in hot) * args.steps
     step_bytes = sum(k.algo_bytes for k in hot)
@@ -1008,6 +1049,16 @@ def main():
                 "note": "the gather and the first input norm as two launches at the forward's "
                         "shapes; the forward runs them fused (fwd_gather_rms_bf16)",
                 "kernels": {k.name: entry(k) for k in alone}}
+    if split:
+        sb = sum(k.launches * k.algo_bytes for k in split)
+        ss = sum(k.launches * k.avg_ms for k in split) / 1e3
+        line.setdefault("forward_shapes", {})["split_gemm_inputs"] = {
+            "note": "the kernels that write GEMM inputs, as the forward with bf16 weights and "
+                    "split_gemm_inputs='all' launches them: every output element as two bf16 "
+                    "terms (4 bytes); SwiGLU reads the fp32 gate/up GEMM output",
+            "kernels": {k.name: dict(entry(k), launches_per_forward=k.launches) for k in split},
+            "gbs_forward_weighted": round(sb / ss / 1e9, 1),
+            "pct_peak_forward_weighted": round(100 * sb / ss / 1e9 / PEAK_GBS, 1)}
     if not args.no_e2e:
         for k in kernels:  # release the kernel benchmark's buffers first
             k.sets, k.graph = None, None
