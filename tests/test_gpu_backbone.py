@@ -573,6 +573,56 @@ def test_full_size_forward_causal_prefix_split(mode):
                           weights, cfg, ids[r, :P], np.ones(P, np.int64))
 
 
+def _poison_free_blocks():
+    """Fill every free block held by torch's caching allocator with NaN: each
+    cached block size is allocated back (the allocator hands out the cached
+    block that fits), filled and released, so the next forward runs on buffers
+    full of NaN wherever it reuses memory (the reference catches scratch-reuse
+    bugs with NaN-poisoned workspaces, test/backbone.jl:315-385)."""
+    torch.cuda.synchronize()
+    sizes = [b["size"] for seg in torch.cuda.memory_snapshot() for b in seg["blocks"]
+             if b["state"] == "inactive"]
+    held = []
+    for size in sorted(sizes, reverse=True):
+        t = torch.empty(size // 4, dtype=torch.float32, device="cuda")
+        t.fill_(float("nan"))
+        held.append(t)
+    torch.cuda.synchronize()
+    del held
+    return len(sizes)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16", "all", "mlp"])
+def test_forward_on_nan_poisoned_memory(mode):
+    """A forward whose reused device memory was filled with NaN equals the
+    first forward bit for bit: no kernel reads an output or workspace element
+    it did not write (partial tiles, padding columns, masked rows, split pieces)."""
+    from qdc_amd import backbone
+    from qdc_amd.config import qwen35_08b_config
+    from qdc_amd.weights import random_weights
+    cfg = dataclasses.replace(qwen35_08b_config(depth=4), vocab=4096)
+    weights = random_weights(cfg, seed=17)
+    dtype = torch.float32 if mode == "fp32" else torch.bfloat16
+    if dtype == torch.bfloat16:
+        weights = bf16_weights(weights)
+    model = model_for(weights, cfg, dtype, split=mode if mode in ("all", "mlp") else False)
+    rng = np.random.default_rng(18)
+    ids = torch.from_numpy(rng.integers(0, cfg.vocab, size=(3, 77)).astype(np.int32)).cuda()
+    mask = np.ones((3, 77), np.int64)
+    mask[1, :9] = 0
+    mask[2, ::5] = 0
+    dmask = torch.from_numpy(mask.astype(np.int32)).cuda()
+    first = backbone.batch_backbone_states(model, ids, dmask).clone()
+    last = torch.from_numpy(backbone.batch_backbone_hidden(model, ids, dmask))
+    poisoned = _poison_free_blocks()
+    again = backbone.batch_backbone_states(model, ids, dmask)
+    assert poisoned > 0
+    assert torch.isfinite(first).all()
+    assert torch.equal(first, again), mode
+    _poison_free_blocks()
+    assert torch.equal(last, torch.from_numpy(backbone.batch_backbone_hidden(model, ids, dmask)))
+
+
 def test_bf16_checkpoint_directory(native_fixture, tmp_path):
     """QwenBackbone(dir) on a BF16 safetensors checkpoint: loaded onto the GPU in
     bf16 (no widening) and packed there; the forward equals the in-memory build of

@@ -135,6 +135,7 @@ QK_CASES = [
     (7, 2, 1, 24, 16, 7, 1e4),          # odd chunk count: general kernel
     (21, 4, 2, 256, 48, 7, 1e6),        # rotary chunks not a power of two: pair-dealt lanes
     (37, 8, 2, 256, 64, 16, 1e7),       # 0.8B heads, sequences of 16 with a partial last one
+    (12, 2, 1, 4, 2, 12, 1e4),          # rotary 2 of head_dim 4 (the reference's partial case)
 ]
 
 
@@ -180,7 +181,8 @@ def test_qk_norm_rope_offset_inplace_one_side(dtype):
 # ----------------------------------------------------------- gated norm -----
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("tokens,heads,width", [(16384, 16, 128), (128, 4, 128), (17, 4, 128),
-                                                (9, 3, 100), (5, 2, 8)])
+                                                (1, 4, 128), (129, 4, 128), (9, 3, 100),
+                                                (5, 2, 8)])
 def test_gated_rmsnorm(dtype, tokens, heads, width):
     from qdc_amd import ops
     x = host((tokens, heads, width), 17, 1.0, dtype)
