@@ -218,11 +218,13 @@ int32_t launch_fast(const Args &a, hipStream_t stream) {
 }
 
 // Fast-path shapes by G = groups per row: a lane holds 2 groups for rows of up
-// to 64 groups and 4 groups for 128- and 256-group rows (8 for plain all-bf16
-// 128-group rows; the splits that measured fastest on MI355X, 32 x 8 and
-// 16 x 16 were not faster for the 256-group fp32-to-bf16 rows); rows of 192,
-// 320, 384 and 448 groups take 64 lanes with 3-7 groups each; wider rows 2
-// wavefronts (512-1536 groups: fp32 rows of
+// to 64 groups and 4 groups for 128-group rows (8 for plain all-bf16 128-group
+// rows; the splits that measured fastest on MI355X); 256-group rows (fp32 rows
+// of 1024) take 2 wavefronts of 2 groups per lane, 2-4% faster than 64 x 4 for
+// the 16-byte-per-element residual rows (all fp32, or fp32 with a split output)
+// and for fp32 rows to bf16, equal for the rest (32 x 8, 16 x 16 and 256 x 1
+// were slower); rows of 192, 320, 384 and 448 groups take 64 lanes with 3-7
+// groups each; wider rows 2 wavefronts (512-1536 groups: fp32 rows of
 // 2048-6144 elements, 4-12 groups per lane) or 4 (2048-4096 groups, 8-16 per
 // lane).  Measured on MI355X against one 64-lane wavefront per row with G/64
 // groups per lane: 2-7% faster at 512-768 groups and 13-15% at 1024 (16 groups
@@ -252,7 +254,7 @@ int32_t dispatch_fast(const Args &a, hipStream_t stream) {
         QDC_FAST(32, 2)
         QDC_FAST(32, 4)
         QDC_FAST(64, 3)
-        QDC_FAST(64, 4)
+        QDC_FAST(128, 2)
         QDC_FAST(64, 5)
         QDC_FAST(64, 6)
         QDC_FAST(64, 7)
