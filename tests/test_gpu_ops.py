@@ -370,6 +370,35 @@ def test_rmsnorm_every_fast_shape(groups, mix):
     report(f"rms {mix} G={groups} width={width}", back(got), exp, out_dtype)
 
 
+@pytest.mark.parametrize("groups", RMS_FAST_GROUPS)
+@pytest.mark.parametrize("mix", ["f32->split", "residual f32+f32->split", "gated bf16->split"])
+def test_rmsnorm_every_fast_shape_split_output(groups, mix):
+    """The same fast-path shapes (4 elements per group) with the split two-term
+    bf16 output: hi + lo within the fp32 bar of the oracle's fp32 result."""
+    from qdc_amd import ops
+    bf, f32 = torch.bfloat16, torch.float32
+    width, rows = groups * 4, 5
+    w = host((width,), 72, 0.02, bf)
+    if mix.startswith("gated"):
+        x = host((rows, 1, width), 74, 1.0, bf)
+        z = host((rows, 1, width), 75, 1.0, bf)
+        got = ops.native_gated_rms(dev(x, bf), dev(z, bf), dev(w, bf), 1e-6,
+                                   out_dtype=ops.BF16X2).view(rows, 2 * width)
+        exp = O.gated_rms(x, z, w, 1e-6).reshape(rows, width)
+    elif mix.startswith("residual"):
+        x, m = host((rows, width), 71), host((rows, width), 73)
+        res, got = ops.native_residual_rms(dev(x, f32), dev(m, f32), dev(w, bf), 1e-6,
+                                           out_dtype=ops.BF16X2)
+        exp_res, exp = O.residual_rms(x, m, w, 1e-6)
+        assert np.array_equal(back(res), exp_res)
+    else:
+        x = host((rows, width), 71)
+        got = ops.native_rms(dev(x, f32), dev(w, bf), 1e-6, out_dtype=ops.BF16X2)
+        exp = O.rms(x, w, 1e-6)
+    bits = got.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    report(f"rms {mix} G={groups} width={width}", O.join_split(bits), exp, f32)
+
+
 # ------------------------------------------- fp32 residual stream mixes ------
 @pytest.mark.parametrize("rows,width", [(16384, 1024), (33, 256), (5, 1000), (7, 5120),
                                         (3, 12288)])
