@@ -1147,6 +1147,36 @@ def test_attention_prepare_checks():
 
 
 # ------------------------------------------------- gather + first input norm --
+GATHER_RMS_FAST_GROUPS = [2, 4, 8, 16, 32, 64, 128, 256, 320, 384, 512, 640, 768, 1024]
+
+
+@pytest.mark.parametrize("groups", GATHER_RMS_FAST_GROUPS)
+@pytest.mark.parametrize("table_dtype,normed", [(torch.bfloat16, "split"), (torch.float32, "split"),
+                                                (torch.bfloat16, torch.float32)])
+def test_gather_rms_every_fast_shape(groups, table_dtype, normed):
+    """Every fast-path width of the fused gather + first norm (4 elements per
+    group) for the type mixes the width table is not otherwise run with: bf16
+    or fp32 table rows into the split output, and bf16 rows into an fp32 norm.
+    hidden bit-exact; normed within the fp32 bar."""
+    from qdc_amd import ops
+    width, vocab, n = groups * 4, 97, 19
+    table = host((vocab, width), 81, 0.02, torch.bfloat16)
+    ids = np.random.default_rng(82).integers(0, vocab, size=n).astype(np.int32)
+    split = normed == "split"
+    wdt = torch.bfloat16 if split else normed
+    w = host((width,), 83, 0.02, wdt)
+    hidden, got = ops.native_gather_rms(dev(table, table_dtype), dev(ids, torch.int32), dev(w, wdt),
+                                        1e-6, normed_dtype=ops.BF16X2 if split else None)
+    rows = O.gather(table, ids)
+    assert np.array_equal(back(hidden), rows)
+    if split:
+        got = O.join_split(got.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+    else:
+        got = back(got)
+    report(f"gather_rms {table_dtype}->{normed} width={width}", got, O.rms(rows, w, 1e-6),
+           torch.float32)
+
+
 @pytest.mark.parametrize("table_dtype,norm_dtype", [(torch.bfloat16, torch.bfloat16),
                                                     (torch.float32, torch.float32),
                                                     (torch.float32, torch.bfloat16)])
