@@ -652,8 +652,8 @@ def e2e_benchmark(dev, steps=3, warmup=1):
                         dtype=torch.int32)
     mask = None  # no padding: every token is kept (the forward then does no masking work)
 
-    def forward_ms(split):
-        model = backbone.QwenBackbone.from_weights(weights, cfg, dev, torch.bfloat16,
+    def forward_ms(split, dtype=torch.bfloat16):
+        model = backbone.QwenBackbone.from_weights(weights, cfg, dev, dtype,
                                                    split_gemm_inputs=split)
         for _ in range(warmup):
             out = model.forward(ids, mask)
@@ -672,6 +672,8 @@ def e2e_benchmark(dev, steps=3, warmup=1):
 
     ms = forward_ms(False)
     split_ms = {mode: forward_ms(mode) for mode in ("all", "mlp")}
+    # the same weights widened to fp32 (exact), fp32 activations and GEMMs
+    fp32_ms = forward_ms(False, torch.float32)
     del weights
     torch.cuda.empty_cache()
     # this library's kernels of one forward, replayed from graphs on buffers of
@@ -697,6 +699,11 @@ def e2e_benchmark(dev, steps=3, warmup=1):
                 **{mode: {"ms_per_forward": round(v, 3),
                           "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (v / 1e3), 1)}
                    for mode, v in split_ms.items()}},
+            "fp32": {
+                "note": "the same weights widened to fp32 (exactly), fp32 activations and GEMMs: "
+                        "the mode within 1e-5 of the fp32 oracle end to end",
+                "ms_per_forward": round(fp32_ms, 3),
+                "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (fp32_ms / 1e3), 1)},
             "steps": steps, "warmup": warmup}
 
 
