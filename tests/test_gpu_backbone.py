@@ -573,6 +573,43 @@ def test_full_size_forward_causal_prefix_split(mode):
                           weights, cfg, ids[r, :P], np.ones(P, np.int64))
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("mode", ["bf16", "all", "fp32"])
+def test_long_sequence_causal_prefix(mode):
+    """One sequence of 16384 tokens through the 4-layer 0.8B-shaped backbone
+    (one full-attention layer over 16384 keys: the multi-wavefront softmax rows
+    and a 8.6 GB score matrix): finite, bitwise repeatable, the last-token
+    forward equal to the last row, and the first 64 positions within the bar of
+    the oracle's forward of those 64 tokens (causality)."""
+    from qdc_amd import backbone
+    from qdc_amd.config import qwen35_08b_config
+    from qdc_amd.weights import random_weights
+    cfg = dataclasses.replace(qwen35_08b_config(depth=4), vocab=4096)
+    weights = random_weights(cfg, seed=41)
+    dtype = torch.float32 if mode == "fp32" else torch.bfloat16
+    if dtype == torch.bfloat16:
+        weights = bf16_weights(weights)
+    model = model_for(weights, cfg, dtype, split=mode if mode == "all" else False)
+    S, P = 16384, 64
+    ids = np.random.default_rng(42).integers(0, cfg.vocab, size=(1, S))
+    d_ids = torch.from_numpy(ids.astype(np.int32)).cuda()
+    first = backbone.batch_backbone_states(model, d_ids, None)
+    again = backbone.batch_backbone_states(model, d_ids, None)
+    assert torch.equal(first, again)
+    assert torch.isfinite(first).all()
+    last = backbone.batch_backbone_hidden(model, d_ids, None)
+    assert normwise(last[0], first[0, -1].cpu().numpy()) <= (1e-6 if mode == "fp32" else 1e-2)
+    prefix = first[0, :P].float().cpu().numpy()
+    del model, first, again
+    torch.cuda.empty_cache()
+    full = np.ones(P, np.int64)
+    exp32 = forward.backbone_hidden(weights, cfg.as_dict(), ids[0, :P], full)
+    err32 = normwise(prefix, exp32)
+    print(f"16384-token sequence ({mode}): first {P} positions vs fp32 oracle {err32:.2e}",
+          flush=True)
+    assert err32 <= (1e-5 if mode == "fp32" else 1e-2)
+
+
 def _poison_free_blocks():
     """Fill every free block held by torch's caching allocator with NaN: each
     cached block size is allocated back (the allocator hands out the cached
