@@ -55,7 +55,7 @@ class QwenBackbone:
     """A Qwen3.5 hybrid backbone resident on one GPU."""
 
     def __init__(self, cfg: BackboneConfig, weights: dict, device="cuda:0",
-                 dtype: torch.dtype = torch.float32, split_gemm_inputs=False):
+                 dtype: torch.dtype = torch.float32, split_gemm_inputs: bool | str = False):
         """``dtype`` is the storage type of weights and GEMM activations; the
         residual stream and the returned hidden states are fp32 either way.
         ``split_gemm_inputs`` (bfloat16 only: False, True / ``"all"``, or
@@ -152,13 +152,13 @@ class QwenBackbone:
     @classmethod
     def from_weights(cls, weights: dict, cfg: BackboneConfig, device="cuda:0",
                      dtype: torch.dtype = torch.float32,
-                     split_gemm_inputs: bool = False) -> "QwenBackbone":
+                     split_gemm_inputs: bool | str = False) -> "QwenBackbone":
         return cls(cfg, weights, device, dtype, split_gemm_inputs)
 
     @classmethod
     def from_directory(cls, directory: str, device="cuda:0",
                        dtype: torch.dtype = torch.float32,
-                       split_gemm_inputs: bool = False) -> "QwenBackbone":
+                       split_gemm_inputs: bool | str = False) -> "QwenBackbone":
         """A local safetensors checkpoint directory (no network access).  Tensors
         load straight onto ``device`` in their stored dtype; with ``dtype=bfloat16``
         a BF16 checkpoint is never widened to fp32 (the packed projection weights
