@@ -50,6 +50,14 @@ def _is_split(out_dtype) -> bool:
     return False
 
 
+def _split_stride(stride: int) -> int:
+    """A split output's row stride in bf16 values -> in split elements (two bf16
+    terms each); rows must start on a whole 16-byte piece (8 bf16 values)."""
+    if stride % 8:
+        raise ValueError("a split output's rows must be a multiple of 8 bf16 values apart")
+    return stride // 2
+
+
 def split_weight(weight: torch.Tensor) -> torch.Tensor:
     """A GEMM weight ``[K, N]`` (``y = x @ weight``) as ``[2K, N]`` for split
     inputs: rows ``8g + j`` and ``8g + 4 + j`` both hold row ``4g + j``, so
@@ -246,7 +254,7 @@ def native_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, centered: bool
                          "form: bfloat16, last axis 2*width)")
     _, _, ld_out = _rows_view(out)
     if split:
-        ld_out //= 2  # the C ABI counts split elements
+        ld_out = _split_stride(ld_out)  # the C ABI counts split elements
     code = _lib.QDC_BF16X2 if split else _DTYPES[weight.dtype]
     keep = _row_mask(token_mask, rows, x)
     if keep is None:
@@ -342,7 +350,7 @@ def native_gated_rms(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps
         raise ValueError("out must be [tokens, heads, width] with contiguous heads "
                          "([tokens, heads, 2*width] for the split form)")
     tok = lambda t: t.stride(0) if tokens > 1 else heads * t.shape[2]  # noqa: E731
-    out_tok = tok(out) // 2 if split else tok(out)  # the C ABI counts split elements
+    out_tok = _split_stride(tok(out)) if split else tok(out)  # the C ABI counts split elements
     check(lib().qdc_gated_rmsnorm(out.data_ptr(), x.data_ptr(), z.data_ptr(), weight.data_ptr(),
                                   tokens, heads, width, tok(x), tok(z), out_tok, eps, code,
                                   _lib.QDC_BF16X2 if split else code, _stream(x)),
@@ -511,7 +519,7 @@ def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
         raise ValueError("out must be [tokens, width] with contiguous rows "
                          "([tokens, 2*width] bfloat16 for the split form)")
     ld = lambda t: t.stride(0) if tokens > 1 else t.shape[1]  # noqa: E731
-    ld_out = ld(out) // 2 if split else ld(out)  # the C ABI counts split elements
+    ld_out = _split_stride(ld(out)) if split else ld(out)  # the C ABI counts split elements
     check(lib().qdc_swiglu(out.data_ptr(), gate.data_ptr(), up.data_ptr(), tokens, width,
                            ld(gate), ld(up), ld_out, code, _lib.QDC_BF16X2 if split else code,
                            _stream(gate)), "native_mlp_gate")
@@ -634,7 +642,7 @@ def attention_gate(values: torch.Tensor, gate: torch.Tensor, out_dtype=None,
                          "([B*S, 2*H*hd] bfloat16 for the split form)")
     tok = out.stride(0) if B * S > 1 else oshape[1]
     if split:
-        tok //= 2  # the C ABI counts split elements
+        tok = _split_stride(tok)  # the C ABI counts split elements
     gtok = gate.stride(0) if B * S > 1 else H * gate.stride(1)
     code = _lib.QDC_BF16X2 if split else _DTYPES[out.dtype]
     check(lib().qdc_attention_gate(out.data_ptr(), code, values.data_ptr(),

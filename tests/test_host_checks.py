@@ -225,3 +225,22 @@ def test_backbone_split_mode_checks():
         backbone.QwenBackbone(odd, {}, "cpu", torch.bfloat16, split_gemm_inputs="all")
     with pytest.raises(KeyError):  # "mlp" does not split the 6-wide value rows: it proceeds
         backbone.QwenBackbone(odd, {}, "cpu", torch.bfloat16, split_gemm_inputs="mlp")
+
+
+def test_split_output_strides_checked(no_launch):
+    """A caller-supplied split output whose rows are not whole 16-byte pieces
+    apart (a bf16 stride that is not a multiple of 8) is rejected before the
+    stride is halved for the C ABI."""
+    X2 = ops.BF16X2
+    odd = torch.empty((8, 140), dtype=BF16, device="meta")[:, :128]      # stride 140
+    with pytest.raises(ValueError, match="multiple of 8"):
+        ops.native_rms(d(8, 64), d(64, dtype=BF16), 1e-6, out=odd, out_dtype=X2)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        ops.native_mlp_gate(d(8, 64), d(8, 64), out=odd, out_dtype=X2)
+    gated = torch.empty((8, 1, 140), dtype=BF16, device="meta")[:, :, :128]
+    with pytest.raises(ValueError, match="multiple of 8"):
+        ops.native_gated_rms(d(8, 1, 64, dtype=BF16), d(8, 1, 64, dtype=BF16),
+                             d(64, dtype=BF16), 1e-6, out=gated, out_dtype=X2)
+    merged = torch.empty((4, 36), dtype=BF16, device="meta")[:, :32]
+    with pytest.raises(ValueError, match="multiple of 8"):
+        ops.attention_gate(d(1, 2, 4, 8), d(4, 2, 8, dtype=BF16), out=merged, out_dtype=X2)
