@@ -573,6 +573,56 @@ def test_full_size_forward_causal_prefix_split(mode):
                           weights, cfg, ids[r, :P], np.ones(P, np.int64))
 
 
+def _wide_config():
+    """A wider hybrid shape than the 0.8B-like one, 4 layers: hidden 2048, 16 Q /
+    4 KV heads of 256 (rotary 64), DeltaNet 16 key heads x 128 and 32 value heads
+    x 128 (2 value heads per key head), intermediate 6144, vocab 4096."""
+    from qdc_amd.config import BackboneConfig, hybrid_layer_types
+    return BackboneConfig(hidden=2048, head_dim=256, heads=16, kv_heads=4, key_heads=16,
+                          value_heads=32, key_dim=128, value_dim=128,
+                          eps=float(np.float32(1e-6)), rope_theta=1e7, rotary_dim=64,
+                          layer_types=hybrid_layer_types(4), intermediate=6144, vocab=4096)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("mode", ["fp32", "bf16", "all", "mlp"])
+def test_wide_backbone(mode):
+    """The wider shape end to end at 80 tokens with a padded prefix (rows of
+    2048 over two wavefronts, the 2048-wide fused gather + norm, 16/4 attention
+    heads, 32 DeltaNet value heads over 16 key heads, SwiGLU of 6144): fp32
+    within 1e-5 of the oracle; bf16 storage within 1e-2 of the oracle with the
+    same storage points; split GEMM inputs within 1e-2 of fp32."""
+    from qdc_amd import backbone
+    from qdc_amd.weights import random_weights
+    cfg = _wide_config()
+    weights = random_weights(cfg, seed=51)
+    dtype = torch.float32 if mode == "fp32" else torch.bfloat16
+    if dtype == torch.bfloat16:
+        weights = bf16_weights(weights)
+    model = model_for(weights, cfg, dtype, split=mode if mode in ("all", "mlp") else False)
+    ids = np.random.default_rng(52).integers(0, cfg.vocab, size=80)
+    mask = np.ones(80, np.int64)
+    mask[:7] = 0
+    got = backbone.backbone_hidden(model, ids, mask)
+    last = backbone.backbone_last_hidden(model, ids, mask)
+    del model
+    torch.cuda.empty_cache()
+    assert normwise(last, got[-1]) <= (1e-6 if mode == "fp32" else 1e-3)
+    exp32 = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask)
+    err32 = normwise(got, exp32)
+    if mode == "fp32":
+        print(f"wide backbone fp32: vs fp32 oracle {err32:.2e}", flush=True)
+        assert err32 <= 1e-5
+    elif mode == "bf16":
+        expbf = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask, bf16=True)
+        errbf = normwise(got, expbf)
+        print(f"wide backbone bf16: vs bf16-storage oracle {errbf:.2e}, vs fp32 {err32:.2e}",
+              flush=True)
+        assert errbf <= 1e-2
+    else:
+        _split_end_to_end("wide backbone,", mode, got, weights, cfg, ids, mask)
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("mode", ["bf16", "all", "fp32"])
 def test_long_sequence_causal_prefix(mode):
