@@ -151,7 +151,7 @@ def build_kernels(dev):
     # rows per workgroup of rms_rows_fast: 256 / lanes per row (64 lanes x 4 groups
     # for fp32 rows of 1024, 16 x 8 for bf16 rows of 1024, 32 x 2 and 16 x 2 for
     # fp32 and bf16 rows of 256)
-    rms("rmsnorm_f32", 8192, 1024, f32, 4)
+    rms("rmsnorm_f32", 8192, 1024, f32, 2)   # 2 wavefronts per 1024-wide fp32 row
     rms("rmsnorm_bf16", 8192, 1024, bf, 16)
     rms("headnorm_f32", 81920, 256, f32, 8)
     rms("headnorm_bf16", 81920, 256, bf, 16)
