@@ -623,6 +623,54 @@ def test_wide_backbone(mode):
         _split_end_to_end("wide backbone,", mode, got, weights, cfg, ids, mask)
 
 
+VARIANT_SHAPES = {
+    # no GQA, rotation over the whole head, DeltaNet key_dim 64 != value_dim 128
+    "mha_full_rotary": dict(hidden=512, head_dim=128, heads=4, kv_heads=4, key_heads=4,
+                            value_heads=8, key_dim=64, value_dim=128, rotary_dim=128,
+                            intermediate=1536),
+    # 8 query heads per KV head, head_dim 128 with rotary 32, hidden 768
+    "gqa8": dict(hidden=768, head_dim=128, heads=16, kv_heads=2, key_heads=8, value_heads=16,
+                 key_dim=128, value_dim=128, rotary_dim=32, intermediate=2048),
+}
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("shape", list(VARIANT_SHAPES))
+@pytest.mark.parametrize("mode", ["fp32", "bf16", "all"])
+def test_variant_backbone_shapes(shape, mode):
+    """Head layouts other than the 0.8B-like one, 4 layers, 70 tokens with
+    holes in the mask: fp32 within 1e-5 of the oracle, bf16 storage within 1e-2
+    of the oracle with the same storage points, split GEMM inputs within 1e-2 of
+    fp32."""
+    from qdc_amd import backbone
+    from qdc_amd.config import BackboneConfig, hybrid_layer_types
+    from qdc_amd.weights import random_weights
+    cfg = BackboneConfig(**VARIANT_SHAPES[shape], eps=float(np.float32(1e-6)), rope_theta=1e6,
+                         layer_types=hybrid_layer_types(4), vocab=2048)
+    weights = random_weights(cfg, seed=61)
+    dtype = torch.float32 if mode == "fp32" else torch.bfloat16
+    if dtype == torch.bfloat16:
+        weights = bf16_weights(weights)
+    model = model_for(weights, cfg, dtype, split=mode if mode == "all" else False)
+    ids = np.random.default_rng(62).integers(0, cfg.vocab, size=70)
+    mask = np.ones(70, np.int64)
+    mask[1:69:3] = 0
+    got = backbone.backbone_hidden(model, ids, mask)
+    exp32 = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask)
+    err32 = normwise(got, exp32)
+    if mode == "fp32":
+        print(f"{shape} fp32: vs fp32 oracle {err32:.2e}", flush=True)
+        assert err32 <= 1e-5
+    elif mode == "bf16":
+        errbf = normwise(got, forward.backbone_hidden(weights, cfg.as_dict(), ids, mask,
+                                                      bf16=True))
+        print(f"{shape} bf16: vs bf16-storage oracle {errbf:.2e}, vs fp32 {err32:.2e}",
+              flush=True)
+        assert errbf <= 1e-2
+    else:
+        _split_end_to_end(f"{shape},", mode, got, weights, cfg, ids, mask)
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("mode", ["bf16", "all", "fp32"])
 def test_long_sequence_causal_prefix(mode):
