@@ -410,3 +410,21 @@ def test_empty_validation():
     assert lib.qdc_empty(-1, None) == -2
     assert lib.qdc_empty(1 << 24, None) == -2
     assert lib.qdc_empty(0, None) == 0
+
+
+def test_c_host_program_host_only(tmp_path):
+    """include/qdc_hip.h compiles as C99 with gcc, a plain C program links
+    against the library, and its host-only checks (version, status strings,
+    argument errors found before any launch) pass; the same program runs its
+    device checks in tests/test_gpu_c_host.py."""
+    src = os.path.join(ROOT, "tests", "c_host", "qdc_c_host.c")
+    exe = tmp_path / "qdc_c_host"
+    lib = os.path.join(ROOT, "qwendecisioncore.jl_amd", "lib")
+    subprocess.run(["gcc", "-std=c99", "-O1", "-Wall", "-Wextra", "-Werror",
+                    "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    "-I" + os.path.join(ROOT, "include"), src, "-o", str(exe), "-L" + lib,
+                    "-lqdc_hip", "-L/opt/rocm/lib", "-lamdhip64", "-lm", "-Wl,-rpath," + lib,
+                    "-Wl,-rpath,/opt/rocm/lib"], check=True)
+    r = subprocess.run([str(exe), "--host-only"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "all checks passed" in r.stdout
