@@ -248,7 +248,7 @@ def _full_depth_case(dtype):
 
 
 def _bf16_end_to_end(got, expbf, what):
-    """The north-star bar for bf16 end to end: 1e-2 against the oracle run with
+    """The bf16 end-to-end bar: 1e-2 against the oracle run with
     the same bf16 storage points.  Where it is missed the test reports xfail
     with the measured distance (see test_full_depth_bf16_teacher_forced for
     the per-layer and per-op parity that holds at every layer)."""
