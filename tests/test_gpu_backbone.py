@@ -560,6 +560,32 @@ def test_full_depth_backbone_split(mode):
     _split_end_to_end("24 layers, 64 tokens,", mode, got, weights, cfg, ids, mask)
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("seed", [101, 102, 103])
+def test_full_depth_split_other_seeds(seed):
+    """The 24-layer bar with other random weights and tokens (vocab cut to
+    4096, 96 tokens with a padded prefix): both split modes within 1e-2 of the
+    fp32 oracle, and all-bf16 storage reported beside them."""
+    from qdc_amd import backbone
+    from qdc_amd.config import qwen35_08b_config
+    from qdc_amd.weights import random_weights
+    cfg = dataclasses.replace(qwen35_08b_config(), vocab=4096)
+    weights = bf16_weights(random_weights(cfg, seed=seed))
+    ids = np.random.default_rng(seed + 1000).integers(0, cfg.vocab, size=96)
+    mask = np.ones(96, np.int64)
+    mask[:seed % 9] = 0
+    exp32 = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask)
+    errs = {}
+    for mode in ("all", "mlp", False):
+        model = model_for(weights, cfg, torch.bfloat16, split=mode)
+        errs[mode or "bf16"] = normwise(backbone.backbone_hidden(model, ids, mask), exp32)
+        del model
+        torch.cuda.empty_cache()
+    print(f"24 layers, seed {seed}: vs fp32 oracle " +
+          ", ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+    assert errs["all"] <= 1e-2 and errs["mlp"] <= 1e-2
+
+
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("mode", list(SPLIT_MODES))
 def test_full_size_forward_causal_prefix_split(mode):
