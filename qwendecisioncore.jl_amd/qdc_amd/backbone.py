@@ -42,6 +42,8 @@ rounding is amplified most, and leaves the other GEMMs at their bf16 size.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
@@ -361,7 +363,24 @@ def backbone_last_hidden(model: QwenBackbone, ids, mask) -> np.ndarray:
     return model.forward(d_ids, d_mask, last_only=True)[0].float().cpu().numpy()
 
 
-def _batch_inputs(model: QwenBackbone, ids, mask):
+def native_sequence_start(mask, row: int) -> int:
+    """0-based index of row ``row``'s first kept token: the leading masked
+    tokens are skipped unless ``QDC_AMDGPU_TRIM_PADDING`` is set to something
+    other than ``"1"`` (then 0), and the last token always stays
+    (``native_sequence_start``, ``ext/QwenDecisionCoreAMDGPUExt.jl:17-24``).
+    Leading masked tokens leave the kept tokens' states unchanged up to
+    rounding: they are zero DeltaNet inputs and masked attention keys, and
+    rotary attention scores depend only on relative positions."""
+    if os.environ.get("QDC_AMDGPU_TRIM_PADDING", "1") != "1":
+        return 0
+    row_mask = np.asarray(mask)[row]
+    start = 0
+    while start < row_mask.shape[0] - 1 and row_mask[start] == 0:
+        start += 1
+    return start
+
+
+def _batch_inputs(model: QwenBackbone, ids, mask, trim: bool = False):
     """``[B, S]`` ids and mask as device tensors, checked as ``check_sequence``
     checks one sequence (``src/backbone.jl:413-422``).  Host inputs are checked
     before anything runs.  Device ids are checked by the gather itself (an id
@@ -374,6 +393,10 @@ def _batch_inputs(model: QwenBackbone, ids, mask):
         if ids.ndim != 2 or host_mask.shape != ids.shape:
             raise ValueError("Input IDs and mask must be [batch, sequence] arrays of one shape.")
         check_sequence(model, ids.reshape(-1), host_mask.reshape(-1))
+        if trim:  # from the earliest first kept token of the rows
+            # (ext/metal_batch_forward.jl:113-116, 124-125)
+            first = min(native_sequence_start(host_mask, r) for r in range(ids.shape[0]))
+            ids, host_mask = ids[:, first:], host_mask[:, first:]
         d_ids = torch.from_numpy(ids.astype(np.int32)).to(model.device)
         d_mask = None if host_mask.all() else torch.from_numpy(
             host_mask.astype(np.int32)).to(model.device)
@@ -412,9 +435,11 @@ def batch_backbone_hidden(model: QwenBackbone, ids, mask) -> np.ndarray:
     ids and 0/1 mask ``[B, S]`` (host arrays, or device tensors; ``mask=None``:
     nothing masked) -> the final-normalised hidden state of each row's last
     position, ``[B, hidden]`` fp32 on the host (the reference's
-    ``(hidden, batch)``).  RoPE positions restart at 0 for every row.  Invalid
-    ids or mask values raise ``ValueError`` as ``check_sequence`` does."""
-    d_ids, d_mask, pending = _batch_inputs(model, ids, mask)
+    ``(hidden, batch)``).  RoPE positions restart at 0 for every row.  With host
+    inputs the masked columns before every row's first kept token are dropped
+    first (:func:`native_sequence_start`), as the reference's batched hook does.
+    Invalid ids or mask values raise ``ValueError`` as ``check_sequence`` does."""
+    d_ids, d_mask, pending = _batch_inputs(model, ids, mask, trim=True)
     flag = None if pending is None else pending[0]
     out = model.forward(d_ids, d_mask, last_only=True, error_flag=flag)
     _raise_if_invalid(pending)

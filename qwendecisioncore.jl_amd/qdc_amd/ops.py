@@ -99,6 +99,30 @@ def _device(*tensors) -> None:
             raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
 
 
+def _vector(t: torch.Tensor, n: int, name: str) -> None:
+    """A parameter vector the kernel reads as ``n`` contiguous elements."""
+    if t.numel() != n or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous vector of {n} elements")
+
+
+def _rope_tables(tables, rotary_dim: int, like: torch.Tensor):
+    """``(cos, sin)`` fp32 ``[n_pos, rotary_dim // 2]`` contiguous device tables
+    (``(None, None)`` without rotation); ``n_pos`` is checked against the
+    positions by the library."""
+    if not rotary_dim:
+        return None, None
+    if tables is None or len(tables) != 2:
+        raise ValueError("rotation needs the (cos, sin) tables of rope_tables")
+    cos, sin = tables
+    _device(like, cos, sin)
+    for t in (cos, sin):
+        if (t.dtype != torch.float32 or t.dim() != 2 or t.shape != cos.shape
+                or t.shape[1] != rotary_dim // 2 or not t.is_contiguous()):
+            raise ValueError("cos and sin must be contiguous float32 [n_pos, rotary_dim//2] "
+                             "tables of one shape")
+    return cos, sin
+
+
 def _rows_view(x: torch.Tensor):
     """(rows, width, row_stride) of a tensor whose rows are its last axis,
     contiguous within a row and evenly strided between rows."""
@@ -289,8 +313,7 @@ def native_residual_rms(x: torch.Tensor, mixed: torch.Tensor, weight: torch.Tens
         raise ValueError("x and mixed must be contiguous tensors of one shape")
     width = x.shape[-1]
     rows = x.numel() // width if width else 0
-    if weight.numel() != width:
-        raise ValueError("weight must be a vector of the row width")
+    _vector(weight, width, "weight")
     split = _is_split(out_dtype)
     if split and (x.dtype != torch.float32 or mixed.dtype != torch.float32
                   or weight.dtype != torch.bfloat16):
@@ -333,6 +356,7 @@ def native_gated_rms(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps
     if x.dim() != 3 or z.shape != x.shape:
         raise ValueError("x and z must be [tokens, heads, width]")
     tokens, heads, width = x.shape
+    _vector(weight, width, "weight")
     for t in (x, z):
         if t.stride(2) != 1 or (heads > 1 and t.stride(1) != width):
             raise ValueError("heads must be contiguous within a token")
@@ -390,7 +414,7 @@ def prepare_heads(q: torch.Tensor | None, k: torch.Tensor | None, q_norm, k_norm
         raise ValueError("q or k required")
     tokens, _, head_dim = ref.shape
     seq_len = max(tokens, 1) if seq_len is None else seq_len
-    cos, sin = tables if rotary_dim else (None, None)
+    cos, sin = _rope_tables(tables, rotary_dim, ref)
     batched = any(o is not None and o.dim() == 4 for o in (q_out, k_out))
 
     def side(x, norm, out):
@@ -399,6 +423,7 @@ def prepare_heads(q: torch.Tensor | None, k: torch.Tensor | None, q_norm, k_norm
         _device(x, norm)
         if x.dim() != 3 or x.shape[0] != tokens or x.shape[2] != head_dim or x.stride(2) != 1:
             raise ValueError("q/k must be [tokens, heads, head_dim] with contiguous rows")
+        _vector(norm, head_dim, "q_norm/k_norm")
         if out is None:
             out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
         _device(x, out)
@@ -463,8 +488,8 @@ def attention_prepare(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm:
     for t in (k, v):
         if KV > 1 and t.stride(1) != hd:
             raise ValueError("k and v heads must be contiguous within a token")
-    if q_norm.numel() != hd or k_norm.numel() != hd:
-        raise ValueError("norm weights must be vectors of head_dim")
+    _vector(q_norm, hd, "q_norm")
+    _vector(k_norm, hd, "k_norm")
     S = T // batch
     shapes = ((batch, H, S, hd), (batch, KV, hd, S), (batch, KV, S, hd))
     if out is None:
@@ -476,7 +501,7 @@ def attention_prepare(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm:
         if o.dtype != q.dtype or tuple(o.shape) != sh or not o.is_contiguous():
             raise ValueError("out must be three contiguous tensors [B, H, S, hd], "
                              "[B, KV, hd, S], [B, KV, S, hd] of q's dtype")
-    cos, sin = tables if rotary_dim else (None, None)
+    cos, sin = _rope_tables(tables, rotary_dim, q)
     ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
     tok = lambda t: t.stride(0) if T > 1 else t.shape[1] * t.shape[2]  # noqa: E731
     check(lib().qdc_attention_prepare(out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
@@ -566,6 +591,13 @@ def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor
     for t in (conv, a_decay, dt_bias):
         if t.dtype != torch.float32 or not t.is_contiguous():
             raise ValueError("conv, a_decay and dt_bias must be contiguous float32")
+    channels = 2 * key_heads * key_dim + value_heads * value_dim
+    if conv.dim() != 2 or conv.shape[0] != channels:
+        raise ValueError(f"conv must be [{channels}, taps] (the q|k|v channels)")
+    _vector(a_decay, value_heads, "a_decay")
+    _vector(dt_bias, value_heads, "dt_bias")
+    if proj.shape[1] < channels + value_heads * value_dim + 2 * value_heads:
+        raise ValueError("proj rows must hold the q|k|v|z|a|b blocks")
     T = proj.shape[0]
     taps = conv.shape[-1]
     dev = proj.device

@@ -199,6 +199,41 @@ def test_batch_matches_single_sequences():
         assert normwise(backbone.backbone_last_hidden(model, ids[r], mask[r]), single[-1]) <= 1e-6
 
 
+def test_batch_trims_common_padding(monkeypatch):
+    """The batched hook drops the masked columns before every row's first kept
+    token (``native_sequence_start``, ``ext/QwenDecisionCoreAMDGPUExt.jl:17-24``;
+    ``ext/metal_batch_forward.jl:113-125``): each row's state equals the
+    single-sequence forward of its trimmed row, and stays within fp32 rounding
+    of the untrimmed one (leading masked tokens change no kept state, rotary
+    scores see relative positions only).  ``QDC_AMDGPU_TRIM_PADDING=0`` and
+    device inputs keep every column."""
+    from qdc_amd import backbone
+    from qdc_amd.config import plumbing_config
+    from qdc_amd.weights import random_weights
+    cfg = plumbing_config()
+    model = model_for(random_weights(cfg, seed=17), cfg)
+    ids = np.random.default_rng(18).integers(0, cfg.vocab, size=(3, 40))
+    mask = np.ones((3, 40), np.int64)
+    mask[0, :6] = 0
+    mask[1, :11] = 0
+    mask[2, :6] = 0
+    mask[2, 20::7] = 0
+    monkeypatch.delenv("QDC_AMDGPU_TRIM_PADDING", raising=False)
+    trimmed = backbone.batch_backbone_hidden(model, ids, mask)
+    monkeypatch.setenv("QDC_AMDGPU_TRIM_PADDING", "0")
+    whole = backbone.batch_backbone_hidden(model, ids, mask)
+    monkeypatch.delenv("QDC_AMDGPU_TRIM_PADDING")
+    on_dev = backbone.batch_backbone_hidden(model, torch.from_numpy(ids).cuda(),
+                                            torch.from_numpy(mask).cuda())
+    for r in range(3):
+        single_trim = backbone.backbone_hidden(model, ids[r, 6:], mask[r, 6:])[-1]
+        single = backbone.backbone_hidden(model, ids[r], mask[r])[-1]
+        assert normwise(trimmed[r], single_trim) <= 1e-6, r
+        assert normwise(trimmed[r], single) <= 1e-5, r
+        assert normwise(whole[r], single) <= 1e-6, r
+        assert normwise(on_dev[r], single) <= 1e-6, r
+
+
 def test_batch_validation():
     """The batched entry points reject what ``check_sequence`` rejects
     (``src/backbone.jl:413-422``): an id outside the vocabulary (device ids:

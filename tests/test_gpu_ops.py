@@ -1082,6 +1082,8 @@ PREP_CASES = [
     (3, 72, 8, 2, 128, 32, True, 5),       # fast path with an offset: partial K and V tiles
     (5, 8, 4, 2, 64, 16, True, 0),         # shortest bf16 fast path: one 8-token K and V tile
     (1, 4, 2, 1, 64, 16, False, 2),        # 4 tokens: fp32 fast path (bf16: general path)
+    (2, 136, 8, 2, 256, 64, True, 0),      # last K tile of 8 tokens: its second row batch empty
+    (2, 200, 4, 2, 512, 128, True, 1),     # 512-wide heads: two row batches of 32 tokens (bf16)
 ]
 
 

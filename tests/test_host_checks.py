@@ -244,3 +244,51 @@ def test_split_output_strides_checked(no_launch):
     merged = torch.empty((4, 36), dtype=BF16, device="meta")[:, :32]
     with pytest.raises(ValueError, match="multiple of 8"):
         ops.attention_gate(d(1, 2, 4, 8), d(4, 2, 8, dtype=BF16), out=merged, out_dtype=X2)
+
+
+def test_native_sequence_start(monkeypatch):
+    """The first kept token of a row (``ext/QwenDecisionCoreAMDGPUExt.jl:17-24``):
+    leading zeros are skipped, the last token always stays, and
+    ``QDC_AMDGPU_TRIM_PADDING`` other than "1" turns the trim off."""
+    import numpy as np
+    from qdc_amd.backbone import native_sequence_start
+    mask = np.array([[1, 1, 0, 1], [0, 0, 1, 1], [0, 0, 0, 0], [0, 0, 0, 1], [0, 1, 0, 1]])
+    monkeypatch.delenv("QDC_AMDGPU_TRIM_PADDING", raising=False)
+    assert [native_sequence_start(mask, r) for r in range(5)] == [0, 2, 3, 3, 1]
+    monkeypatch.setenv("QDC_AMDGPU_TRIM_PADDING", "1")
+    assert native_sequence_start(mask, 1) == 2
+    monkeypatch.setenv("QDC_AMDGPU_TRIM_PADDING", "0")
+    assert [native_sequence_start(mask, r) for r in range(5)] == [0] * 5
+
+
+def test_parameter_vectors_checked_before_launch(no_launch):
+    """Norm weights, RoPE tables and the DeltaNet parameters are read by the
+    kernels as contiguous vectors of a known length: a shorter or strided one,
+    or a table of the wrong width, dtype or device, raises ValueError before
+    the library is reached (the kernels would read past their ends)."""
+    tables = (d(8, 4), d(8, 4))
+    q, k, v = d(8, 2, 16), d(8, 1, 16), d(8, 1, 16)
+    proj = d(4, 3 * 16 + 16 + 4, dtype=BF16)
+    bad = [
+        lambda: ops.native_residual_rms(d(8, 16), d(8, 16), d(32)[::2], 1e-6),
+        lambda: ops.native_residual_rms(d(8, 16), d(8, 16), d(15), 1e-6),
+        lambda: ops.native_gated_rms(d(4, 2, 16, dtype=BF16), d(4, 2, 16, dtype=BF16),
+                                     d(8, dtype=BF16), 1e-6),
+        lambda: ops.native_gated_rms(d(4, 2, 16, dtype=BF16), d(4, 2, 16, dtype=BF16),
+                                     d(32, dtype=BF16)[::2], 1e-6),
+        lambda: ops.prepare_heads(q, k, d(8), d(16), tables, 8, 1e-6),
+        lambda: ops.prepare_heads(q, k, d(16), d(32)[::2], tables, 8, 1e-6),
+        lambda: ops.prepare_heads(q, k, d(16), d(16), (d(8, 3), d(8, 3)), 8, 1e-6),
+        lambda: ops.prepare_heads(q, k, d(16), d(16), (d(8, 4), d(7, 4)), 8, 1e-6),
+        lambda: ops.prepare_heads(q, k, d(16), d(16), (d(8, 4, dtype=BF16),) * 2, 8, 1e-6),
+        lambda: ops.prepare_heads(q, k, d(16), d(16), None, 8, 1e-6),
+        lambda: ops.attention_prepare(q, k, v, d(32)[::2], d(16), tables, 8, 1e-6, 2),
+        lambda: ops.attention_prepare(q, k, v, d(16), d(16), (d(8, 4), host(8, 4)), 8, 1e-6, 2),
+        lambda: ops.delta_prologue(proj, d(40, 4), d(2), d(2), 4, 1, 16, 2, 8),
+        lambda: ops.delta_prologue(proj, d(48, 4), d(3), d(2), 4, 1, 16, 2, 8),
+        lambda: ops.delta_prologue(proj, d(48, 4), d(2), d(4)[::2], 4, 1, 16, 2, 8),
+        lambda: ops.delta_prologue(d(4, 60, dtype=BF16), d(48, 4), d(2), d(2), 4, 1, 16, 2, 8),
+    ]
+    for i, call in enumerate(bad):
+        with pytest.raises(ValueError):
+            call()
