@@ -290,6 +290,11 @@ def test_gather_checks_and_device_ids():
     got = out.cpu().numpy()
     assert np.array_equal(got[0], exp[3]) and np.array_equal(got[2], exp[5])
     assert not got[1].any() and not got[3].any()
+    # without a flag (the kernel form with no atomic): the same rows, bf16 too
+    for t in (table, table.to(torch.bfloat16)):
+        out = ops.native_gather(t, ids).cpu()
+        assert torch.equal(out[0], t[3].cpu()) and torch.equal(out[2], t[5].cpu())
+        assert not out[1].any() and not out[3].any()
 
 
 def test_gather_widening_invalid_ids_mid_wavefront():
