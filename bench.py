@@ -505,6 +505,42 @@ def copy_ceilings(dev, kernels, steps, warmup):
     return {k.name: (by_name[f"copy_{k.name}"], by_name.get(f"rows_{k.name}")) for k in kernels}
 
 
+PAIR_ROUNDS = 3
+
+
+def paired_ratios(kernels, ceilings, rounds=PAIR_ROUNDS):
+    """Each kernel's graph replayed right before its ceilings' graphs (the
+    same-size copy, and the random-row copy where there is one), in `rounds`
+    rounds over all kernels: the median over rounds of ceiling time / kernel
+    time.  Back to back, a kernel and its ceiling run in the same clock and
+    memory state, which the separate timing phases above do not ensure."""
+    import torch
+    stream = torch.cuda.current_stream()
+    ratios = {k.name: ([], []) for k in kernels}
+    for _ in range(rounds):
+        marks = []
+        for k in kernels:
+            c, rows = ceilings[k.name]
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            ev[0].record(stream)
+            k.graph.replay()
+            ev[1].record(stream)
+            c.graph.replay()
+            ev[2].record(stream)
+            if rows is not None:
+                rows.graph.replay()
+            ev[3].record(stream)
+            marks.append((k, rows is not None, ev))
+        torch.cuda.synchronize()
+        for k, has_rows, ev in marks:
+            t_k = ev[0].elapsed_time(ev[1])
+            ratios[k.name][0].append(ev[1].elapsed_time(ev[2]) / t_k)
+            if has_rows:
+                ratios[k.name][1].append(ev[2].elapsed_time(ev[3]) / t_k)
+    med = lambda v: sorted(v)[len(v) // 2] if v else None  # noqa: E731
+    return {name: (med(a), med(b)) for name, (a, b) in ratios.items()}
+
+
 CALIB_BYTES = 512 << 20
 
 
@@ -986,6 +1022,7 @@ def main():
     ceilings = copy_ceilings(dev, hot + [k for k in fwd + alone + split if k not in hot],
                              args.steps, args.warmup)
     floors = empty_floors(hot, args.steps, args.warmup)
+    paired = paired_ratios([k for k in kernels if k.name in ceilings], ceilings)
     hot_ms = sum(k.avg_ms for k in hot) * args.steps
     step_bytes = sum(k.algo_bytes for k in hot)
     value = step_bytes * args.steps / (hot_ms / 1e3) / 1e9
@@ -1010,6 +1047,11 @@ def main():
                      ceiling_pct_peak=round(100 * rows.algo_bytes / (rows.avg_ms / 1e3) / 1e9
                                             / PEAK_GBS, 1),
                      pct_of_ceiling=round(100 * rows.avg_ms / k.avg_ms, 1))
+        pc, prow = paired.get(k.name, (None, None))
+        if pc is not None:  # the kernel and its ceilings replayed back to back
+            e.update(pct_of_copy_paired=round(100 * pc, 1))
+        if prow is not None:
+            e.update(pct_of_ceiling_paired=round(100 * prow, 1))
         f = floors.get(k.name)
         if f is not None:  # an empty launch of the same grid
             e.update(workgroups=k.workgroups, empty_us=round(f.avg_ms * 1e3, 3))
