@@ -1089,6 +1089,8 @@ PREP_CASES = [
     (1, 4, 2, 1, 64, 16, False, 2),        # 4 tokens: fp32 fast path (bf16: general path)
     (2, 136, 8, 2, 256, 64, True, 0),      # last K tile of 8 tokens: its second row batch empty
     (2, 200, 4, 2, 512, 128, True, 1),     # 512-wide heads: two row batches of 32 tokens (bf16)
+    (3, 40, 8, 2, 64, 16, True, 2),        # 8 heads: Q rows half staged through LDS
+    (2, 72, 16, 4, 128, 32, False, 0),     # 16 heads, q inside q||gate rows, staged Q rows
 ]
 
 
