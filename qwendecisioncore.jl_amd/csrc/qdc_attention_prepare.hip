@@ -215,8 +215,8 @@ __device__ __forceinline__ void v_tile(const PrepArgs<T> &a, int64_t index) {
 
 // Q, K and V workgroups are dealt through the grid in proportion (block i is a
 // Q block when floor((i+1)*nq/n) > floor(i*nq/n); the others split between K
-// and V the same way), so every role streams from the first wave of workgroups
-// to the last instead of one role trailing.
+// and V the same way, the K tiles over the first 3/4 of them), so every role
+// streams from the first wave of workgroups instead of one role trailing.
 template <typename T, int LPR, int RPGQ>
 __global__ __launch_bounds__(kBlock) void attention_prepare_fast(PrepArgs<T> a) {
     const int64_t i = blockIdx.x, n = a.q_blocks + a.k_blocks + a.v_blocks;
@@ -225,9 +225,14 @@ __global__ __launch_bounds__(kBlock) void attention_prepare_fast(PrepArgs<T> a) 
         qk_side_contig<T, LPR, RPGQ>(a.qk, a.qk.q, q_upto - 1);
         return;
     }
+    // K tiles, the longest workgroups, are dealt over the first 3/4 of the
+    // non-Q blocks only, so none starts in the launch's last stretch (2-3%
+    // faster at 8 x 2048 tokens than dealing them over all, 1/4-5/8 in between)
     const int64_t j = i - q_upto, m = a.k_blocks + a.v_blocks;
-    const int64_t k_upto = (j + 1) * a.k_blocks / m;
-    if (k_upto > j * a.k_blocks / m)
+    const int64_t mk = std::max<int64_t>(a.k_blocks, m * 3 / 4);
+    const int64_t jk = j < mk ? j : mk - 1;
+    const int64_t k_upto = j < mk ? (jk + 1) * a.k_blocks / mk : a.k_blocks;  // K among [0, j]
+    if (j < mk && k_upto > jk * a.k_blocks / mk)
         k_tile<T, LPR>(a, k_upto - 1);
     else
         v_tile<T, LPR>(a, j - k_upto);
