@@ -970,6 +970,243 @@ def traffic_source():
             "note": "counted by rocprofv3 --pmc in that profiling run of bench.py, not in this run"}
 
 
+# ------------------------------------------------- profile summaries ------
+def _dispatches(path, counter=None):
+    """rocprofv3 CSV rows in dispatch order: (signature, duration us, value)."""
+    import csv
+    out = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if counter is not None and r.get("Counter_Name") != counter:
+                continue
+            sig = (r["Kernel_Name"], int(r.get("Grid_Size") or r.get("Grid_Size_X")),
+                   int(r.get("Workgroup_Size") or r.get("Workgroup_Size_X")))
+            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            val = float(r["Counter_Value"]) if counter is not None else None
+            out.append((int(r["Dispatch_Id"]), sig, dur, val))
+    out.sort(key=lambda d: d[0])
+    return [d[1:] for d in out]
+
+
+def _runs(disp, steps):
+    """Consecutive dispatches of one signature, cut into runs of `steps` where
+    a run is a whole multiple of it (graph replays of adjacent kernels that
+    share a signature)."""
+    runs = []
+    for d in disp:
+        if runs and runs[-1][0][0] == d[0]:
+            runs[-1].append(d)
+        else:
+            runs.append([d])
+    out = []
+    for r in runs:
+        if len(r) > steps and len(r) % steps == 0:
+            out += [r[i:i + steps] for i in range(0, len(r), steps)]
+        else:
+            out.append(r)
+    return out
+
+
+def _find_passes(runs, names, steps, start=0):
+    """The untimed and timed replay passes of `names` (in order): the first
+    place from `start` where 2*len(names) runs of `steps` dispatches follow
+    one another with the second half repeating the first half's signatures.
+    Returns ({name: [untimed run, timed run]}, index after the passes)."""
+    n = len(names)
+    for i in range(start, len(runs) - 2 * n + 1):
+        block = runs[i:i + 2 * n]
+        if all(len(r) == steps for r in block) and \
+                all(block[j][0][0] == block[n + j][0][0] for j in range(n)):
+            return {name: [block[j], block[n + j]] for j, name in enumerate(names)}, i + 2 * n
+    raise RuntimeError(f"no replay passes of {n} kernels x {steps} launches found")
+
+
+def summarize_profiles(out_dir, commit):
+    """Write profiles/fused_kernels_trace_pmc.md, profiles/pmc_traffic.json,
+    profiles/launch_ceilings.md and profiles/kernel_stats_bench.txt from the
+    outputs of the three rocprofv3 runs named in PROFILE_COMMANDS under
+    `out_dir` (each bench run's stdout beside its rocprofv3 directory, its
+    stderr holding the timed order of the kernels)."""
+    import csv
+    import statistics
+
+    def bench_line(name):
+        with open(os.path.join(out_dir, name)) as f:
+            return json.loads([ln for ln in f if ln.startswith("{")][-1])
+
+    def order(name):
+        with open(os.path.join(out_dir, name)) as f:
+            return [ln.split(": ", 1)[1].strip().split(",") for ln in f
+                    if ln.startswith("timed order: ")][-1]
+
+    line = bench_line("prof_k_bench.json")
+    names = order("prof_k_bench.err")
+    fwd = line["forward_shapes"]
+    groups = {"hot": list(line["kernels"]), "fwd": list(fwd["kernels"]),
+              "alone": list(fwd.get("standalone", {}).get("kernels", {})),
+              "split": list(fwd.get("split_gemm_inputs", {}).get("kernels", {}))}
+    entry = {**line["kernels"], **line.get("widened", {}), **fwd["kernels"],
+             **fwd.get("standalone", {}).get("kernels", {}),
+             **fwd.get("split_gemm_inputs", {}).get("kernels", {})}
+    steps = line["steps"]
+    # the ceilings and floors in the order bench.py times them
+    ceil_names = []
+    for k in groups["hot"] + [k for g in ("fwd", "alone", "split") for k in groups[g]
+                              if k not in groups["hot"]]:
+        ceil_names.append("copy_" + k)
+        if "ceiling_us" in entry[k]:
+            ceil_names.append("rows_" + k)
+    floor_names = ["empty_" + k for k in groups["hot"] if "empty_us" in entry[k]]
+
+    runs = _runs(_dispatches(os.path.join(out_dir, "prof_k", "trace_kernel_trace.csv")), steps)
+    kp, nxt = _find_passes(runs, names, steps)
+    cp, nxt = _find_passes(runs, ceil_names, steps, nxt)
+    fp, _ = _find_passes(runs, floor_names, steps, nxt)
+    timed = {**{k: v[1] for k, v in kp.items()}, **{k: v[1] for k, v in cp.items()},
+             **{k: v[1] for k, v in fp.items()}}
+
+    # HBM traffic: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the two
+    # replay passes of the PMC runs, scaled by the calibration copies
+    traffic = {}
+    scale = {}
+    for counter, sub, stem in (("FETCH_SIZE", "pmc_fetch", "fetch"),
+                               ("WRITE_SIZE", "pmc_write", "write")):
+        disp = _dispatches(os.path.join(out_dir, sub, f"{stem}_counter_collection.csv"), counter)
+        calib = [d for d in disp[:40] if "copyBuffer" in d[0][0]]
+        counted = sum(d[2] for d in calib) * 1024
+        scale[counter] = 4 * CALIB_BYTES / counted if counted else 1.0
+        pl = bench_line(f"{sub}_bench.json")
+        pruns = _runs(disp, pl["steps"])
+        pp, _ = _find_passes(pruns, order(f"{sub}.err"), pl["steps"])
+        for k, (a, b) in pp.items():
+            traffic.setdefault(k, {})[counter] = statistics.median(
+                [d[2] for d in a + b]) * 1024 * scale[counter]
+
+    pmc = {"source": "profiles/fused_kernels_trace_pmc.md", "commit": commit,
+           "commands": [c.replace("$R/", "") for c in PROFILE_COMMANDS],
+           "scale_fetch": scale["FETCH_SIZE"], "scale_write": scale["WRITE_SIZE"],
+           "kernels": {}}
+    rows = []
+    for k in names:
+        e = entry[k]
+        durs = [d[1] for d in timed[k]]
+        avg, mn = sum(durs) / len(durs), min(durs)
+        t = traffic.get(k, {})
+        rd, wr = t.get("FETCH_SIZE"), t.get("WRITE_SIZE")
+        if rd is not None and wr is not None:
+            pmc["kernels"][k] = {"hbm_bytes_per_launch": int(rd + wr), "read_bytes": int(rd),
+                                 "write_bytes": int(wr), "avg_us_trace": round(avg, 3)}
+        gbs = e["bytes"] / avg / 1e3
+        rows.append(f"| {k} | {e.get('launches_per_forward', '')} | {avg:.2f} | {mn:.2f} | "
+                    f"{e['us']:.2f} | {e['bytes'] / 1e6:.2f} | "
+                    + (f"{rd / 1e6:.2f} | {wr / 1e6:.2f} | {(rd + wr) / e['bytes']:.3f} | "
+                       if rd is not None and wr is not None else " |  |  | ")
+                    + f"{gbs:.0f} | {100 * gbs / PEAK_GBS:.1f} |")
+    with open(os.path.join(ROOT, "profiles", "pmc_traffic.json"), "w") as f:
+        json.dump(pmc, f, indent=1)
+        f.write("\n")
+    cmds = "\n".join(PROFILE_COMMANDS)
+    with open(os.path.join(ROOT, "profiles", "fused_kernels_trace_pmc.md"), "w") as f:
+        f.write(f"""# Fused row kernels and widened kernels: rocprofv3 kernel trace and HBM traffic (bench.py shapes)
+
+Workload: `bench.py` kernel benchmark (each kernel at its benchmark shape, {steps} steps per kernel
+captured in a HIP graph, rotating buffer sets > 640 MB per kernel). The rows follow the bench's
+timed order: the fused row kernels at their per-kernel benchmark shapes, the widened kernels
+(attention softmax and gate merge, DeltaNet prologue and recurrence), then the `fwd_*` rows, the
+fused row kernels exactly as one forward of the 0.8B-like backbone launches them (8 x 2048 tokens;
+"per fwd" = launches per forward), the two launches `fwd_gather_rms_bf16` fuses, at the same shapes
+(not launched by the forward), and the split-output kernels of the split-GEMM-input forward.
+
+Commands (run from `/tmp` with `TMPDIR=/tmp`, `$R` = repository root), commit {commit}; each
+bench run's stdout and stderr saved beside its rocprofv3 directory, then
+`python bench.py --summarize-profiles $R/gpurun_out --commit {commit}` wrote this file,
+`pmc_traffic.json`, `launch_ceilings.md` and `kernel_stats_bench.txt`:
+
+```
+{cmds}
+```
+
+Counter calibration: `--calibrate` runs four 512 MiB device copies (`__amd_rocclr_copyBuffer`);
+FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled so that those copies read and write
+their bytes: fetch x {scale['FETCH_SIZE']:.4f}, write x {scale['WRITE_SIZE']:.4f}. Per-kernel counter values
+are the median over the kernel's dispatches in the two graph replays of its PMC run; trace
+durations are the {steps} launches of the timed replay; "bench us" is the HIP-event average of the
+traced bench run (it includes the graph's gap between nodes).
+
+| kernel (bench name) | per fwd | avg us (trace) | min us | bench us | algorithmic MB | HBM read MB | HBM write MB | traffic / algorithmic | GB/s (algo / avg) | % of 8 TB/s |
+|---|---|---|---|---|---|---|---|---|---|---|
+""" + "\n".join(rows) + "\n")
+
+    # single-launch ceilings, from the same trace
+    def avg(name):
+        r = timed.get(name)
+        return None if r is None else sum(d[1] for d in r) / len(r)
+
+    lrows = []
+    for k in groups["hot"] + [k for g in ("fwd", "alone", "split") for k in groups[g]
+                              if k not in groups["hot"]]:
+        e = entry[k]
+        ku, cu, ru, eu = avg(k), avg("copy_" + k), avg("rows_" + k), avg("empty_" + k)
+        wg = timed[k][0][0][1] // timed[k][0][0][2]
+        cwg = timed["copy_" + k][0][0][1] // timed["copy_" + k][0][0][2]
+        kb, cb = e["bytes"], (e["bytes"] // 2) // 16 * 16 * 2
+        lrows.append(f"| {k} | {kb / 1e6:.1f} | {wg} | {ku:.2f} | {cu:.2f} | {cwg} | "
+                     f"{'' if ru is None else f'{ru:.2f}'} | {'' if eu is None else f'{eu:.2f}'} | "
+                     f"{100 * kb / ku / 1e3 / PEAK_GBS:.1f} | {100 * cb / cu / 1e3 / PEAK_GBS:.1f} | "
+                     f"{100 * (kb / ku) / (cb / cu):.1f} | "
+                     f"{e.get('pct_of_copy_paired', '')} | {e.get('pct_of_ceiling_paired', '')} |")
+    with open(os.path.join(ROOT, "profiles", "launch_ceilings.md"), "w") as f:
+        f.write(f"""# Single-launch ceilings: each fused kernel beside a copy of its bytes and an empty launch of its grid
+
+Same trace as `fused_kernels_trace_pmc.md` (commit {commit}; command there). Every row is the
+average over the {steps} launches of a timed graph replay, from the trace's own timestamps. For each
+kernel the same run times, in the same way:
+
+- `qdc_copy` of the kernel's algorithmic bytes, half read and half written, one 16-byte chunk
+  per thread with nontemporal loads and stores;
+- for the gathers, `qdc_copy_rows`: the same table, the same number of rows read at uniformly
+  random places and written contiguously 1, 2 or 3 times (the gather's access pattern and bytes);
+- for the per-kernel configurations of the RMSNorm family and the q/k kernel, `qdc_empty` over
+  the kernel's own grid (workgroups of 256 threads that do nothing): the fixed cost of the launch.
+
+The last two columns are the bench line's paired ratios of the same run: the kernel's graph
+replayed right before its ceilings' graphs, median of three rounds (HIP events; ceiling time /
+kernel time).
+
+| kernel | MB | workgroups | kernel us | copy us | copy workgroups | random-row copy us | empty us (same grid) | kernel % of 8 TB/s | copy % of 8 TB/s | kernel % of copy | paired % of copy | paired % of random-row copy |
+|---|---|---|---|---|---|---|---|---|---|---|---|---|
+""" + "\n".join(lrows) + "\n")
+
+    # rocprofv3 --stats of the library's kernels
+    with open(os.path.join(out_dir, "prof_k", "trace_kernel_stats.csv"), newline="") as f:
+        st = [r for r in csv.DictReader(f) if "qdc::" in r["Name"]]
+    with open(os.path.join(ROOT, "profiles", "kernel_stats_bench.txt"), "w") as f:
+        f.write(f"""rocprofv3 --kernel-trace --stats summary (kernel_stats.csv) of the bench kernel run, library kernels only
+Command (from /tmp with TMPDIR=/tmp, $R = repository root), commit {commit}:
+  {PROFILE_COMMANDS[0]}
+Averages cover every call of a symbol (warmup, eager checks and graph replays; a symbol shared by
+several shapes averages them all). The per-shape timed-replay averages are in
+fused_kernels_trace_pmc.md; copy_chunks, copy_rows<R> and empty_grid are the benchmark's ceilings
+(launch_ceilings.md); "% time" is of all kernels in the run.
+
+calls    avg us    min us    max us % time  kernel
+""")
+        for r in st:
+            f.write(f"{int(r['Calls']):5d} {float(r['AverageNs']) / 1e3:9.2f} "
+                    f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} "
+                    f"{float(r['Percentage']):6.2f}  {r['Name'][:150]}\n")
+
+
+PROFILE_COMMANDS = [
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_k -o trace "
+    "-- python -u $R/bench.py --no-cpu --no-e2e",
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_fetch -o fetch "
+    "-- python -u $R/bench.py --no-cpu --no-e2e --steps 2 --warmup 1 --calibrate",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_write -o write "
+    "-- python -u $R/bench.py --no-cpu --no-e2e --steps 2 --warmup 1 --calibrate",
+]
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -984,7 +1221,13 @@ def main():
                     help="run only the single-sequence last-token latency run (profiling runs)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 4 plain 512 MiB device copies (scales the PMC byte counters)")
+    ap.add_argument("--summarize-profiles", metavar="DIR", default="",
+                    help="write the profiles/ summaries from rocprofv3 outputs under DIR (no GPU)")
+    ap.add_argument("--commit", default="", help="commit the profiled tree was at (summaries)")
     args = ap.parse_args()
+    if args.summarize_profiles:
+        summarize_profiles(args.summarize_profiles, args.commit)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(the row kernels need no exchange; see the sharding notes)", file=sys.stderr)
@@ -1010,6 +1253,8 @@ def main():
     for i in range(args.warmup):
         for k in kernels:
             k.run(i)
+    # the order of the timed graph replays, for matching a rocprofv3 trace
+    print("timed order: " + ",".join(k.name for k in kernels), file=sys.stderr, flush=True)
     capture(kernels, args.steps)
     check_replay(kernels, args.steps)
     for k in kernels:  # one untimed replay
