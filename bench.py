@@ -1197,6 +1197,183 @@ calls    avg us    min us    max us % time  kernel
                     f"{float(r['Percentage']):6.2f}  {r['Name'][:150]}\n")
 
 
+def _kernel_label(name, gemm="hipBLASLt GEMM"):
+    """A table label for a traced kernel: the library's kernels by function
+    name, Tensile GEMMs by their output type, the runtime's copy kernels."""
+    import re
+    m = re.search(r"qdc::\(anonymous namespace\)::(\w+)", name)
+    if m:
+        return f"`{m.group(1)}`"
+    if name.startswith("Cijk_"):
+        code = name.split("_")[3]
+        out = {"B": "bf16", "S": "fp32", "H": "fp16"}.get(code[1:2], code) if len(code) == 3 else None
+        return f"{gemm} {out} out" if out else f"{gemm}s (Tensile kernels of the kept library)"
+    if "copyBuffer" in name:
+        return "runtime copy"
+    m = re.search(r"at::native::(?:\(anonymous namespace\)::)?(\w+)", name)
+    return f"torch `{m.group(1)}`" if m else name[:40]
+
+
+def _trace_rows(path):
+    import csv
+    with open(path, newline="") as f:
+        rows = list(csv.DictReader(f))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    grid = "Grid_Size_X" if "Grid_Size_X" in rows[0] else "Grid_Size"
+    return [(r["Kernel_Name"], int(r[grid]), int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+            for r in rows]
+
+
+def _kernel_table(segments, per, gemm="hipBLASLt GEMM", unit_ms=True):
+    """Markdown rows: label, launches and time per forward (summed over the
+    segments, divided by `per`; ms with the share of kernel time, or µs), and
+    the total kernel time per forward in ms."""
+    from collections import OrderedDict
+    acc = OrderedDict()
+    for seg in segments:
+        for name, _, t0, t1 in seg:
+            label = _kernel_label(name, gemm)
+            n, t = acc.get(label, (0, 0))
+            acc[label] = (n + 1, t + (t1 - t0))
+    total = sum(t for _, t in acc.values())
+    out = []
+    for label, (n, t) in sorted(acc.items(), key=lambda kv: -kv[1][1]):
+        if unit_ms:
+            out.append(f"| {label} | {n // per} | {t / per / 1e6:.3f} | {100 * t / total:.1f}% |")
+        else:
+            out.append(f"| {label} | {n // per} | {t / per / 1e3:.1f} |")
+    return out, total / per / 1e6
+
+
+def summarize_forward(out_dir, commit):
+    """Write profiles/backbone_forward_kernels.md, split_gemm_inputs_forward.md
+    and decision_latency_kernels.md from the end-to-end and decision traces
+    under `out_dir` (FORWARD_COMMANDS) and the untraced bench line of the same
+    commit in `out_dir`/bench.log."""
+    rows = _trace_rows(os.path.join(out_dir, "prof_e2e", "e2e_kernel_trace.csv"))
+    starts = [i for i, r in enumerate(rows) if "gather_rms" in r[0]]
+    untraced = json.loads([ln for ln in open(os.path.join(out_dir, "bench.log"))
+                           if ln.startswith("{")][-1])
+    b = untraced["backbone"]
+    modes = [("all-bf16 storage", starts[0:5], b["ms_per_forward"]),
+             ("all", starts[4:9], b["split_gemm_inputs"]["all"]["ms_per_forward"]),
+             ("mlp", starts[8:13], b["split_gemm_inputs"]["mlp"]["ms_per_forward"])]
+    cmd = FORWARD_COMMANDS[0]
+    tables = {}
+    for mode, st, ms in modes:
+        # the first and second timed forwards (after one warm-up forward)
+        segs = [rows[st[1]:st[2]], rows[st[2]:st[3]]]
+        t, busy = _kernel_table(segs, 2)
+        span = sum((s[-1][3] - s[0][2]) for s in segs) / 2 / 1e6
+        tables[mode] = (t, busy, span, ms)
+    hdr = "| kernel | launches / forward | ms / forward | share of kernel time |\n|---|---|---|---|\n"
+    t, busy, span, ms = tables["all-bf16 storage"]
+    with open(os.path.join(ROOT, "profiles", "backbone_forward_kernels.md"), "w") as f:
+        f.write(f"""# backbone_hidden forward: per-kernel time (random-init Qwen3.5-0.8B-like, bf16, 8 x 2048 tokens)
+
+Command (run from `/tmp` with `TMPDIR=/tmp`, `$R` = repository root), commit {commit}; then
+`python bench.py --summarize-forward $R/gpurun_out --commit {commit}` (with the untraced bench line
+of the same commit in `gpurun_out/bench.log`) wrote this file, `split_gemm_inputs_forward.md` and
+`decision_latency_kernels.md`:
+
+```
+{cmd}
+```
+
+The trace covers the whole run; the table sums the kernels of the first and second timed
+forwards of `bench.py`'s end-to-end benchmark (each forward starts with its one gather launch,
+the gather fused with the first input norm) and divides by two. 24 layers: 18 DeltaNet + 6 full
+attention, hidden 1024, 16384 tokens per forward. GEMMs are labelled by the output type of their
+Tensile kernel. The same run continues with the split-GEMM-input modes, summarised in
+`split_gemm_inputs_forward.md`.
+
+forward span {span:.3f} ms, kernels busy {busy:.3f} ms under the tracer; untraced, the bench line of
+the same commit gives {ms:.3f} ms per forward
+
+""" + hdr + "\n".join(t) + """
+
+`rms_rows_fast` covers 47 residual + next-norm launches (fp32 residual stream, bf16 output), the
+18 DeltaNet gated norms and the residual + final norm (fp32).
+""")
+    with open(os.path.join(ROOT, "profiles", "split_gemm_inputs_forward.md"), "w") as f:
+        f.write(f"""# backbone_hidden forward with split GEMM inputs: per-kernel time (random-init Qwen3.5-0.8B-like, bf16 weights, 8 x 2048 tokens)
+
+Command (run from `/tmp` with `TMPDIR=/tmp`, `$R` = repository root), commit {commit} -- the same
+run as `backbone_forward_kernels.md`:
+
+```
+{cmd}
+```
+
+`bench.py`'s end-to-end benchmark runs the same weights and tokens in all-bf16 storage, then
+`split_gemm_inputs="all"` (every GEMM input written as two bf16 terms; projection weights with
+their input rows repeated, twice the inner dimension), then `"mlp"` (only the MLP's two inputs
+split), one warm-up and three timed forwards each. Each table sums the kernels of the first and
+second timed forwards of its mode and divides by two. In both split modes the MLP gate/up GEMM
+writes fp32 and SwiGLU reads it, so `swiglu_fast` moves 704 MB per launch instead of 352 MB. The
+split-output kernels alone, at these shapes beside their copy ceilings and with counted HBM
+traffic, are in `fused_kernels_trace_pmc.md` and `launch_ceilings.md` (`fwd_*_split`).
+""")
+        for mode in ("all", "mlp", "all-bf16 storage"):
+            t, busy, span, ms = tables[mode]
+            f.write(f"""
+## {mode}: forward span {span:.3f} ms, kernels busy {busy:.3f} ms (untraced: {ms:.3f} ms)
+
+""" + hdr + "\n".join(t) + "\n")
+
+    # decision latency: the last graph replay of each length
+    rows = _trace_rows(os.path.join(out_dir, "prof_dec", "dec_kernel_trace.csv"))
+    starts = [i for i, r in enumerate(rows) if "gather_rms" in r[0]]
+    segs = {}
+    for j, i in enumerate(starts):
+        a = i - 1 if i > 0 and "copyBuffer" in rows[i - 1][0] else i   # the ids copied in
+        end = starts[j + 1] - 1 if j + 1 < len(starts) else len(rows)
+        if end > a and "copyBuffer" not in rows[end - 1][0] and j + 1 < len(starts):
+            end += 1  # the next start has no copy-in of its own
+        segs[rows[i][1]] = rows[a:end]  # keyed by the gather's grid: one per length
+    d = untraced["decision"]
+    lengths = sorted(d["graph_ms"], key=int)
+    with open(os.path.join(ROOT, "profiles", "decision_latency_kernels.md"), "w") as f:
+        f.write(f"""# Single-sequence last-token latency: kernels of one graph replay per length
+
+Workload: `bench.py --decision-only`, the reference's inference benchmark protocol
+(`benchmark/inference.jl`) on its synthetic model's shapes (`benchmark/synthetic.jl`: 4 layers,
+3 DeltaNet + 1 full attention, hidden 256, intermediate 512, fp32): `backbone_last_hidden` of one
+sequence of 64, 128, 256 and 512 tokens served from recorded HIP graphs (`qdc_amd.graphs`).
+
+Command (run from `/tmp` with `TMPDIR=/tmp`, `$R` = repository root), commit {commit}; summary as in
+`backbone_forward_kernels.md`:
+
+```
+{FORWARD_COMMANDS[1]}
+```
+
+Each table is the last graph replay of its length. "Kernel µs" sums the kernel durations in the
+trace; the untraced median per call of the same commit (`bench.py`'s decision section: the
+host-to-device copy of the ids, the graph launch, the kernels, the device-to-host copy of the
+result and the stream synchronisation) is in each heading. GEMM library kept per length:
+{d.get("graph_gemm_library")} ("cublas" is rocBLAS, "cublaslt" hipBLASLt, in torch's names).
+""")
+        for n, grid in zip(lengths, sorted(segs)):
+            seg = segs[grid]
+            t, busy = _kernel_table([seg], 1, gemm="GEMM", unit_ms=False)
+            t = [ln.replace("| runtime copy |", "| runtime copy (ids in, result out) |") for ln in t]
+            f.write(f"""
+## {n} tokens: {len(seg)} kernels, {busy * 1e3:.1f} kernel µs (untraced: {d["graph_ms"][n] * 1e3:.0f} µs per call)
+
+| kernel | launches | µs |
+|---|---|---|
+""" + "\n".join(t) + "\n")
+
+
+FORWARD_COMMANDS = [
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_e2e -o e2e "
+    "-- python -u $R/bench.py --no-cpu --only swiglu_bf16 --steps 2 --warmup 1",
+    "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_dec -o dec "
+    "-- python -u $R/bench.py --decision-only --no-cpu",
+]
+
+
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/prof_k -o trace "
     "-- python -u $R/bench.py --no-cpu --no-e2e",
@@ -1223,10 +1400,15 @@ def main():
                     help="first run 4 plain 512 MiB device copies (scales the PMC byte counters)")
     ap.add_argument("--summarize-profiles", metavar="DIR", default="",
                     help="write the profiles/ summaries from rocprofv3 outputs under DIR (no GPU)")
+    ap.add_argument("--summarize-forward", metavar="DIR", default="",
+                    help="write the forward and decision-latency summaries from traces under DIR")
     ap.add_argument("--commit", default="", help="commit the profiled tree was at (summaries)")
     args = ap.parse_args()
     if args.summarize_profiles:
         summarize_profiles(args.summarize_profiles, args.commit)
+        return
+    if args.summarize_forward:
+        summarize_forward(args.summarize_forward, args.commit)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "

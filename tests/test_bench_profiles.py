@@ -42,3 +42,14 @@ def test_find_passes_with_a_shared_signature_and_failure():
     assert set(passes) == {"k1", "k2"}
     with pytest.raises(RuntimeError):
         bench._find_passes(bench._runs(_d("a", 5), steps), ["k1"], steps)
+
+
+def test_kernel_labels():
+    """Trace kernel names as the forward tables label them."""
+    assert bench._kernel_label("void qdc::(anonymous namespace)::rms_rows_fast<float>(x)") == \
+        "`rms_rows_fast`"
+    assert bench._kernel_label("Cijk_Ailk_Bljk_BBS_BH_Bias_HA_S_SAV") == "hipBLASLt GEMM bf16 out"
+    assert bench._kernel_label("Cijk_Ailk_Bljk_BSS_BH_Bias_S_HA") == "hipBLASLt GEMM fp32 out"
+    assert bench._kernel_label("Cijk_Ailk_Bljk_SB_MT32x32x64", "GEMM") == \
+        "GEMMs (Tensile kernels of the kept library)"
+    assert bench._kernel_label("__amd_rocclr_copyBuffer") == "runtime copy"
