@@ -411,7 +411,7 @@ int32_t launch(void *out, const void *table, const int32_t *ids, int64_t n_ids, 
 
 using namespace qdc;
 
-extern "C" const char *qdc_version(void) { return "qdc_hip 0.1.0"; }
+extern "C" const char *qdc_version(void) { return QDC_HIP_VERSION; }
 
 extern "C" const char *qdc_status_string(int32_t status) {
     switch (status) {

@@ -45,10 +45,23 @@ const QDC_LOCK = ReentrantLock()
 
 qdc_library_path() = get(ENV, "QDC_HIP_LIBRARY", "libqdc_hip.so")
 
+# QDC_HIP_VERSION of the header these bindings follow; a library built from
+# another header is refused at load, since a changed signature would pass its
+# arguments in the wrong slots without any error.
+const QDC_HIP_VERSION = "qdc_hip 0.2.0"
+
+function qdc_open()
+    handle = Libdl.dlopen(qdc_library_path())
+    built = unsafe_string(ccall(Libdl.dlsym(handle, :qdc_version), Cstring, ()))
+    built == QDC_HIP_VERSION ||
+        error("$(qdc_library_path()) is $built; these bindings need $QDC_HIP_VERSION")
+    return handle
+end
+
 function qdc_sym(name::Symbol)
     lock(QDC_LOCK) do
         get!(QDC_SYMBOLS, name) do
-            QDC_HANDLE[] == C_NULL && (QDC_HANDLE[] = Libdl.dlopen(qdc_library_path()))
+            QDC_HANDLE[] == C_NULL && (QDC_HANDLE[] = qdc_open())
             Libdl.dlsym(QDC_HANDLE[], name)
         end
     end
@@ -377,10 +390,15 @@ function amdgpu_delta_attention(attention, x::AMDGPU.ROCArray{Float32,2,ROCBuffe
     return QwenDecisionCore.native_linear(attention.out, gated)
 end
 
+# qdc_delta_scan keeps a key row per lane group in registers up to 256 wide; a
+# wider key head is refused here rather than sent to a generic AMDGPU.jl path
+# (the reference's ext/amdgpu_delta.jl:121-128 falls back to `invoke`).
+check_key_dim(cfg) = cfg.key_dim <= 256 ||
+    throw(ArgumentError("The HIP DeltaNet path supports key_dim <= 256, got $(cfg.key_dim)."))
+
 function QwenDecisionCore.delta_attention(attention, x::AMDGPU.ROCArray{Float32,2,ROCBuffer},
                                           mask, cfg)
-    cfg.key_dim <= 256 || return invoke(QwenDecisionCore.delta_attention,
-                                        Tuple{Any,Any,Any,Any}, attention, x, mask, cfg)
+    check_key_dim(cfg)
     # called directly with an unmasked input (the layer loops below never do)
     device_mask = mask isa AMDGPU.ROCArray ? mask : QwenDecisionCore.native_prepare_mask(x, mask)
     masked = scratch(Float32, size(x))
@@ -392,7 +410,7 @@ end
 function QwenDecisionCore.native_delta_attention(attention,
                                                  x::AMDGPU.ROCArray{Float32,2,ROCBuffer}, mask,
                                                  cfg, ::Val{true})
-    cfg.key_dim <= 256 || return QwenDecisionCore.delta_attention(attention, x, mask, cfg)
+    check_key_dim(cfg)
     return amdgpu_delta_attention(attention, x, cfg)
 end
 

@@ -145,3 +145,37 @@ def test_checker_catches_a_changed_signature(mutation, monkeypatch):
     monkeypatch.setattr(__import__(__name__), "header_prototypes", lambda: protos)
     with pytest.raises(AssertionError):
         test_every_ccall_matches_the_header()
+
+
+def _fallbacks(code: str) -> list:
+    """Places where an overriding method hands its work to another method of the
+    same function instead of the library: ``invoke(...)`` (the generic method)
+    and a short-circuit ``|| return QwenDecisionCore.f(...)``."""
+    pats = (r"\binvoke\s*\(", r"\|\|\s*return\s+(?:QwenDecisionCore\.)?\w+\s*\(")
+    return [code[m.start():m.start() + 60] for p in pats for m in re.finditer(p, code)]
+
+
+def test_shim_has_no_generic_fallback():
+    """No in-scope operator of the shim falls back to a generic AMDGPU.jl method;
+    unsupported shapes raise instead."""
+    code = _julia_code(open(SHIM).read())
+    assert _fallbacks(code) == []
+    assert "throw(ArgumentError" in code
+
+
+@pytest.mark.parametrize("planted", [
+    "cfg.key_dim <= 256 || return invoke(QwenDecisionCore.delta_attention,\n"
+    "    Tuple{Any,Any,Any,Any}, attention, x, mask, cfg)\n",
+    "cfg.key_dim <= 256 || return QwenDecisionCore.delta_attention(attention, x, mask, cfg)\n",
+])
+def test_fallback_check_catches_a_planted_fallback(planted):
+    code = _julia_code(open(SHIM).read() + planted)
+    assert _fallbacks(code)
+
+
+def test_shim_version_is_the_header_version():
+    """The shim refuses a library built from another header: its constant must be
+    the header's QDC_HIP_VERSION."""
+    header = re.search(r'#define\s+QDC_HIP_VERSION\s+"([^"]+)"', open(HEADER).read()).group(1)
+    shim = re.search(r'const QDC_HIP_VERSION = "([^"]+)"', open(SHIM).read()).group(1)
+    assert shim == header
