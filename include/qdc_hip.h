@@ -63,7 +63,16 @@ typedef enum {
     QDC_ERR_ALIAS = -5        /* an output overlaps an input it may not alias */
 } qdc_status;
 
-/* Library version string ("qdc_hip <major>.<minor>.<patch>"). */
+/*
+ * Version of this header; qdc_version() returns the same string for the
+ * library that was built from it, so a host can refuse a library whose entry
+ * points it was not compiled against.  The minor number changes with any
+ * signature change of an existing entry point (0.2.0: qdc_gated_rmsnorm and
+ * qdc_swiglu take out_dtype before the stream).
+ */
+#define QDC_HIP_VERSION "qdc_hip 0.2.0"
+
+/* Library version string ("qdc_hip <major>.<minor>.<patch>"), QDC_HIP_VERSION. */
 const char *qdc_version(void);
 /* Human-readable text for a status returned by any entry point. */
 const char *qdc_status_string(int32_t status);
@@ -241,7 +250,11 @@ int32_t qdc_qk_norm_rope_batched(void *q_out, void *k_out, const void *q_in, con
  * per query head, since the heads/kv_heads query heads of KV head g are the
  * rows of one [heads/kv_heads * seq_len, head_dim] block of q_out.  heads a
  * multiple of kv_heads; tables as qdc_qk_norm_rope (pos_offset + seq_len <=
- * table_len); outputs may not overlap each other or an input.
+ * table_len); outputs may not overlap each other or an input.  heads = 0
+ * prepares K and V only (q_out, q_in and q_norm are then unused and may be
+ * NULL): the keys and values over a whole context for a query projected
+ * apart, as the final-query attention of the last-token forward does
+ * (cpu_final_full_attention, src/backbone_cpu.jl:984-1034).
  */
 int32_t qdc_attention_prepare(void *q_out, void *k_out, void *v_out, const void *q_in,
                               const void *k_in, const void *v_in, const void *q_norm,

@@ -346,7 +346,7 @@ int32_t prepare(void *q_out, void *k_out, void *v_out, const void *q_in, const v
                 int64_t table_len, int64_t q_in_tok, int64_t q_in_head, int64_t k_in_tok,
                 int64_t v_in_tok, float eps, int32_t dtype, hipStream_t stream) {
     if (!valid_dtype(dtype)) return QDC_ERR_DTYPE;
-    if (batch < 0 || seq < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || dim <= 0 ||
+    if (batch < 0 || seq < 0 || heads < 0 || kv_heads <= 0 || heads % kv_heads || dim <= 0 ||
         rotary_dim < 0 || rotary_dim % 2 || rotary_dim > dim || pos_offset < 0 || table_len < 0)
         return QDC_ERR_SHAPE;
     const int64_t tokens = batch * seq;
@@ -354,20 +354,23 @@ int32_t prepare(void *q_out, void *k_out, void *v_out, const void *q_in, const v
     if (dim > INT32_MAX || tokens * (heads + 2 * kv_heads) >= ((int64_t)1 << 26))
         return QDC_ERR_SHAPE;
     if (tokens == 0) return QDC_OK;
-    if (!q_out || !k_out || !v_out || !q_in || !k_in || !v_in || !q_norm || !k_norm)
-        return QDC_ERR_NULL;
+    // heads == 0: K and V only (the q pointers are not used and may be NULL)
+    if (!k_out || !v_out || !k_in || !v_in || !k_norm) return QDC_ERR_NULL;
+    if (heads > 0 && (!q_out || !q_in || !q_norm)) return QDC_ERR_NULL;
     if (rotary_dim > 0) {
         if (!cos_table || !sin_table) return QDC_ERR_NULL;
         if (pos_offset + seq > table_len) return QDC_ERR_RANGE;
     }
     // input rows must not overlap (tokens and heads), strides non-negative
     if (q_in_tok < 0 || q_in_head < 0 || k_in_tok < 0 || v_in_tok < 0) return QDC_ERR_SHAPE;
-    if ((heads > 1 && q_in_head < dim) || (tokens > 1 && q_in_tok < (heads - 1) * q_in_head + dim) ||
+    if ((heads > 1 && q_in_head < dim) ||
+        (heads > 0 && tokens > 1 && q_in_tok < (heads - 1) * q_in_head + dim) ||
         (tokens > 1 && (k_in_tok < kv_heads * dim || v_in_tok < kv_heads * dim)))
         return QDC_ERR_SHAPE;
     const int64_t es = elem_size(dtype);
     const int64_t q_bytes = tokens * heads * dim * es, kv_bytes = tokens * kv_heads * dim * es;
-    const int64_t qi_bytes = ((tokens - 1) * q_in_tok + (heads - 1) * q_in_head + dim) * es;
+    const int64_t qi_bytes =
+        heads > 0 ? ((tokens - 1) * q_in_tok + (heads - 1) * q_in_head + dim) * es : 0;
     const int64_t ki_bytes = ((tokens - 1) * k_in_tok + kv_heads * dim) * es;
     const int64_t vi_bytes = ((tokens - 1) * v_in_tok + kv_heads * dim) * es;
     const struct { const void *p; int64_t n; } outs[3] = {{q_out, q_bytes}, {k_out, kv_bytes},
@@ -397,7 +400,7 @@ int32_t prepare(void *q_out, void *k_out, void *v_out, const void *q_in, const v
             PrepArgs<T> a{};
             a.qk.q = Side<T>{(const T *)q_in, (T *)q_out, (const T *)q_norm, q_in_tok, q_in_head,
                              dim, seq * dim, heads * seq * dim, tokens * heads,
-                             make_fastdiv((uint32_t)heads)};
+                             make_fastdiv((uint32_t)std::max<int64_t>(heads, 1))};
             a.qk.cos = cos_table;
             a.qk.sin = sin_table;
             a.qk.seq_len = make_fastdiv((uint32_t)seq);

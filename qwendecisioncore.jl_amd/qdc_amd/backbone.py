@@ -203,9 +203,10 @@ class QwenBackbone:
         means every token is kept (no masking work is done).
 
         ``last_only`` returns ``[B, hidden]``, the last position of each row:
-        after the last attention block only those rows go through the last MLP
-        and the final norm (the last-token forward ``native_hidden_forward``,
-        ``src/backbone.jl:390-396``).  ``error_flag`` (device int32, cleared by
+        a full-attention last layer attends from each row's last query only
+        (:meth:`_final_query_attention`), and after the last attention block only
+        those rows go through the last MLP and the final norm (the last-token
+        forward ``native_hidden_forward``, ``src/backbone.jl:390-396``).  ``error_flag`` (device int32, cleared by
         the caller) is set by the gather when an id is outside the vocabulary."""
         B, S = ids.shape
         cfg = self.cfg
@@ -221,14 +222,20 @@ class QwenBackbone:
                                           token_mask=delta_keep(0), error_flag=error_flag,
                                           normed_dtype=self.gemm_in)
         for i, layer in enumerate(self.layers):
-            if layer["kind"] == "full_attention":
+            last = i + 1 == len(self.layers)
+            # the last-token forward's last attention layer attends from the
+            # last query only (its attention output comes back as [B, hidden])
+            final_query = last and last_only and layer["kind"] == "full_attention"
+            if final_query:
+                mixed = self._final_query_attention(layer, normed, mask32, B, S)
+            elif layer["kind"] == "full_attention":
                 mixed = self._full_attention(layer, normed, mask32, B, S)
             else:
                 mixed = self._delta_attention(layer, normed, B, S)
-            last = i + 1 == len(self.layers)
             if last and last_only:  # the MLP and the final norm of the last rows only
                 h = h.view(B, S, -1)[:, -1].contiguous()
-                mixed = mixed.view(B, S, -1)[:, -1].contiguous()
+                if not final_query:
+                    mixed = mixed.view(B, S, -1)[:, -1].contiguous()
             residual, normed = ops.native_residual_rms(h, mixed, layer["post_norm"], cfg.eps,
                                                        out_dtype=self.mlp_in)
             # split inputs: fp32 gate/up for SwiGLU (bf16 there costs ~6x the
@@ -273,6 +280,42 @@ class QwenBackbone:
                                       else None)
         values = self._bmm32(probs.view(B * KV, G * S, S), v.view(B * KV, S, hd))  # [B, H, S, hd]
         merged = ops.attention_gate(values.view(B, H, S, hd), gate,
+                                    out_dtype=self.gemm_in or self.dtype)
+        return self._mm32(merged, layer["out"])
+
+    def _final_query_attention(self, layer, x, mask32, B, S):
+        """Final-query attention of the last-token forward: K and V over the
+        whole context, q and its gate for each sequence's last position only, as
+        the reference's CPU and CUDA last-token paths do
+        (``cpu_final_full_attention``, ``src/backbone_cpu.jl:984-1034``, chosen at
+        ``:1106-1131``; ``full_attention_last``, ``ext/cuda_attention.jl:188-267``).
+        The query keeps its position S - 1 (rotated there, ``:1026-1034``) and
+        sees every kept key.  Returns the attention output of the last rows,
+        ``[B, hidden]`` fp32: the S x S scores, softmax and PV work of the full
+        form shrink to one query row per head."""
+        cfg = self.cfg
+        hd, H, KV = cfg.head_dim, cfg.heads, cfg.kv_heads
+        G = H // KV
+        T = B * S
+        w = layer["qkv"]                                     # [in, q | k | v | gate]
+        kv = self._mm(x, w[:, H * hd:(H + 2 * KV) * hd])    # [T, k | v] of every token
+        proj = self._mm(x.view(B, S, -1)[:, -1], w)          # [B, q | k | v | gate], last rows
+        tables = self.rope_tables(S) if cfg.rotary_dim else None
+        _, kt, v = ops.attention_prepare(None, kv[:, :KV * hd].view(T, KV, hd),
+                                         kv[:, KV * hd:].view(T, KV, hd), None, layer["k_norm"],
+                                         tables, cfg.rotary_dim, cfg.eps, B)
+        # q norm + RoPE of the B last rows, each at position S - 1
+        q, _ = ops.prepare_heads(proj[:, :H * hd].view(B, H, hd), None, layer["q_norm"], None,
+                                 tables, cfg.rotary_dim, cfg.eps, seq_len=1, pos_offset=S - 1)
+        scores = self._bmm32(q.view(B * KV, G, hd), kt.view(B * KV, hd, S))      # [B*KV, G, S]
+        scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+        probs = ops.attention_softmax(scores.view(B, H, 1, S), mask32, scale, q_offset=S - 1,
+                                      out_dtype=self.dtype,
+                                      out=scores.view(B, H, 1, S) if self.dtype == torch.float32
+                                      else None)
+        values = self._bmm32(probs.view(B * KV, G, S), v.view(B * KV, S, hd))  # [B, H, 1, hd]
+        gate = proj[:, (H + 2 * KV) * hd:].view(B, H, hd)
+        merged = ops.attention_gate(values.view(B, H, 1, hd), gate,
                                     out_dtype=self.gemm_in or self.dtype)
         return self._mm32(merged, layer["out"])
 

@@ -462,9 +462,9 @@ def prepare_heads(q: torch.Tensor | None, k: torch.Tensor | None, q_norm, k_norm
     return qo, ko
 
 
-def attention_prepare(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm: torch.Tensor,
-                      k_norm: torch.Tensor, tables, rotary_dim: int, eps: float, batch: int,
-                      pos_offset: int = 0, out=None):
+def attention_prepare(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
+                      q_norm: torch.Tensor | None, k_norm: torch.Tensor, tables, rotary_dim: int,
+                      eps: float, batch: int, pos_offset: int = 0, out=None):
     """The attention prologue in one launch (``prepare_head_kernel!`` for Q and K
     and ``prepare_value_kernel!``, ``ext/amdgpu_attention.jl:1-59``): per-head
     zero-centred RMSNorm + half-split partial RoPE of ``q [T, H, hd]`` and
@@ -473,44 +473,57 @@ def attention_prepare(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm:
     stride its heads, e.g. inside a q||gate projection; k and v heads are
     contiguous within a token).  Returns ``(q_out [B, H, S, hd], k_t [B, KV, hd, S],
     v_out [B, KV, S, hd])``: K transposed, so both attention products are plain
-    batched GEMMs.  ``out`` optionally supplies the three contiguous outputs."""
-    _device(q, k, v, q_norm, k_norm)
-    code = _dtype_code(q, k, v, q_norm, k_norm)
-    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
+    batched GEMMs.  ``out`` optionally supplies the three contiguous outputs.
+    ``q=None`` (with ``q_norm=None``) prepares K and V only and returns
+    ``(None, k_t, v_out)``: the context of a query projected apart (final-query
+    attention)."""
+    kv_only = q is None
+    if kv_only and q_norm is not None:
+        raise ValueError("q_norm without q")
+    present = [t for t in (q, k, v, q_norm, k_norm) if t is not None]
+    _device(*present)
+    code = _dtype_code(*present)
+    if (not kv_only and q.dim() != 3) or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
         raise ValueError("q must be [T, H, hd] and k, v [T, KV, hd]")
-    T, H, hd = q.shape
-    KV = k.shape[1]
-    if k.shape[0] != T or k.shape[2] != hd or batch <= 0 or T % batch:
+    T, KV, hd = k.shape
+    H = 0 if kv_only else q.shape[1]
+    if (not kv_only and (q.shape[0] != T or q.shape[2] != hd)) or batch <= 0 or T % batch:
         raise ValueError("q, k and v must share tokens and head_dim; tokens a multiple of batch")
     for t in (q, k, v):
-        if t.stride(2) != 1:
+        if t is not None and t.stride(2) != 1:
             raise ValueError("rows must be contiguous")
     for t in (k, v):
         if KV > 1 and t.stride(1) != hd:
             raise ValueError("k and v heads must be contiguous within a token")
-    _vector(q_norm, hd, "q_norm")
+    if not kv_only:
+        _vector(q_norm, hd, "q_norm")
     _vector(k_norm, hd, "k_norm")
     S = T // batch
     shapes = ((batch, H, S, hd), (batch, KV, hd, S), (batch, KV, S, hd))
     if out is None:
-        out = tuple(torch.empty(sh, dtype=q.dtype, device=q.device) for sh in shapes)
+        out = tuple(None if kv_only and i == 0 else
+                    torch.empty(sh, dtype=k.dtype, device=k.device) for i, sh in enumerate(shapes))
     if len(out) != 3:
         raise ValueError("out must be three tensors (q, K transposed, v)")
-    for o, sh in zip(out, shapes):
-        _device(q, o)
-        if o.dtype != q.dtype or tuple(o.shape) != sh or not o.is_contiguous():
+    if kv_only and out[0] is not None:
+        raise ValueError("out[0] must be None when q is None")
+    for o, sh in zip(out[1:] if kv_only else out, shapes[1:] if kv_only else shapes):
+        _device(k, o)
+        if o.dtype != k.dtype or tuple(o.shape) != sh or not o.is_contiguous():
             raise ValueError("out must be three contiguous tensors [B, H, S, hd], "
-                             "[B, KV, hd, S], [B, KV, S, hd] of q's dtype")
-    cos, sin = _rope_tables(tables, rotary_dim, q)
+                             "[B, KV, hd, S], [B, KV, S, hd] of k's dtype")
+    cos, sin = _rope_tables(tables, rotary_dim, k)
     ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
     tok = lambda t: t.stride(0) if T > 1 else t.shape[1] * t.shape[2]  # noqa: E731
-    check(lib().qdc_attention_prepare(out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
-                                      q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                      q_norm.data_ptr(), k_norm.data_ptr(), ptr(cos), ptr(sin),
+    check(lib().qdc_attention_prepare(ptr(out[0]), out[1].data_ptr(), out[2].data_ptr(),
+                                      ptr(q), k.data_ptr(), v.data_ptr(),
+                                      ptr(q_norm), k_norm.data_ptr(), ptr(cos), ptr(sin),
                                       batch, S, H, KV, hd, rotary_dim, pos_offset,
-                                      cos.shape[0] if rotary_dim else 0, tok(q),
-                                      q.stride(1) if H > 1 else hd, tok(k), tok(v), eps, code,
-                                      _stream(q)), "attention_prepare")
+                                      cos.shape[0] if rotary_dim else 0,
+                                      0 if kv_only else tok(q),
+                                      0 if kv_only else (q.stride(1) if H > 1 else hd),
+                                      tok(k), tok(v), eps, code, _stream(k)),
+          "attention_prepare")
     return out
 
 

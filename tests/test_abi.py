@@ -36,6 +36,14 @@ def test_exports_match_header():
     assert _lib.version().startswith("qdc_hip ")
 
 
+def test_version_matches_the_header():
+    """qdc_version() is the QDC_HIP_VERSION of the header the library was built
+    from (0.2.0: out_dtype added to qdc_gated_rmsnorm and qdc_swiglu)."""
+    m = re.search(r'#define\s+QDC_HIP_VERSION\s+"([^"]+)"', open(HEADER).read())
+    assert m and re.fullmatch(r"qdc_hip \d+\.\d+\.\d+", m.group(1))
+    assert _lib.version() == m.group(1) == "qdc_hip 0.2.0"
+
+
 def test_status_strings():
     for code, name in _lib.STATUS.items():
         assert _lib.status_string(code)
@@ -343,6 +351,38 @@ def test_attention_softmax_validation():
     assert sm(FAKE, BF16, FAKE, None, 1, 2, 8, 8, 0, 0.5) == -5     # in place needs fp32
     assert sm(FAKE + 64, F32, FAKE, None, 1, 2, 8, 8, 0, 0.5) == -5  # partial overlap
     assert sm(FAKE, F32, FAKE + 65536, FAKE + 16, 1, 2, 8, 8, 0, 0.5) == -5  # writes the mask
+
+
+def test_attention_prepare_validation():
+    lib = _lib.lib()
+    ins = [FAKE + (1 + i) * 65536 for i in range(3)]        # q_in, k_in, v_in
+    outs = [FAKE + (4 + i) * 65536 for i in range(3)]       # q_out, k_t, v_out
+    norms = [FAKE + 7 * 65536, FAKE + 7 * 65536 + 256]      # q_norm, k_norm
+    tabs = [FAKE + 8 * 65536, FAKE + 9 * 65536]             # cos, sin
+
+    def prep(heads=4, kv=2, batch=2, seq=8, dim=64, rotary=16, pos=0, table_len=8,
+             q=True, k_out=True, q_out_at=None):
+        qi, ki, vi = ins
+        qo, ko, vo = outs
+        qo = qo if q_out_at is None else q_out_at
+        return lib.qdc_attention_prepare(qo if q else None, ko if k_out else None, vo,
+                                         qi if q else None, ki, vi, norms[0] if q else None,
+                                         norms[1], *tabs, batch, seq, heads, kv, dim, rotary, pos,
+                                         table_len, 2 * heads * dim if q else 0,
+                                         dim if q else 0, 2 * kv * dim, 2 * kv * dim, 1e-6, F32,
+                                         None)
+
+    assert prep(heads=-1) == -2
+    assert prep(heads=3) == -2                      # not a multiple of kv_heads
+    assert prep(kv=0) == -2
+    assert prep(q=False, batch=0) == 0              # nothing to do
+    assert prep(table_len=7) == -4                  # positions 0..7 need 8 table rows
+    assert prep(q=False) == -1                      # q pointers NULL with heads > 0
+    assert prep(q=False, heads=0, k_out=False) == -1
+    # heads = 0: K and V only, the q pointers NULL; the range check comes after
+    # the pointer checks, so reaching it shows NULL q passes
+    assert prep(q=False, heads=0, table_len=7) == -4
+    assert prep(q_out_at=ins[1]) == -5              # q output over the k input
 
 
 def test_attention_gate_validation():

@@ -191,12 +191,67 @@ def test_batch_matches_single_sequences():
                                                torch.from_numpy(mask).cuda())
     lasts_host = backbone.batch_backbone_hidden(model, ids, mask)
     assert lasts_host.shape == (3, cfg.hidden)
+    # the last-token forward attends from the last query alone (other GEMM
+    # shapes than the full forward): equal to fp32 rounding, the fp32 bar
     for r in range(3):
         single = backbone.backbone_hidden(model, ids[r], mask[r])
         assert normwise(states[r], single) <= 1e-6, r
-        assert normwise(lasts_dev[r], single[-1]) <= 1e-6, r
-        assert normwise(lasts_host[r], single[-1]) <= 1e-6, r
-        assert normwise(backbone.backbone_last_hidden(model, ids[r], mask[r]), single[-1]) <= 1e-6
+        assert normwise(lasts_dev[r], single[-1]) <= 1e-5, r
+        assert normwise(lasts_host[r], single[-1]) <= 1e-5, r
+        assert normwise(backbone.backbone_last_hidden(model, ids[r], mask[r]), single[-1]) <= 1e-5
+
+
+@pytest.mark.parametrize("n", [1, 9, 64, 129])
+def test_final_query_attention(n, monkeypatch):
+    """The last-token forward attends from each row's last query only in its
+    last (full-attention) layer, as the reference's CPU and CUDA last-token
+    paths do (``cpu_final_full_attention``, ``src/backbone_cpu.jl:984-1034``;
+    ``ext/cuda_attention.jl:188-267``): K and V over the whole context, q at
+    position n - 1.  ``backbone_last_hidden`` and ``batch_backbone_hidden``
+    against the oracle's last row, fp32 within 1e-5, with every mask kind (all
+    kept, padded prefix, holes, only the last kept, none kept); the final-query
+    path is the one taken."""
+    from qdc_amd import backbone
+    from qdc_amd.config import plumbing_config
+    from qdc_amd.weights import random_weights
+    cfg = plumbing_config()
+    assert cfg.layer_types[-1] == "full_attention"
+    weights = random_weights(cfg, seed=33)
+    model = model_for(weights, cfg)
+    taken = []
+    final_query = backbone.QwenBackbone._final_query_attention
+
+    def spy(self, layer, x, mask32, B, S):
+        taken.append((B, S))
+        return final_query(self, layer, x, mask32, B, S)
+
+    monkeypatch.setattr(backbone.QwenBackbone, "_final_query_attention", spy)
+    monkeypatch.setenv("QDC_AMDGPU_TRIM_PADDING", "0")   # whole rows in the batched hook
+    rng = np.random.default_rng(34 + n)
+    kinds = masks(n, rng)
+    ids = rng.integers(0, cfg.vocab, size=(len(kinds), n))
+    exp = {}
+    for r, (tag, mask) in enumerate(kinds.items()):
+        exp[tag] = forward.backbone_hidden(weights, cfg.as_dict(), ids[r], mask)[-1]
+        got = backbone.backbone_last_hidden(model, ids[r], mask)
+        err = normwise(got, exp[tag])
+        print(f"final-query last hidden n={n} {tag}: {err:.2e}", flush=True)
+        assert err <= 1e-5, (n, tag, err)
+    assert taken == [(1, n)] * len(kinds)
+    batch_mask = np.stack(list(kinds.values()))
+    for host_inputs in (True, False):
+        if host_inputs:
+            lasts = backbone.batch_backbone_hidden(model, ids, batch_mask)
+        else:
+            lasts = backbone.batch_backbone_hidden(model, torch.from_numpy(ids).cuda(),
+                                                   torch.from_numpy(batch_mask).cuda())
+        for r, tag in enumerate(kinds):
+            assert normwise(lasts[r], exp[tag]) <= 1e-5, (n, tag, host_inputs)
+    assert taken[-1] == (len(kinds), n)
+    # the full forward never takes it
+    taken.clear()
+    backbone.backbone_hidden(model, ids[0], batch_mask[0])
+    assert not taken
 
 
 def test_batch_trims_common_padding(monkeypatch):
@@ -228,10 +283,10 @@ def test_batch_trims_common_padding(monkeypatch):
     for r in range(3):
         single_trim = backbone.backbone_hidden(model, ids[r, 6:], mask[r, 6:])[-1]
         single = backbone.backbone_hidden(model, ids[r], mask[r])[-1]
-        assert normwise(trimmed[r], single_trim) <= 1e-6, r
+        assert normwise(trimmed[r], single_trim) <= 1e-5, r
         assert normwise(trimmed[r], single) <= 1e-5, r
-        assert normwise(whole[r], single) <= 1e-6, r
-        assert normwise(on_dev[r], single) <= 1e-6, r
+        assert normwise(whole[r], single) <= 1e-5, r
+        assert normwise(on_dev[r], single) <= 1e-5, r
 
 
 def test_batch_validation():
@@ -282,12 +337,26 @@ def _full_depth_case(dtype):
     return cfg, weights, ids, mask
 
 
-def _bf16_end_to_end(got, expbf, what):
+def _bf16_miss_ceiling(drift):
+    """The largest distance still reported as the known compounding-rounding
+    miss rather than a failure: max(2.5e-2, 1.25 x the bf16-storage oracle's own
+    distance from the fp32 oracle).  Two bf16 evaluations of this network drift
+    toward each other's bf16 noise floor, which that distance measures; a
+    regression beyond it fails."""
+    return max(2.5e-2, 1.25 * drift)
+
+
+def _bf16_end_to_end(got, expbf, what, drift):
     """The bf16 end-to-end bar: 1e-2 against the oracle run with
-    the same bf16 storage points.  Where it is missed the test reports xfail
-    with the measured distance (see test_full_depth_bf16_teacher_forced for
-    the per-layer and per-op parity that holds at every layer)."""
+    the same bf16 storage points.  Where it is missed by no more than the
+    ceiling of ``_bf16_miss_ceiling(drift)`` the test reports xfail with the
+    measured distance (see test_full_depth_bf16_teacher_forced for the
+    per-layer and per-op parity that holds at every layer); beyond it, it
+    fails."""
     err = normwise(got, expbf)
+    ceiling = _bf16_miss_ceiling(drift)
+    assert err <= ceiling, (f"{what}: GPU bf16 vs bf16-storage oracle {err:.2e} beyond the "
+                            f"{ceiling:.2e} ceiling of the known rounding drift")
     if err > 1e-2:
         pytest.xfail(f"{what}: GPU bf16 vs bf16-storage oracle {err:.2e} > 1e-2 (two bf16 "
                      "evaluations of the 24-layer random-init backbone diverge through rounding "
@@ -313,10 +382,13 @@ def test_full_depth_qwen35_backbone(dtype):
     last = backbone.backbone_last_hidden(model, ids, mask)
     del model
     torch.cuda.empty_cache()
-    # the last-token forward normalises only the last row: the same values
-    assert normwise(last, got[-1]) <= (1e-6 if dtype == torch.float32 else 1e-2)
+    # the last-token forward (final-query attention in the last layer, the
+    # last row only after it): the same values to rounding
+    assert normwise(last, got[-1]) <= (1e-5 if dtype == torch.float32 else 1e-2)
     exp32 = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask)
     err32 = normwise(got, exp32)
+    if dtype == torch.float32:
+        assert normwise(last, exp32[-1]) <= 1e-5
     if dtype == torch.float32:
         print(f"full-depth qwen3.5 fp32 vs fp32 oracle: {err32:.2e}", flush=True)
         assert err32 <= 1e-5
@@ -325,7 +397,7 @@ def test_full_depth_qwen35_backbone(dtype):
     print(f"full-depth qwen3.5 bf16: GPU vs bf16-storage oracle {normwise(got, expbf):.2e}; "
           f"GPU vs fp32 oracle {err32:.2e}; bf16-storage oracle vs fp32 oracle "
           f"{normwise(expbf, exp32):.2e}", flush=True)
-    _bf16_end_to_end(got, expbf, "24 layers, 64 tokens")
+    _bf16_end_to_end(got, expbf, "24 layers, 64 tokens", normwise(expbf, exp32))
 
 
 def _mismatch(got, exp):
@@ -500,7 +572,7 @@ def _full_size_prefixes(dtype, P, split=False):
     lasts = backbone.batch_backbone_hidden(model, d_ids, None)
     assert lasts.shape == (B, cfg.hidden)
     assert normwise(lasts, first[:, -1].float().cpu().numpy()) <= (
-        1e-6 if dtype == torch.float32 else 1e-2)
+        1e-5 if dtype == torch.float32 else 1e-2)
     prefixes = first[:, :P].float().cpu().numpy()
     del model, first, again
     torch.cuda.empty_cache()
@@ -535,6 +607,9 @@ def test_full_size_forward_causal_prefix(dtype):
         errbf = normwise(prefixes[r], expbf)
         print(f"full-size bf16, sequence {r}: first {P} positions vs bf16-storage oracle "
               f"{errbf:.2e}, vs fp32 oracle {err32:.2e}", flush=True)
+        ceiling = _bf16_miss_ceiling(normwise(expbf, exp32))
+        assert errbf <= ceiling, (f"sequence {r}: {errbf:.2e} beyond the {ceiling:.2e} ceiling "
+                                  "of the known rounding drift")
         if errbf > 1e-2:
             misses.append((r, errbf))
     if misses:
@@ -669,7 +744,7 @@ def test_wide_backbone(mode):
     last = backbone.backbone_last_hidden(model, ids, mask)
     del model
     torch.cuda.empty_cache()
-    assert normwise(last, got[-1]) <= (1e-6 if mode == "fp32" else 1e-3)
+    assert normwise(last, got[-1]) <= (1e-5 if mode == "fp32" else 1e-2)
     exp32 = forward.backbone_hidden(weights, cfg.as_dict(), ids, mask)
     err32 = normwise(got, exp32)
     if mode == "fp32":
@@ -758,7 +833,7 @@ def test_long_sequence_causal_prefix(mode):
     assert torch.equal(first, again)
     assert torch.isfinite(first).all()
     last = backbone.batch_backbone_hidden(model, d_ids, None)
-    assert normwise(last[0], first[0, -1].cpu().numpy()) <= (1e-6 if mode == "fp32" else 1e-2)
+    assert normwise(last[0], first[0, -1].cpu().numpy()) <= (1e-5 if mode == "fp32" else 1e-2)
     prefix = first[0, :P].float().cpu().numpy()
     del model, first, again
     torch.cuda.empty_cache()

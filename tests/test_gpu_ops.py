@@ -1087,10 +1087,10 @@ PREP_CASES = [
     (3, 72, 8, 2, 128, 32, True, 5),       # fast path with an offset: partial K and V tiles
     (5, 8, 4, 2, 64, 16, True, 0),         # shortest bf16 fast path: one 8-token K and V tile
     (1, 4, 2, 1, 64, 16, False, 2),        # 4 tokens: fp32 fast path (bf16: general path)
-    (2, 136, 8, 2, 256, 64, True, 0),      # last K tile of 8 tokens: its second row batch empty
-    (2, 200, 4, 2, 512, 128, True, 1),     # 512-wide heads: two row batches of 32 tokens (bf16)
-    (3, 40, 8, 2, 64, 16, True, 2),        # 8 heads: Q rows half staged through LDS
-    (2, 72, 16, 4, 128, 32, False, 0),     # 16 heads, q inside q||gate rows, staged Q rows
+    (2, 136, 8, 2, 256, 64, True, 0),      # last K tile of 8 tokens: rows and pieces past the end skipped
+    (2, 200, 4, 2, 512, 128, True, 1),     # 512-wide heads: bf16 LPR 32 (8 rows per lane group); fp32 general path
+    (3, 40, 8, 2, 64, 16, True, 2),        # 8 heads: two 4-head Q row groups per token
+    (2, 72, 16, 4, 128, 32, False, 0),     # 16 heads, 4 KV heads, q read out of interleaved q||gate rows
 ]
 
 
@@ -1135,6 +1135,32 @@ def test_attention_prepare(dtype, case):
     report(f"prepare k {case}", got_k, exp_k, dtype)
     got_v = v_out.permute(0, 2, 1, 3).reshape(T, KV, hd)
     assert torch.equal(got_v, vd.contiguous()), case
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", [PREP_CASES[i] for i in (0, 1, 2, 4, 6, 9)])
+def test_attention_prepare_kv_only(dtype, case):
+    """heads = 0 (``q=None``): K transposed and V head-major only, for a query
+    projected apart (final-query attention).  Bit-identical to the K and V of
+    the launch with Q rows, on the fast path's K and V tiles and on the
+    general path."""
+    from qdc_amd import ops
+    B, S, H, KV, hd, rd, packed, pos_offset = case
+    T = B * S
+    proj = dev(host((T, (2 * H + 2 * KV) * hd), 44, 1.0, dtype), dtype)
+    qd = proj[:, :H * hd].view(T, H, hd)
+    kd = proj[:, H * hd:(H + KV) * hd].view(T, KV, hd)
+    vd = proj[:, (H + KV) * hd:(H + 2 * KV) * hd].view(T, KV, hd)
+    qn, kn = dev(host((hd,), 45, 0.02, dtype), dtype), dev(host((hd,), 46, 0.02, dtype), dtype)
+    tables = ops.rope_tables(S + pos_offset, rd, 1e7, DEV) if rd else None
+    _, k_full, v_full = ops.attention_prepare(qd, kd, vd, qn, kn, tables, rd, 1e-6, B,
+                                              pos_offset=pos_offset)
+    none, k_t, v_out = ops.attention_prepare(None, kd, vd, None, kn, tables, rd, 1e-6, B,
+                                             pos_offset=pos_offset)
+    torch.cuda.synchronize()
+    assert none is None
+    assert torch.equal(k_t, k_full), case
+    assert torch.equal(v_out, v_full), case
 
 
 def test_attention_prepare_checks():

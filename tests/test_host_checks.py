@@ -63,6 +63,15 @@ def _calls():
           dict(out=(d(2, 2, 4, 16), host(2, 1, 16, 4), d(2, 1, 4, 16))),
           dict(out=(d(2, 2, 4, 16), d(2, 1, 4, 16), d(2, 1, 4, 16))),
           dict(out=(d(2, 2, 4, 16), d(2, 1, 16, 4)))]),
+        # K and V only (q=None): the final-query attention's context
+        ("attention_prepare_kv",
+         lambda **kw: ops.attention_prepare(kw.pop("q", None), d(8, 1, 16), d(8, 1, 16),
+                                            kw.pop("q_norm", None), d(16), tables, 8, 1e-6, 2,
+                                            **kw),
+         [dict(q_norm=d(16)),
+          dict(out=(d(2, 2, 4, 16), d(2, 1, 16, 4), d(2, 1, 4, 16))),
+          dict(out=(None, d(2, 1, 4, 16), d(2, 1, 4, 16))),
+          dict(out=(None, d(2, 1, 16, 4, dtype=BF16), d(2, 1, 4, 16)))]),
         ("device_copy_rows",
          lambda **kw: ops.device_copy_rows(kw.get("dst", d(4, 16, dtype=BF16)),
                                            d(10, 16, dtype=BF16), d(4, dtype=torch.int32)),
