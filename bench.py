@@ -559,14 +559,18 @@ def calibrate(dev):
 E2E_BATCH, E2E_SEQ = 8, 2048
 
 
-def fused_sequence(cfg, dev, tokens):
+def fused_sequence(cfg, dev, tokens, split=None):
     """The fused row-kernel launches of one bf16 forward at `tokens` tokens
     (gather + first input norm, 2 residual norms per layer, SwiGLU per layer, the
     attention prologue per full-attention layer, gated norm per DeltaNet layer)
-    on buffers of the forward's shapes and strides."""
+    on buffers of the forward's shapes and strides.  `split="mlp"` launches them
+    as the forward with split MLP inputs does: the post-attention norm writes
+    the split output, SwiGLU reads fp32 gate/up and writes the split output."""
     import torch
     from qdc_amd import ops
     bf, f32 = torch.bfloat16, torch.float32
+    if split not in (None, "mlp"):
+        raise ValueError("split must be None or 'mlp'")
     g = torch.Generator(device=dev)
     g.manual_seed(1)
     rn = lambda shape, dt: torch.randn(shape, generator=g, device=dev).to(dt)  # noqa: E731
@@ -576,8 +580,10 @@ def fused_sequence(cfg, dev, tokens):
     w = rn((H,), bf)
     h, mixed = rn((tokens, H), f32), rn((tokens, H), f32)
     res, normed = torch.empty_like(h), torch.empty((tokens, H), dtype=bf, device=dev)
-    gu = rn((tokens, 2 * cfg.intermediate), bf)
-    act = torch.empty((tokens, cfg.intermediate), dtype=bf, device=dev)
+    mlp_in = ops.BF16X2 if split else None
+    gu = rn((tokens, 2 * cfg.intermediate), f32 if split else bf)
+    act = torch.empty((tokens, (2 if split else 1) * cfg.intermediate), dtype=bf, device=dev)
+    post = torch.empty((tokens, 2 * H), dtype=bf, device=dev) if split else normed
     hd, nh, kv = cfg.head_dim, cfg.heads, cfg.kv_heads
     qkv = rn((tokens, 2 * hd * nh + 2 * hd * kv), bf)
     qn = rn((hd,), bf)
@@ -607,8 +613,8 @@ def fused_sequence(cfg, dev, tokens):
                 ops.native_gated_rms(dx, proj[:, cq:cq + vw].view(tokens, cfg.value_heads,
                                                                   cfg.value_dim), wv, 1e-6,
                                      out=gated)
-            ops.native_residual_rms(h, mixed, w, 1e-6, residual=res, out=normed)
-            ops.native_mlp_gate(gu[:, :I], gu[:, I:], out=act)
+            ops.native_residual_rms(h, mixed, w, 1e-6, residual=res, out=post, out_dtype=mlp_in)
+            ops.native_mlp_gate(gu[:, :I], gu[:, I:], out=act, out_dtype=mlp_in)
             ops.native_residual_rms(res, mixed, w, 1e-6, residual=h, out=normed)
     return run
 
@@ -706,40 +712,57 @@ def e2e_benchmark(dev, steps=3, warmup=1):
         torch.cuda.empty_cache()
         return start.elapsed_time(end) / steps
 
-    ms = forward_ms(False)
-    split_ms = {mode: forward_ms(mode) for mode in ("all", "mlp")}
+    # headline: bf16 weights with the MLP's two GEMM inputs split, the fastest
+    # bf16-weight mode that meets the 1e-2 end-to-end bar at 24 layers
+    ms = forward_ms("mlp")
+    all_split_ms = forward_ms("all")
+    bf16_ms = forward_ms(False)
     # the same weights widened to fp32 (exact), fp32 activations and GEMMs
     fp32_ms = forward_ms(False, torch.float32)
     del weights
     torch.cuda.empty_cache()
     # this library's kernels of one forward, replayed from graphs on buffers of
-    # the forward's shapes: the fused row kernels, then the widened kernels
-    fused_ms = _graph_ms(fused_sequence(cfg, dev, E2E_BATCH * E2E_SEQ))
+    # the forward's shapes: the fused row kernels (as the headline mode and as
+    # all-bf16 storage launch them), then the widened kernels
+    fused_ms = _graph_ms(fused_sequence(cfg, dev, E2E_BATCH * E2E_SEQ, split="mlp"))
+    torch.cuda.empty_cache()
+    fused_bf16_ms = _graph_ms(fused_sequence(cfg, dev, E2E_BATCH * E2E_SEQ))
     torch.cuda.empty_cache()
     widened_ms = _graph_ms(widened_sequence(cfg, dev, E2E_BATCH, E2E_SEQ))
     torch.cuda.empty_cache()
+    tps = lambda v: round(E2E_BATCH * E2E_SEQ / (v / 1e3), 1)  # noqa: E731
     return {"workload": "random-init Qwen3.5-0.8B-like backbone, 24 layers (18 DeltaNet + 6 full), "
-                        "hidden 1024, vocab 248320, bf16 weights and activations, fp32 residual",
+                        "hidden 1024, vocab 248320, bf16 weights, fp32 residual stream, the MLP's "
+                        "two GEMM inputs split into two bf16 terms (split_gemm_inputs='mlp')",
+            "mode": "split_gemm_inputs='mlp'",
+            "end_to_end_vs_fp32_oracle": {"24 layers, 64 tokens": 3.00e-3,
+                                          "full size, first 64 positions": [3.11e-3, 3.13e-3],
+                                          "bar": 1e-2, "meets_1e-2_end_to_end": True},
             "batch": E2E_BATCH, "seq_len": E2E_SEQ, "ms_per_forward": round(ms, 3),
-            "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (ms / 1e3), 1),
+            "tokens_per_s": tps(ms),
             "fused_kernels_ms": round(fused_ms, 3),
             "fused_kernel_time_share": round(fused_ms / ms, 4),
             "widened_kernels_ms": round(widened_ms, 3),
             "widened_kernel_time_share": round(widened_ms / ms, 4),
-            "split_gemm_inputs": {
-                "note": "the same weights and tokens with GEMM inputs written by their "
-                        "producing kernels as two bf16 terms (hi + lo, the GEMMs' inner "
-                        "dimension doubled) and fp32 MLP gate/up -- every GEMM input ('all') "
-                        "or the MLP's two ('mlp'): the bf16-weight modes that meet the 1e-2 "
-                        "end-to-end bar against the fp32 oracle at 24 layers",
-                **{mode: {"ms_per_forward": round(v, 3),
-                          "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (v / 1e3), 1)}
-                   for mode, v in split_ms.items()}},
+            "split_gemm_inputs_all": {
+                "note": "every GEMM input split (split_gemm_inputs='all'): 2.31e-3 from the fp32 "
+                        "oracle at 24 layers, within the 1e-2 bar",
+                "ms_per_forward": round(all_split_ms, 3), "tokens_per_s": tps(all_split_ms)},
+            "bf16_storage": {
+                "note": "all-bf16 storage (bf16 GEMM inputs, no split): faster, but misses the "
+                        "1e-2 end-to-end bar at 24 layers (1.40e-2 against the oracle with the "
+                        "same storage points, 2.05e-2 against the fp32 oracle; the two xfails "
+                        "of the GPU suite), so it is not the headline",
+                "meets_1e-2_end_to_end": False,
+                "end_to_end_24_layers": {"vs_same_storage_oracle": 1.40e-2, "vs_fp32_oracle": 2.05e-2},
+                "ms_per_forward": round(bf16_ms, 3), "tokens_per_s": tps(bf16_ms),
+                "fused_kernels_ms": round(fused_bf16_ms, 3),
+                "fused_kernel_time_share": round(fused_bf16_ms / bf16_ms, 4),
+                "widened_kernel_time_share": round(widened_ms / bf16_ms, 4)},
             "fp32": {
                 "note": "the same weights widened to fp32 (exactly), fp32 activations and GEMMs: "
                         "the mode within 1e-5 of the fp32 oracle end to end",
-                "ms_per_forward": round(fp32_ms, 3),
-                "tokens_per_s": round(E2E_BATCH * E2E_SEQ / (fp32_ms / 1e3), 1)},
+                "ms_per_forward": round(fp32_ms, 3), "tokens_per_s": tps(fp32_ms)},
             "steps": steps, "warmup": warmup}
 
 
@@ -1255,9 +1278,10 @@ def summarize_forward(out_dir, commit):
     untraced = json.loads([ln for ln in open(os.path.join(out_dir, "bench.log"))
                            if ln.startswith("{")][-1])
     b = untraced["backbone"]
-    modes = [("all-bf16 storage", starts[0:5], b["ms_per_forward"]),
-             ("all", starts[4:9], b["split_gemm_inputs"]["all"]["ms_per_forward"]),
-             ("mlp", starts[8:13], b["split_gemm_inputs"]["mlp"]["ms_per_forward"])]
+    # e2e_benchmark's order: the headline "mlp" mode, "all", all-bf16 storage, fp32
+    modes = [("mlp", starts[0:5], b["ms_per_forward"]),
+             ("all", starts[4:9], b["split_gemm_inputs_all"]["ms_per_forward"]),
+             ("all-bf16 storage", starts[8:13], b["bf16_storage"]["ms_per_forward"])]
     cmd = FORWARD_COMMANDS[0]
     tables = {}
     for mode, st, ms in modes:
@@ -1267,36 +1291,40 @@ def summarize_forward(out_dir, commit):
         span = sum((s[-1][3] - s[0][2]) for s in segs) / 2 / 1e6
         tables[mode] = (t, busy, span, ms)
     hdr = "| kernel | launches / forward | ms / forward | share of kernel time |\n|---|---|---|---|\n"
-    t, busy, span, ms = tables["all-bf16 storage"]
+    t, busy, span, ms = tables["mlp"]
     with open(os.path.join(ROOT, "profiles", "backbone_forward_kernels.md"), "w") as f:
-        f.write(f"""# backbone_hidden forward: per-kernel time (random-init Qwen3.5-0.8B-like, bf16, 8 x 2048 tokens)
+        f.write(f"""# backbone_hidden forward: per-kernel time (random-init Qwen3.5-0.8B-like, bf16 weights, split MLP inputs, 8 x 2048 tokens)
 
 Command (run from `/tmp` with `TMPDIR=/tmp`, `$R` = repository root), commit {commit}; then
 `python bench.py --summarize-forward $R/gpurun_out --commit {commit}` (with the untraced bench line
-of the same commit in `gpurun_out/bench.log`) wrote this file, `split_gemm_inputs_forward.md` and
+of the same commit in `gpurun_out/bench.log`) wrote this file, `other_modes_forward.md` and
 `decision_latency_kernels.md`:
 
 ```
 {cmd}
 ```
 
-The trace covers the whole run; the table sums the kernels of the first and second timed
-forwards of `bench.py`'s end-to-end benchmark (each forward starts with its one gather launch,
-the gather fused with the first input norm) and divides by two. 24 layers: 18 DeltaNet + 6 full
-attention, hidden 1024, 16384 tokens per forward. GEMMs are labelled by the output type of their
-Tensile kernel. The same run continues with the split-GEMM-input modes, summarised in
-`split_gemm_inputs_forward.md`.
+The headline mode: bf16 weights, the MLP's two GEMM inputs (the post-attention norm's output and
+SwiGLU's) written as two bf16 terms, the MLP gate/up GEMM writing fp32 for SwiGLU
+(`split_gemm_inputs="mlp"`, within 1e-2 of the fp32 oracle end to end). The trace covers the whole
+run; the table sums the kernels of the first and second timed forwards of `bench.py`'s end-to-end
+benchmark (each forward starts with its one gather launch, the gather fused with the first input
+norm) and divides by two. 24 layers: 18 DeltaNet + 6 full attention, hidden 1024, 16384 tokens
+per forward. GEMMs are labelled by the output type of their Tensile kernel. The same run
+continues with the other modes, summarised in `other_modes_forward.md`.
 
 forward span {span:.3f} ms, kernels busy {busy:.3f} ms under the tracer; untraced, the bench line of
 the same commit gives {ms:.3f} ms per forward
 
 """ + hdr + "\n".join(t) + """
 
-`rms_rows_fast` covers 47 residual + next-norm launches (fp32 residual stream, bf16 output), the
-18 DeltaNet gated norms and the residual + final norm (fp32).
+`rms_rows_fast` covers the 24 post-attention residual norms (fp32 residual stream, split output),
+the 23 residual + next-input norms (bf16 output), the 18 DeltaNet gated norms and the residual +
+final norm (fp32). `swiglu_fast` reads the fp32 gate/up GEMM output and writes the split form
+(704 MB per launch).
 """)
-    with open(os.path.join(ROOT, "profiles", "split_gemm_inputs_forward.md"), "w") as f:
-        f.write(f"""# backbone_hidden forward with split GEMM inputs: per-kernel time (random-init Qwen3.5-0.8B-like, bf16 weights, 8 x 2048 tokens)
+    with open(os.path.join(ROOT, "profiles", "other_modes_forward.md"), "w") as f:
+        f.write(f"""# backbone_hidden forward in the other bf16-weight modes: per-kernel time (random-init Qwen3.5-0.8B-like, 8 x 2048 tokens)
 
 Command (run from `/tmp` with `TMPDIR=/tmp`, `$R` = repository root), commit {commit} -- the same
 run as `backbone_forward_kernels.md`:
@@ -1305,16 +1333,17 @@ run as `backbone_forward_kernels.md`:
 {cmd}
 ```
 
-`bench.py`'s end-to-end benchmark runs the same weights and tokens in all-bf16 storage, then
-`split_gemm_inputs="all"` (every GEMM input written as two bf16 terms; projection weights with
-their input rows repeated, twice the inner dimension), then `"mlp"` (only the MLP's two inputs
-split), one warm-up and three timed forwards each. Each table sums the kernels of the first and
-second timed forwards of its mode and divides by two. In both split modes the MLP gate/up GEMM
-writes fp32 and SwiGLU reads it, so `swiglu_fast` moves 704 MB per launch instead of 352 MB. The
-split-output kernels alone, at these shapes beside their copy ceilings and with counted HBM
-traffic, are in `fused_kernels_trace_pmc.md` and `launch_ceilings.md` (`fwd_*_split`).
+`bench.py`'s end-to-end benchmark runs the same weights and tokens with `split_gemm_inputs="mlp"`
+(the headline, `backbone_forward_kernels.md`), then `"all"` (every GEMM input written as two bf16
+terms; projection weights with their input rows repeated, twice the inner dimension), then
+all-bf16 storage (no split; misses the 1e-2 end-to-end bar at 24 layers), one warm-up and three
+timed forwards each. Each table sums the kernels of the first and second timed forwards of its
+mode and divides by two. In both split modes the MLP gate/up GEMM writes fp32 and SwiGLU reads
+it, so `swiglu_fast` moves 704 MB per launch instead of 352 MB. The split-output kernels alone,
+at these shapes beside their copy ceilings and with counted HBM traffic, are in
+`fused_kernels_trace_pmc.md` and `launch_ceilings.md` (`fwd_*_split`).
 """)
-        for mode in ("all", "mlp", "all-bf16 storage"):
+        for mode in ("all", "all-bf16 storage", "mlp"):
             t, busy, span, ms = tables[mode]
             f.write(f"""
 ## {mode}: forward span {span:.3f} ms, kernels busy {busy:.3f} ms (untraced: {ms:.3f} ms)
