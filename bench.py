@@ -26,9 +26,11 @@ DeltaNet layers (reported under "widened", not in `value`):
                        TFLOP/s against the dense fp32 MFMA peak too)
 
 Beside each fused row kernel the run times the library's plain streaming copy
-(qdc_copy) of the same total bytes, half read and half written, in the same
-way: `copy_pct_peak` is what a single launch of that size reaches, and
-`pct_of_copy` the kernel's bandwidth as a share of it.
+of the same total bytes, half read and half written, in the same way and in
+several launch shapes (qdc_copy, qdc_copy_grid): `copy_pct_peak` is what the
+fastest single launch of that size reaches (`copy_shape`), and `pct_of_copy`
+the kernel's bandwidth as a share of it (`pct_of_one_chunk_copy` against the
+one-chunk-per-thread shape alone).
 
 Inputs are resident in HBM before timing.  Every kernel cycles through
 several input/output buffer sets totalling more than 512 MB, so the 256 MB
@@ -475,21 +477,38 @@ def empty_floors(kernels, steps, warmup):
     return {e.name[len("empty_"):]: e for e in empties}
 
 
+# Launch shapes of the copy ceiling, (16-byte chunks per thread, threads per
+# workgroup): qdc_copy's one chunk per thread and the qdc_copy_grid shapes that
+# measured faster at some sizes (2 or 4 chunks per thread at 33-67 MB,
+# 512-thread workgroups at 352 MB).  Each kernel is held against the fastest.
+COPY_SHAPES = ((1, 256), (2, 256), (4, 256), (1, 512))
+
+
 def copy_ceilings(dev, kernels, steps, warmup):
-    """For each kernel, the library's plain streaming copy (qdc_copy: one
-    16-byte chunk per thread, nontemporal) of the same total bytes, half read
-    and half written, graph-replayed over rotating buffers like the kernels:
-    what a single launch moving that many bytes reaches on this GPU."""
+    """For each kernel, the library's plain streaming copy (qdc_copy /
+    qdc_copy_grid: 16-byte chunks, nontemporal) of the same total bytes, half
+    read and half written, graph-replayed over rotating buffers like the
+    kernels, in every shape of COPY_SHAPES (sharing one set of buffers): what
+    a single launch moving that many bytes reaches on this GPU.  Returns
+    {kernel: (fastest copy, random-row copy or None, {shape: copy})}."""
     import torch
     from qdc_amd import ops
     copies = []
     for k in kernels:
         side = (k.algo_bytes // 2) // 16 * 16
-        copies.append(Kernel(
-            f"copy_{k.name}", "copy_chunks", 2 * side,
-            lambda i, side=side: (torch.empty(side, dtype=torch.uint8, device=dev),
-                                  torch.empty(side, dtype=torch.uint8, device=dev)),
-            lambda st: ops.device_copy(st[1], st[0]), [side], "u8"))
+        bufs = {}
+
+        def make_set(i, side=side, bufs=bufs):
+            if i not in bufs:
+                bufs[i] = (torch.empty(side, dtype=torch.uint8, device=dev),
+                           torch.empty(side, dtype=torch.uint8, device=dev))
+            return bufs[i]
+
+        for cpt, blk in COPY_SHAPES:
+            copies.append(Kernel(
+                f"copy{cpt}x{blk}_{k.name}", "copy_chunks" if (cpt, blk) == (1, 256) else "copy_grid",
+                2 * side, make_set,
+                lambda st, cpt=cpt, blk=blk: ops.device_copy(st[1], st[0], cpt, blk), [side], "u8"))
         if k.ceiling is not None:  # the same access pattern as a plain copy
             make_set, launch = k.ceiling
             copies.append(Kernel(f"rows_{k.name}", "copy_rows", k.algo_bytes, make_set, launch,
@@ -502,7 +521,12 @@ def copy_ceilings(dev, kernels, steps, warmup):
         c.graph.replay()
     time_gpu(copies, steps)
     by_name = {c.name: c for c in copies}
-    return {k.name: (by_name[f"copy_{k.name}"], by_name.get(f"rows_{k.name}")) for k in kernels}
+    out = {}
+    for k in kernels:
+        shapes = {f"{cpt}x{blk}": by_name[f"copy{cpt}x{blk}_{k.name}"] for cpt, blk in COPY_SHAPES}
+        best = min(shapes.values(), key=lambda c: c.avg_ms)
+        out[k.name] = (best, by_name.get(f"rows_{k.name}"), shapes)
+    return out
 
 
 PAIR_ROUNDS = 3
@@ -520,7 +544,7 @@ def paired_ratios(kernels, ceilings, rounds=PAIR_ROUNDS):
     for _ in range(rounds):
         marks = []
         for k in kernels:
-            c, rows = ceilings[k.name]
+            c, rows = ceilings[k.name][:2]
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
             ev[0].record(stream)
             k.graph.replay()
@@ -1076,7 +1100,7 @@ def summarize_profiles(out_dir, commit):
     ceil_names = []
     for k in groups["hot"] + [k for g in ("fwd", "alone", "split") for k in groups[g]
                               if k not in groups["hot"]]:
-        ceil_names.append("copy_" + k)
+        ceil_names += [f"copy{cpt}x{blk}_{k}" for cpt, blk in COPY_SHAPES]
         if "ceiling_us" in entry[k]:
             ceil_names.append("rows_" + k)
     floor_names = ["empty_" + k for k in groups["hot"] if "empty_us" in entry[k]]
@@ -1169,11 +1193,14 @@ traced bench run (it includes the graph's gap between nodes).
     for k in groups["hot"] + [k for g in ("fwd", "alone", "split") for k in groups[g]
                               if k not in groups["hot"]]:
         e = entry[k]
-        ku, cu, ru, eu = avg(k), avg("copy_" + k), avg("rows_" + k), avg("empty_" + k)
+        # the copy shape that was fastest by HIP events in the same run
+        cn = f"copy{e.get('copy_shape', '1x256')}_{k}"
+        ku, cu, ru, eu = avg(k), avg(cn), avg("rows_" + k), avg("empty_" + k)
         wg = timed[k][0][0][1] // timed[k][0][0][2]
-        cwg = timed["copy_" + k][0][0][1] // timed["copy_" + k][0][0][2]
+        cwg = timed[cn][0][0][1] // timed[cn][0][0][2]
         kb, cb = e["bytes"], (e["bytes"] // 2) // 16 * 16 * 2
-        lrows.append(f"| {k} | {kb / 1e6:.1f} | {wg} | {ku:.2f} | {cu:.2f} | {cwg} | "
+        lrows.append(f"| {k} | {kb / 1e6:.1f} | {wg} | {ku:.2f} | {e.get('copy_shape', '1x256')} | "
+                     f"{cu:.2f} | {cwg} | "
                      f"{'' if ru is None else f'{ru:.2f}'} | {'' if eu is None else f'{eu:.2f}'} | "
                      f"{100 * kb / ku / 1e3 / PEAK_GBS:.1f} | {100 * cb / cu / 1e3 / PEAK_GBS:.1f} | "
                      f"{100 * (kb / ku) / (cb / cu):.1f} | "
@@ -1185,8 +1212,10 @@ Same trace as `fused_kernels_trace_pmc.md` (commit {commit}; command there). Eve
 average over the {steps} launches of a timed graph replay, from the trace's own timestamps. For each
 kernel the same run times, in the same way:
 
-- `qdc_copy` of the kernel's algorithmic bytes, half read and half written, one 16-byte chunk
-  per thread with nontemporal loads and stores;
+- a copy of the kernel's algorithmic bytes, half read and half written, nontemporal 16-byte
+  chunks, in each launch shape of `COPY_SHAPES` (chunks per thread x threads per workgroup:
+  `qdc_copy` and `qdc_copy_grid`); the table shows the shape that was fastest by HIP events in
+  the same run (`copy shape`), and each kernel is held against it;
 - for the gathers, `qdc_copy_rows`: the same table, the same number of rows read at uniformly
   random places and written contiguously 1, 2 or 3 times (the gather's access pattern and bytes);
 - for the per-kernel configurations of the RMSNorm family and the q/k kernel, `qdc_empty` over
@@ -1196,8 +1225,8 @@ The last two columns are the bench line's paired ratios of the same run: the ker
 replayed right before its ceilings' graphs, median of three rounds (HIP events; ceiling time /
 kernel time).
 
-| kernel | MB | workgroups | kernel us | copy us | copy workgroups | random-row copy us | empty us (same grid) | kernel % of 8 TB/s | copy % of 8 TB/s | kernel % of copy | paired % of copy | paired % of random-row copy |
-|---|---|---|---|---|---|---|---|---|---|---|---|---|
+| kernel | MB | workgroups | kernel us | copy shape | copy us | copy workgroups | random-row copy us | empty us (same grid) | kernel % of 8 TB/s | copy % of 8 TB/s | kernel % of copy | paired % of copy | paired % of random-row copy |
+|---|---|---|---|---|---|---|---|---|---|---|---|---|---|
 """ + "\n".join(lrows) + "\n")
 
     # rocprofv3 --stats of the library's kernels
@@ -1491,12 +1520,16 @@ def main():
         t = load_traffic(k.name)
         if t is not None:  # counted in the profiling run named by traffic_source
             e.update(hbm_bytes_counted=t, traffic_per_algorithmic=round(t / k.algo_bytes, 4))
-        c, rows = ceilings.get(k.name, (None, None))
-        if c is not None:  # the same bytes as one plain streaming copy launch
+        c, rows, shapes = ceilings.get(k.name, (None, None, None))
+        if c is not None:  # the same bytes as one plain streaming copy launch, fastest shape
             copy_gbs = c.algo_bytes / (c.avg_ms / 1e3) / 1e9
+            one = shapes["1x256"]
             e.update(copy_us=round(c.avg_ms * 1e3, 3),
+                     copy_shape=c.name.split("_", 1)[0][len("copy"):],
                      copy_pct_peak=round(100 * copy_gbs / PEAK_GBS, 1),
-                     pct_of_copy=round(100 * e["gbs"] / copy_gbs, 1))
+                     pct_of_copy=round(100 * e["gbs"] / copy_gbs, 1),
+                     copy_us_by_shape={n: round(x.avg_ms * 1e3, 3) for n, x in shapes.items()},
+                     pct_of_one_chunk_copy=round(100 * one.avg_ms / k.avg_ms, 1))
         if rows is not None:  # the same access pattern as a plain random-row copy
             e.update(ceiling="random-row copy (qdc_copy_rows), same table, bytes and row count",
                      ceiling_us=round(rows.avg_ms * 1e3, 3),

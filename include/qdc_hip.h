@@ -382,6 +382,17 @@ int32_t qdc_attention_gate(void *out, int32_t out_dtype, const float *values, co
 int32_t qdc_copy(void *dst, const void *src, int64_t bytes, hipStream_t stream);
 
 /*
+ * qdc_copy in another launch shape: `chunks_per_thread` (1, 2, 4 or 8) 16-byte
+ * chunks per thread in workgroups of `block` (256 or 512) threads, every load
+ * before the first store; the k-th load instruction of a workgroup covers its
+ * k-th run of `block` consecutive chunks.  Other values: QDC_ERR_SHAPE.
+ * qdc_copy is (1, 256).  No counterpart in the reference: the benchmark times
+ * several shapes beside each kernel and holds the kernel against the fastest.
+ */
+int32_t qdc_copy_grid(void *dst, const void *src, int64_t bytes, int32_t chunks_per_thread,
+                      int32_t block, hipStream_t stream);
+
+/*
  * Random-row copy: destination row i (row_bytes * repeat bytes, rows
  * contiguous) holds `repeat` copies of source row rows[i] (rows: device int32,
  * each in [0, n_src); one outside writes zeros).  row_bytes a multiple of 16,

@@ -18,9 +18,26 @@ __global__ __launch_bounds__(kBlock) void copy_chunks(u32x4 *__restrict__ dst,
     if (i < n) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
+// CPT chunks per thread: workgroup b covers chunks [b*CPT*BLOCK, (b+1)*CPT*BLOCK),
+// the k-th load instruction of every thread the k-th run of BLOCK consecutive
+// chunks, so each wavefront instruction stays one contiguous 1 KB span; all
+// loads are issued before the first store.
+template <int CPT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void copy_grid(u32x4 *__restrict__ dst,
+                                                   const u32x4 *__restrict__ src, uint32_t n) {
+    const uint32_t base = blockIdx.x * (CPT * BLOCK) + threadIdx.x;
+    u32x4 v[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+        if (base + k * BLOCK < n) v[k] = __builtin_nontemporal_load(src + base + k * BLOCK);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+        if (base + k * BLOCK < n) __builtin_nontemporal_store(v[k], dst + base + k * BLOCK);
+}
+
 // chunks * 16 bytes; the grid (chunks rounded up to whole workgroups) stays
 // below 2^32 work-items
-constexpr int64_t kMaxChunks = ((int64_t)1 << 32) - kBlock;
+constexpr int64_t kMaxChunks = ((int64_t)1 << 32) - 8 * 512;
 
 // An empty workgroup: the fixed cost of a launch of a given grid.
 __global__ __launch_bounds__(kBlock) void empty_grid() {}
@@ -62,6 +79,38 @@ extern "C" int32_t qdc_copy(void *dst, const void *src, int64_t bytes, hipStream
     hipLaunchKernelGGL(copy_chunks, dim3((uint32_t)ceil_div(n, kBlock)), dim3(kBlock), 0, stream,
                        static_cast<u32x4 *>(dst), static_cast<const u32x4 *>(src), (uint32_t)n);
     return launch_status();
+}
+
+extern "C" int32_t qdc_copy_grid(void *dst, const void *src, int64_t bytes,
+                                 int32_t chunks_per_thread, int32_t block, hipStream_t stream) {
+    if (bytes < 0 || bytes % 16 != 0 || bytes / 16 > kMaxChunks) return QDC_ERR_SHAPE;
+    if (block != 256 && block != 512) return QDC_ERR_SHAPE;
+    if (chunks_per_thread != 1 && chunks_per_thread != 2 && chunks_per_thread != 4 &&
+        chunks_per_thread != 8)
+        return QDC_ERR_SHAPE;
+    if (bytes == 0) return QDC_OK;
+    if (!dst || !src) return QDC_ERR_NULL;
+    if (!aligned16(dst) || !aligned16(src)) return QDC_ERR_SHAPE;
+    if (overlaps(dst, bytes, src, bytes)) return QDC_ERR_ALIAS;
+    const int64_t n = bytes / 16;
+    const dim3 grid((uint32_t)ceil_div(n, (int64_t)chunks_per_thread * block));
+    auto *d = static_cast<u32x4 *>(dst);
+    auto *s = static_cast<const u32x4 *>(src);
+#define QDC_COPY_GRID(C, B)                                                                      \
+    if (chunks_per_thread == C && block == B) {                                                  \
+        hipLaunchKernelGGL((copy_grid<C, B>), grid, dim3(B), 0, stream, d, s, (uint32_t)n);      \
+        return launch_status();                                                                  \
+    }
+    QDC_COPY_GRID(1, 256)
+    QDC_COPY_GRID(2, 256)
+    QDC_COPY_GRID(4, 256)
+    QDC_COPY_GRID(8, 256)
+    QDC_COPY_GRID(1, 512)
+    QDC_COPY_GRID(2, 512)
+    QDC_COPY_GRID(4, 512)
+    QDC_COPY_GRID(8, 512)
+#undef QDC_COPY_GRID
+    return QDC_ERR_SHAPE;
 }
 
 extern "C" int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows, int64_t n_rows,

@@ -57,6 +57,7 @@ SIGNATURES = {
     "qdc_attention_gate": (_i32, [_vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _vp]),
     "qdc_copy": (_i32, [_vp, _vp, _i64, _vp]),
+    "qdc_copy_grid": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp]),
     "qdc_copy_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "qdc_empty": (_i32, [_i64, _vp]),
 }

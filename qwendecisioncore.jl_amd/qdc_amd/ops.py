@@ -697,17 +697,24 @@ def attention_gate(values: torch.Tensor, gate: torch.Tensor, out_dtype=None,
     return out
 
 
-def device_copy(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+def device_copy(dst: torch.Tensor, src: torch.Tensor, chunks_per_thread: int = 1,
+                block: int = 256) -> torch.Tensor:
     """Plain copy of ``src``'s bytes into ``dst`` (both contiguous, same byte
     count, a multiple of 16) with the library's streaming copy kernel: the
-    single-launch bandwidth ceiling the benchmark sets beside each row kernel."""
+    single-launch bandwidth ceiling the benchmark sets beside each row kernel.
+    ``chunks_per_thread`` (1, 2, 4, 8) and ``block`` (256, 512) select the launch
+    shape (``qdc_copy_grid``); the default is ``qdc_copy``'s."""
     _device(dst, src)
     if not dst.is_contiguous() or not src.is_contiguous():
         raise ValueError("dst and src must be contiguous")
     nbytes = src.numel() * src.element_size()
     if dst.numel() * dst.element_size() != nbytes:
         raise ValueError("dst and src must hold the same number of bytes")
-    check(lib().qdc_copy(dst.data_ptr(), src.data_ptr(), nbytes, _stream(src)), "device_copy")
+    if (chunks_per_thread, block) == (1, 256):
+        check(lib().qdc_copy(dst.data_ptr(), src.data_ptr(), nbytes, _stream(src)), "device_copy")
+    else:
+        check(lib().qdc_copy_grid(dst.data_ptr(), src.data_ptr(), nbytes, chunks_per_thread, block,
+                                  _stream(src)), "device_copy")
     return dst
 
 

@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 22, names
+    assert len(names) == 23, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -429,6 +429,18 @@ def test_copy_validation():
     assert f(None, None, 0) == 0
     assert f(FAKE, FAKE + 16, 64) == -5          # overlapping
     assert f(FAKE, FAKE * 2, 1 << 37) == -2      # 2^33 chunks: grid over 2^32 work-items
+
+
+def test_copy_grid_validation():
+    lib = _lib.lib()
+    cg = lambda *a: lib.qdc_copy_grid(*a, None)  # noqa: E731
+    assert cg(FAKE, FAKE + (1 << 20), 4096, 3, 256) == -2     # chunks per thread
+    assert cg(FAKE, FAKE + (1 << 20), 4096, 2, 128) == -2     # block
+    assert cg(FAKE, FAKE + (1 << 20), 4100, 2, 256) == -2     # not whole chunks
+    assert cg(FAKE + 8, FAKE + (1 << 20), 4096, 2, 256) == -2  # misaligned
+    assert cg(None, FAKE, 4096, 4, 512) == -1
+    assert cg(FAKE, FAKE + 2048, 4096, 8, 256) == -5          # overlap
+    assert cg(None, None, 0, 8, 512) == 0
 
 
 def test_copy_rows_validation():

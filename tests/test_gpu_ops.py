@@ -1075,6 +1075,25 @@ def test_device_copy():
                         torch.empty(24, dtype=torch.uint8, device=DEV))
 
 
+@pytest.mark.parametrize("cpt,block", [(1, 256), (2, 256), (4, 256), (8, 256), (1, 512), (2, 512),
+                                       (4, 512), (8, 512)])
+def test_device_copy_shapes(cpt, block):
+    """Every launch shape of the copy ceiling (qdc_copy_grid) moves every byte,
+    with a last workgroup that is partly past the end and one that is whole, and
+    touches nothing after the destination."""
+    from qdc_amd import ops
+    for nbytes in (16, cpt * block * 16 * 3, cpt * block * 16 * 3 + 4096 + 48, 16_777_216 + 16):
+        src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=DEV)
+        dst = torch.zeros(nbytes + 4096, dtype=torch.uint8, device=DEV)
+        ops.device_copy(dst[:nbytes], src, cpt, block)
+        torch.cuda.synchronize()
+        assert torch.equal(dst[:nbytes], src), (cpt, block, nbytes)
+        assert not dst[nbytes:].any(), (cpt, block, nbytes)
+    with pytest.raises(ValueError):   # not a launch shape of the library
+        ops.device_copy(torch.empty(32, dtype=torch.uint8, device=DEV),
+                        torch.empty(32, dtype=torch.uint8, device=DEV), 3, 256)
+
+
 # ------------------------------------------------------ attention prologue ----
 PREP_CASES = [
     # B, S, H, KV, hd, rotary, packed [q|k|v|gate] (else q read from interleaved q||gate), offset

@@ -17,7 +17,7 @@ from conftest import ROOT
 
 HEADER = os.path.join(ROOT, "include", "qdc_hip.h")
 SHIM = os.path.join(ROOT, "qwendecisioncore.jl_amd", "julia", "amdgpu_hip.jl")
-UNBOUND = {"qdc_copy", "qdc_copy_rows", "qdc_empty"}  # the benchmark's ceilings: no reference counterpart
+UNBOUND = {"qdc_copy", "qdc_copy_grid", "qdc_copy_rows", "qdc_empty"}  # the benchmark's ceilings: no reference counterpart
 
 _SCALARS = {"int32_t": "Int32", "int64_t": "Int64", "float": "Float32", "hipStream_t": "Ptr{Cvoid}"}
 _POINTEES = {"void": "Cvoid", "float": "Float32", "int32_t": "Int32", "int64_t": "Int64"}
@@ -104,7 +104,7 @@ def shim_ccalls() -> list:
 
 def test_header_parses():
     protos = header_prototypes()
-    assert len(protos) == 22, sorted(protos)
+    assert len(protos) == 23, sorted(protos)
     assert protos["qdc_version"] == ("Cstring", [])
     assert protos["qdc_check_ids"] == ("Int32", ["Ptr{Int64}", "Int64", "Int64"])
 
