@@ -52,6 +52,13 @@ template <typename T> struct PrepArgs {
     int64_t batch, seq, kv_heads;
     int64_t tiles;                     // tiles of kTileTokens per sequence
     int64_t q_blocks, k_blocks, v_blocks;
+    // role dealing (attention_prepare_fast): Q blocks over the first nq blocks
+    // at the rate rq / 2^32 per block, K tiles over the first mk non-Q blocks
+    // at rk / 2^32, both ceil(count * 2^32 / span) so that exactly q_blocks
+    // and k_blocks are dealt
+    int64_t nq, mk;
+    uint64_t rq, rk;
+    FastDiv kv_div, tiles_div, vtiles_div;  // kv_heads, tiles, V tiles per sequence
 };
 
 // One K tile: tokens [s0, s0 + 64) of sequence b, KV head g.
@@ -68,9 +75,10 @@ __device__ __forceinline__ void k_tile(const PrepArgs<T> &a, int64_t index) {
 
     const QKArgs<T> &qa = a.qk;
     const int lane = threadIdx.x % LPR, grp = threadIdx.x / LPR;
-    const int64_t g = index % a.kv_heads;
-    const int64_t bt = index / a.kv_heads;
-    const int64_t b = bt / a.tiles, s0 = (bt - b * a.tiles) * kTileTokens;
+    const uint32_t bt = fastdiv((uint32_t)index, a.kv_div);
+    const int64_t g = (uint32_t)index - bt * a.kv_div.d;
+    const uint32_t b32 = fastdiv(bt, a.tiles_div);
+    const int64_t b = b32, s0 = (int64_t)(bt - b32 * a.tiles_div.d) * kTileTokens;
     const int hc = qa.half / V;
     const bool rotary = lane < 2 * hc;
     const bool first = lane < hc;
@@ -194,9 +202,10 @@ __device__ __forceinline__ void v_tile(const PrepArgs<T> &a, int64_t index) {
     constexpr int CH = 2 * LPR;
     constexpr int DIM = CH * V;
     constexpr int PER = (kVTokens * CH + kBlock - 1) / kBlock;
-    const int64_t vt = (a.seq + kVTokens - 1) / kVTokens;
-    const int64_t g = index % a.kv_heads, bt = index / a.kv_heads;
-    const int64_t b = bt / vt, s0 = (bt - b * vt) * kVTokens;
+    const uint32_t bt = fastdiv((uint32_t)index, a.kv_div);
+    const int64_t g = (uint32_t)index - bt * a.kv_div.d;
+    const uint32_t b32 = fastdiv(bt, a.vtiles_div);
+    const int64_t b = b32, s0 = (int64_t)(bt - b32 * a.vtiles_div.d) * kVTokens;
     const int64_t rows = std::min<int64_t>(kVTokens, a.seq - s0);
     T *out = a.v_out + ((b * a.kv_heads + g) * a.seq + s0) * DIM;
     const T *in = a.v_in + (b * a.seq + s0) * a.v_in_tok + g * DIM;
@@ -213,35 +222,38 @@ __device__ __forceinline__ void v_tile(const PrepArgs<T> &a, int64_t index) {
     }
 }
 
-// Q, K and V workgroups are dealt through the grid in proportion (block i is a
-// Q block when floor((i+1)*nq/n') > floor(i*nq/n') over the first n' = 9n/10
-// blocks; the others split between K and V the same way, the K tiles over the
-// first 3/4 of them), so every role streams from the first wave of workgroups,
-// the long K tiles finish early and the short V tiles fill the launch's tail.
+// Q, K and V workgroups are dealt through the grid in proportion: the count of
+// Q blocks among blocks [0, i] is f(i) = floor((i+1) * rq / 2^32) over the
+// first nq = 9n/10 blocks, and block i is a Q block when f(i) > f(i-1); the
+// other blocks split between K and V the same way, the K tiles over the first
+// 3/4 of them.  So every role streams from the first wave of workgroups, the
+// long K tiles finish early and the short V tiles fill the launch's tail.  The
+// rates are fixed-point multipliers computed on the host, and the K/V tile
+// indices split with multiply-high divisions: the 64-bit divisions they replace
+// (about a hundred scalar instructions each before a workgroup's first load)
+// cost 1-2% of the launch at 8 x 2048 tokens.
 template <typename T, int LPR, int RPGQ>
 __global__ __launch_bounds__(kBlock) void attention_prepare_fast(PrepArgs<T> a) {
     // Q blocks over the first 9/10 of the grid, so the last stretch holds
     // only V tiles, the shortest workgroups (2-3% faster at 8 x 2048 tokens
     // than over the whole grid; 8/10 no better)
-    const int64_t i = blockIdx.x, n = a.q_blocks + a.k_blocks + a.v_blocks;
-    const int64_t nq = std::max<int64_t>(a.q_blocks, n * 9 / 10);
-    const int64_t iq = i < nq ? i : nq - 1;
-    const int64_t q_upto = i < nq ? (iq + 1) * a.q_blocks / nq : a.q_blocks;  // Q among [0, i]
-    if (i < nq && q_upto > iq * a.q_blocks / nq) {
+    const uint64_t i = blockIdx.x;
+    const bool in_q = i < (uint64_t)a.nq;
+    const int64_t q_upto = in_q ? (int64_t)(((i + 1) * a.rq) >> 32) : a.q_blocks;  // Q among [0, i]
+    if (in_q && q_upto > (int64_t)((i * a.rq) >> 32)) {
         qk_side_contig<T, LPR, RPGQ>(a.qk, a.qk.q, q_upto - 1);
         return;
     }
     // K tiles, the longest workgroups, are dealt over the first 3/4 of the
     // non-Q blocks only, so none starts in the launch's last stretch (2-3%
     // faster at 8 x 2048 tokens than dealing them over all, 1/4-5/8 in between)
-    const int64_t j = i - q_upto, m = a.k_blocks + a.v_blocks;
-    const int64_t mk = std::max<int64_t>(a.k_blocks, m * 3 / 4);
-    const int64_t jk = j < mk ? j : mk - 1;
-    const int64_t k_upto = j < mk ? (jk + 1) * a.k_blocks / mk : a.k_blocks;  // K among [0, j]
-    if (j < mk && k_upto > jk * a.k_blocks / mk)
+    const uint64_t j = i - (uint64_t)q_upto;
+    const bool in_k = j < (uint64_t)a.mk;
+    const int64_t k_upto = in_k ? (int64_t)(((j + 1) * a.rk) >> 32) : a.k_blocks;  // K among [0, j]
+    if (in_k && k_upto > (int64_t)((j * a.rk) >> 32))
         k_tile<T, LPR>(a, k_upto - 1);
     else
-        v_tile<T, LPR>(a, j - k_upto);
+        v_tile<T, LPR>(a, (int64_t)j - k_upto);
 }
 
 // General path: one wavefront per row; rows [0, tokens*heads) are Q, then
@@ -325,8 +337,23 @@ int32_t launch_fast(PrepArgs<T> a, hipStream_t stream) {
     constexpr int64_t gpb = kBlock / LPR;
     a.q_blocks = ceil_div(a.qk.q.rows / RPGQ, gpb);
     a.k_blocks = a.batch * a.tiles * a.kv_heads;
-    a.v_blocks = a.batch * ((a.seq + kVTokens - 1) / kVTokens) * a.kv_heads;
+    const int64_t vtiles = (a.seq + kVTokens - 1) / kVTokens;
+    a.v_blocks = a.batch * vtiles * a.kv_heads;
     const int64_t blocks = a.q_blocks + a.k_blocks + a.v_blocks;
+    // fixed-point dealing rates: ceil(count * 2^32 / span) <= 2^32, so the
+    // count of a role among the first `span` blocks is exactly `count`
+    // (span < 2^32) and it grows by at most one per block
+    auto rate = [](int64_t count, int64_t span) {
+        return span > 0 ? (((uint64_t)count << 32) + (uint64_t)span - 1) / (uint64_t)span : 0;
+    };
+    a.nq = std::max<int64_t>(a.q_blocks, blocks * 9 / 10);
+    a.rq = rate(a.q_blocks, a.nq);
+    const int64_t m = a.k_blocks + a.v_blocks;
+    a.mk = std::max<int64_t>(a.k_blocks, m * 3 / 4);
+    a.rk = rate(a.k_blocks, a.mk);
+    a.kv_div = make_fastdiv((uint32_t)a.kv_heads);
+    a.tiles_div = make_fastdiv((uint32_t)std::max<int64_t>(a.tiles, 1));
+    a.vtiles_div = make_fastdiv((uint32_t)std::max<int64_t>(vtiles, 1));
     hipLaunchKernelGGL((attention_prepare_fast<T, LPR, RPGQ>), dim3((uint32_t)blocks),
                        dim3(kBlock), 0, stream, a);
     return launch_status();

@@ -266,9 +266,19 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
 }
 
 // 1/sqrt(sum/width + eps) in fp32, the reference's operation order
-// (src/backbone_cpu.jl:344): divide, add, square root, reciprocal.
+// (src/backbone_cpu.jl:344): divide, add, square root, reciprocal.  For a
+// power-of-two width (uniform: a kernel argument) the division is a multiply by
+// the exact reciprocal 2^-k, the same correctly rounded quotient without the
+// division sequence.
 __device__ __forceinline__ float rms_scale(float sum_squares, float width, float eps) {
-    return 1.0f / __builtin_sqrtf(sum_squares / width + eps);
+    const uint32_t wb = __float_as_uint(width);
+    const uint32_t e = wb & 0x7f800000u;
+    float mean;
+    if ((wb & 0x807fffffu) == 0u && e >= 0x3f800000u && e <= 0x7e800000u)  // 2^k, 0 <= k <= 126
+        mean = sum_squares * __uint_as_float(0x7f000000u - e);
+    else
+        mean = sum_squares / width;
+    return 1.0f / __builtin_sqrtf(mean + eps);
 }
 
 // silu(x) = x * (1/(1 + exp(-x))) (src/backbone.jl:196-197).  exp(-x) is
