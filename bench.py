@@ -1298,7 +1298,7 @@ def _kernel_table(segments, per, gemm="hipBLASLt GEMM", unit_ms=True):
 
 
 def summarize_forward(out_dir, commit):
-    """Write profiles/backbone_forward_kernels.md, split_gemm_inputs_forward.md
+    """Write profiles/backbone_forward_kernels.md, other_modes_forward.md
     and decision_latency_kernels.md from the end-to-end and decision traces
     under `out_dir` (FORWARD_COMMANDS) and the untraced bench line of the same
     commit in `out_dir`/bench.log."""
