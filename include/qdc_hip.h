@@ -68,9 +68,10 @@ typedef enum {
  * library that was built from it, so a host can refuse a library whose entry
  * points it was not compiled against.  The minor number changes with any
  * signature change of an existing entry point (0.2.0: qdc_gated_rmsnorm and
- * qdc_swiglu take out_dtype before the stream).
+ * qdc_swiglu take out_dtype before the stream), the patch number with added
+ * entry points (0.2.1: qdc_row_scale, qdc_row_scale_check).
  */
-#define QDC_HIP_VERSION "qdc_hip 0.2.0"
+#define QDC_HIP_VERSION "qdc_hip 0.2.1"
 
 /* Library version string ("qdc_hip <major>.<minor>.<patch>"), QDC_HIP_VERSION. */
 const char *qdc_version(void);
@@ -414,6 +415,29 @@ int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows, int64_t n
  * beside the kernel and its same-size copy.
  */
 int32_t qdc_empty(int64_t workgroups, hipStream_t stream);
+
+/*
+ * out[i] = 1 / sqrt(sum_squares[i] / width + eps), fp32, exactly as every
+ * RMSNorm kernel of this library scales a row with that sum of squares: the
+ * division (a multiply by 2^-k when width is a power of two), the add, then
+ * RN(1 / RN(sqrt(.))) as 1.0f / sqrtf computes it (n < 2^32 - 256; out may
+ * equal sum_squares).  No counterpart in the reference: it exposes the row
+ * scale of cpu_rmsnorm! (src/backbone_cpu.jl:344) so that tests can compare it
+ * with the CPU's correctly rounded square root and division.
+ */
+int32_t qdc_row_scale(float *out, const float *sum_squares, int64_t n, float width, float eps,
+                      hipStream_t stream);
+
+/*
+ * Adds to *mismatches (a device uint64) the number of fp32 bit patterns
+ * first + k, 0 <= k < count (count <= 2^32 - first), for which the row
+ * kernels' 1 / sqrt(x) differs in any bit from the general expression
+ * 1.0f / sqrtf(x) (two NaN results count as equal).  No counterpart in the
+ * reference: a self-check of the short hardware-estimate sequence the row
+ * kernels use for 2^-96 <= x < inf; a sweep of all 2^32 patterns finds none.
+ */
+int32_t qdc_row_scale_check(uint32_t first, int64_t count, uint64_t *mismatches,
+                            hipStream_t stream);
 
 #ifdef __cplusplus
 }

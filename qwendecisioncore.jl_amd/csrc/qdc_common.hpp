@@ -265,11 +265,35 @@ template <int N> __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// 1 / sqrt(x) as two correctly rounded operations, RN(1 / RN(sqrt(x))): the
+// value of 1.0f / sqrtf(x).  For 2^-96 <= x < inf it is built from the hardware
+// estimates: v_sqrt_f32's root r is within one ulp, and the residuals
+// x - (r -/+ ulp) * r, exact with FMA, pick the rounded root among r - ulp, r and
+// r + ulp (the correction LLVM's AMDGPU lowering applies to its f32 square
+// root); v_rcp_f32's reciprocal q of that root is refined by one Newton step
+// with FMA, q + q * (1 - y * q) (Markstein).  About 12 instructions instead of
+// the ~30 of the general sequences, which rescale small inputs and handle
+// division overflow.  Equal bit for bit to the general expression for every
+// float in that range on MI355X (qdc_row_scale_check sweeps all 2^32 bit
+// patterns); other inputs (zero, tiny, inf, NaN, negative) take the general
+// expression itself.
+__device__ __forceinline__ float inv_sqrt_rn(float x) {
+    if (!(x >= 0x1p-96f && x < __builtin_inff())) return 1.0f / __builtin_sqrtf(x);
+    const float r = __builtin_amdgcn_sqrtf(x);
+    const float dn = __uint_as_float(__float_as_uint(r) - 1u);
+    const float up = __uint_as_float(__float_as_uint(r) + 1u);
+    float y = r;
+    if (__builtin_fmaf(-dn, r, x) <= 0.0f) y = dn;
+    if (__builtin_fmaf(-up, r, x) > 0.0f) y = up;
+    const float q = __builtin_amdgcn_rcpf(y);
+    return __builtin_fmaf(__builtin_fmaf(-y, q, 1.0f), q, q);
+}
+
 // 1/sqrt(sum/width + eps) in fp32, the reference's operation order
 // (src/backbone_cpu.jl:344): divide, add, square root, reciprocal.  For a
 // power-of-two width (uniform: a kernel argument) the division is a multiply by
 // the exact reciprocal 2^-k, the same correctly rounded quotient without the
-// division sequence.
+// division sequence; the square root and reciprocal are inv_sqrt_rn.
 __device__ __forceinline__ float rms_scale(float sum_squares, float width, float eps) {
     const uint32_t wb = __float_as_uint(width);
     const uint32_t e = wb & 0x7f800000u;
@@ -278,7 +302,7 @@ __device__ __forceinline__ float rms_scale(float sum_squares, float width, float
         mean = sum_squares * __uint_as_float(0x7f000000u - e);
     else
         mean = sum_squares / width;
-    return 1.0f / __builtin_sqrtf(mean + eps);
+    return inv_sqrt_rn(mean + eps);
 }
 
 // silu(x) = x * (1/(1 + exp(-x))) (src/backbone.jl:196-197).  exp(-x) is

@@ -386,10 +386,57 @@ int32_t residual_rmsnorm(void *residual, void *out, const void *x, const void *m
     return run<float, bf16_t, float, Mode::kResidual, true>(a, stream);
 }
 
+// out[i] = rms_scale(sum_squares[i], width, eps), the scale every row kernel
+// applies to a row with that sum of squares.
+__global__ __launch_bounds__(kBlock) void row_scale_map(float *out, const float *ss, int64_t n,
+                                                        float width, float eps) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i < n) out[i] = rms_scale(ss[i], width, eps);
+}
+
+// Adds to *mismatches the number of bit patterns first + k, k < count, whose
+// inv_sqrt_rn differs from the general expression 1.0f / sqrtf in any bit (two
+// NaN results count as equal).  Grid-stride over k; one atomic per thread that
+// found any.
+constexpr uint32_t kCheckBlocks = 8192;
+__global__ __launch_bounds__(kBlock) void row_scale_check(uint32_t first, uint64_t count,
+                                                          unsigned long long *mismatches) {
+    uint32_t n = 0;
+    const uint64_t stride = (uint64_t)kCheckBlocks * kBlock;
+    for (uint64_t k = (uint64_t)blockIdx.x * kBlock + threadIdx.x; k < count; k += stride) {
+        const float x = __uint_as_float(first + (uint32_t)k);
+        const float a = inv_sqrt_rn(x), b = 1.0f / __builtin_sqrtf(x);
+        n += (__float_as_uint(a) != __float_as_uint(b)) && !(a != a && b != b);
+    }
+    if (n) atomicAdd(mismatches, (unsigned long long)n);
+}
+
 }  // namespace
 }  // namespace qdc
 
 using namespace qdc;
+
+extern "C" int32_t qdc_row_scale(float *out, const float *sum_squares, int64_t n, float width,
+                                 float eps, hipStream_t stream) {
+    if (n < 0 || n >= ((int64_t)1 << 32) - kBlock) return QDC_ERR_SHAPE;
+    if (n == 0) return QDC_OK;
+    if (!out || !sum_squares) return QDC_ERR_NULL;
+    if ((const void *)out != (const void *)sum_squares && overlaps(out, n * 4, sum_squares, n * 4))
+        return QDC_ERR_ALIAS;
+    hipLaunchKernelGGL(row_scale_map, dim3((uint32_t)ceil_div(n, kBlock)), dim3(kBlock), 0, stream,
+                       out, sum_squares, n, width, eps);
+    return launch_status();
+}
+
+extern "C" int32_t qdc_row_scale_check(uint32_t first, int64_t count, uint64_t *mismatches,
+                                       hipStream_t stream) {
+    if (count < 0 || count > ((int64_t)1 << 32) - (int64_t)first) return QDC_ERR_SHAPE;
+    if (!mismatches) return QDC_ERR_NULL;
+    if (count == 0) return QDC_OK;
+    hipLaunchKernelGGL(row_scale_check, dim3(kCheckBlocks), dim3(kBlock), 0, stream, first,
+                       (uint64_t)count, (unsigned long long *)mismatches);
+    return launch_status();
+}
 
 extern "C" int32_t qdc_rmsnorm(void *out, const void *x, const void *weight, int64_t rows,
                                int64_t width, int64_t ld_x, int64_t ld_out, float eps,

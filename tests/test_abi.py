@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 23, names
+    assert len(names) == 25, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -38,10 +38,11 @@ def test_exports_match_header():
 
 def test_version_matches_the_header():
     """qdc_version() is the QDC_HIP_VERSION of the header the library was built
-    from (0.2.0: out_dtype added to qdc_gated_rmsnorm and qdc_swiglu)."""
+    from (0.2.0: out_dtype added to qdc_gated_rmsnorm and qdc_swiglu; 0.2.1:
+    qdc_row_scale and qdc_row_scale_check added)."""
     m = re.search(r'#define\s+QDC_HIP_VERSION\s+"([^"]+)"', open(HEADER).read())
     assert m and re.fullmatch(r"qdc_hip \d+\.\d+\.\d+", m.group(1))
-    assert _lib.version() == m.group(1) == "qdc_hip 0.2.0"
+    assert _lib.version() == m.group(1) == "qdc_hip 0.2.1"
 
 
 def test_status_strings():
@@ -462,6 +463,23 @@ def test_empty_validation():
     assert lib.qdc_empty(-1, None) == -2
     assert lib.qdc_empty(1 << 24, None) == -2
     assert lib.qdc_empty(0, None) == 0
+
+
+def test_row_scale_validation():
+    lib = _lib.lib()
+    rs = lambda *a: lib.qdc_row_scale(*a, None)  # noqa: E731
+    assert rs(FAKE, FAKE, -1, 1.0, 0.0) == -2
+    assert rs(FAKE, FAKE, (1 << 32) - 256, 1.0, 0.0) == -2
+    assert rs(None, FAKE, 4, 1.0, 0.0) == -1
+    assert rs(FAKE, None, 4, 1.0, 0.0) == -1
+    assert rs(FAKE, FAKE + 4, 4, 1.0, 0.0) == -5     # partial overlap
+    assert rs(None, None, 0, 1.0, 0.0) == 0
+    ck = lambda *a: lib.qdc_row_scale_check(*a, None)  # noqa: E731
+    assert ck(0, -1, FAKE) == -2
+    assert ck(0, (1 << 32) + 1, FAKE) == -2
+    assert ck(16, (1 << 32) - 15, FAKE) == -2         # past the last pattern
+    assert ck(0, 1 << 32, None) == -1
+    assert ck(5, 0, FAKE) == 0
 
 
 def test_c_host_program_host_only(tmp_path):

@@ -1094,6 +1094,47 @@ def test_device_copy_shapes(cpt, block):
                         torch.empty(32, dtype=torch.uint8, device=DEV), 3, 256)
 
 
+# ---------------------------------------------------------------- row scale --
+def test_row_scale_check_every_pattern():
+    """The row kernels take 1/sqrt(x) from the hardware square root and
+    reciprocal estimates with one-ulp corrections for 2^-96 <= x < inf; over
+    all 2^32 fp32 bit patterns it equals the general 1.0f / sqrtf(x) in every
+    bit (qdc_row_scale_check counts the differences on the device)."""
+    from qdc_amd import _lib
+    lib = _lib.lib()
+    count = torch.zeros(1, dtype=torch.int64, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    step = 1 << 30
+    for first in range(0, 1 << 32, step):
+        assert lib.qdc_row_scale_check(first, step, count.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(count.item()) == 0
+
+
+@pytest.mark.parametrize("width,eps", [(1.0, 0.0), (256.0, 1e-6), (1000.0, 1e-6), (3.0, 1e-5)])
+def test_row_scale_matches_numpy(width, eps):
+    """qdc_row_scale, the scale the row kernels apply, against numpy's correctly
+    rounded float32 divide, add, square root and reciprocal, bit for bit, on 4M
+    random bit patterns and the boundary values (zeros, denormals, 2^-96 and its
+    neighbours, the largest finite value, infinities, NaN, negatives)."""
+    from qdc_amd import _lib
+    lib = _lib.lib()
+    special = np.array([0, 0x80000000, 1, 0x007FFFFF, 0x00800000, 0x0F7FFFFF, 0x0F800000,
+                        0x0F800001, 0x2F800000, 0x3F800000, 0x3F800001, 0x7F7FFFFF, 0x7F800000,
+                        0xFF800000, 0x7FC00000, 0xBF800000, 0x358637BD], dtype=np.uint32)
+    bits = np.random.default_rng(11).integers(0, 1 << 32, size=1 << 22, dtype=np.uint64)
+    x = np.concatenate([special, bits.astype(np.uint32)]).view(np.float32)
+    with np.errstate(all="ignore"):
+        exp = np.float32(1) / np.sqrt(x / np.float32(width) + np.float32(eps))
+    xd = torch.from_numpy(x).to(DEV)
+    out = torch.empty_like(xd)
+    assert lib.qdc_row_scale(out.data_ptr(), xd.data_ptr(), x.size, width, eps,
+                             torch.cuda.current_stream().cuda_stream) == 0
+    got = out.cpu().numpy()
+    same = (got.view(np.uint32) == exp.view(np.uint32)) | (np.isnan(got) & np.isnan(exp))
+    assert same.all(), x[~same][:8]
+
+
 # ------------------------------------------------------ attention prologue ----
 PREP_CASES = [
     # B, S, H, KV, hd, rotary, packed [q|k|v|gate] (else q read from interleaved q||gate), offset
