@@ -85,6 +85,16 @@ def _sets(set_bytes: int) -> int:
     return max(2, math.ceil(ROTATE_BYTES / set_bytes))
 
 
+def _qkv_views(tokens, heads, dim, dev):
+    """q, k, v [tokens, heads, dim] fp32 as the column blocks of one
+    [tokens, q|k|v] buffer (the DeltaNet prologue's output layout in the
+    forward)."""
+    import torch
+    w = heads * dim
+    qkv = torch.empty((tokens, 3 * w), dtype=torch.float32, device=dev)
+    return tuple(qkv[:, i * w:(i + 1) * w].view(tokens, heads, dim) for i in range(3))
+
+
 class Kernel:
     """One fused kernel at its benchmark shape with rotating buffer sets."""
 
@@ -227,8 +237,10 @@ def build_kernels(dev):
         "bfloat16", group="next"))
 
     # DeltaNet prologue of one layer: 16384 tokens, 16 key/value heads of 128,
-    # packed projection [qkv | z | a | b] in bf16 (z is not read), fp32 outputs;
-    # rows padded to a multiple of 256 columns as the backbone packs the weight.
+    # packed projection [qkv | z | a | b] in bf16 (z is not read), fp32 outputs
+    # q, k, v as the column blocks of one [T, q|k|v] buffer, as the forward
+    # writes them; rows padded to a multiple of 256 columns as the backbone
+    # packs the weight.
     Tp, hp, dp = 16384, 16, 128
     cqp = 3 * hp * dp
     widthp = -(-(cqp + hp * dp + 2 * hp) // 256) * 256
@@ -238,10 +250,7 @@ def build_kernels(dev):
     kernels.append(Kernel(
         "delta_prologue_bf16", "delta_prologue_fast",
         Tp * (cqp + 2 * hp) * 2 + Tp * (cqp + 2 * hp) * 4 + cqp * 4 * 4 + 2 * hp * 4,
-        lambda i: (randn((Tp, widthp), bf),
-                   torch.empty((Tp, hp, dp), dtype=f32, device=dev),
-                   torch.empty((Tp, hp, dp), dtype=f32, device=dev),
-                   torch.empty((Tp, hp, dp), dtype=f32, device=dev),
+        lambda i: (randn((Tp, widthp), bf), *_qkv_views(Tp, hp, dp, dev),
                    torch.empty((Tp, hp), dtype=f32, device=dev),
                    torch.empty((Tp, hp), dtype=f32, device=dev)),
         lambda s: ops.delta_prologue(s[0], convp, a_dec, dtb, 2048, hp, dp, hp, dp, out=s[1:]),
@@ -251,10 +260,13 @@ def build_kernels(dev):
     # per-token state update, reported with its bytes for reference)
     Bs, Ss = 8, 2048
 
-    def scan_set(i):
-        qs = torch.nn.functional.normalize(randn((Bs, Ss, hp, dp), f32), dim=-1) / math.sqrt(dp)
-        ks = torch.nn.functional.normalize(randn((Bs, Ss, hp, dp), f32), dim=-1)
-        return (qs, ks, randn((Bs, Ss, hp, dp), f32),
+    def scan_set(i):  # q, k, v read from one [tokens, q|k|v] buffer, as in the forward
+        qkv = torch.empty((Bs, Ss, 3, hp, dp), dtype=f32, device=dev)
+        qkv[:, :, 0] = torch.nn.functional.normalize(randn((Bs, Ss, hp, dp), f32),
+                                                     dim=-1) / math.sqrt(dp)
+        qkv[:, :, 1] = torch.nn.functional.normalize(randn((Bs, Ss, hp, dp), f32), dim=-1)
+        qkv[:, :, 2] = randn((Bs, Ss, hp, dp), f32)
+        return (qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2],
                 torch.sigmoid(randn((Bs, Ss, hp), f32)), -torch.rand((Bs, Ss, hp), generator=g,
                                                                         device=dev),
                 torch.empty((Bs, Ss, hp, dp), dtype=bf, device=dev))
@@ -666,8 +678,10 @@ def widened_sequence(cfg, dev, batch, seq):
     proj = rn((T, cq + vh * vd + 2 * vh), bf)
     conv = rn((cq, cfg.conv_kernel), f32)
     a_dec, dtb = -torch.exp(rn((vh,), f32)), rn((vh,), f32)
-    outs = [torch.empty(sh, dtype=f32, device=dev)
-            for sh in ((T, kh, kd), (T, kh, kd), (T, vh, vd), (T, vh), (T, vh))]
+    qkv = torch.empty((T, cq), dtype=f32, device=dev)  # the forward's [T, q|k|v] rows
+    outs = [qkv[:, :kh * kd].view(T, kh, kd), qkv[:, kh * kd:2 * kh * kd].view(T, kh, kd),
+            qkv[:, 2 * kh * kd:].view(T, vh, vd)]
+    outs += [torch.empty((T, vh), dtype=f32, device=dev) for _ in range(2)]
     scanned = torch.empty((batch, seq, vh, vd), dtype=bf, device=dev)
     scale = 1.0 / math.sqrt(hd)
 

@@ -68,10 +68,12 @@ typedef enum {
  * library that was built from it, so a host can refuse a library whose entry
  * points it was not compiled against.  The minor number changes with any
  * signature change of an existing entry point (0.2.0: qdc_gated_rmsnorm and
- * qdc_swiglu take out_dtype before the stream), the patch number with added
- * entry points (0.2.1: qdc_row_scale, qdc_row_scale_check).
+ * qdc_swiglu take out_dtype before the stream; 0.3.0: qdc_delta_prologue and
+ * qdc_delta_scan take the q/k and v row strides ld_qk, ld_v before the
+ * stream), the patch number with added entry points (0.2.1: qdc_row_scale,
+ * qdc_row_scale_check).
  */
-#define QDC_HIP_VERSION "qdc_hip 0.2.1"
+#define QDC_HIP_VERSION "qdc_hip 0.3.0"
 
 /* Library version string ("qdc_hip <major>.<minor>.<patch>"), QDC_HIP_VERSION. */
 const char *qdc_version(void);
@@ -315,15 +317,19 @@ int32_t qdc_swiglu(void *out, const void *gate, const void *up, int64_t tokens, 
  * row kernels; provided so backbone_hidden runs at speed.  Per sequence b and
  * value head h (key head h / (heads / key_heads)), state S[value_dim, key_dim]
  * from zero, for t = 0..seq-1:  f = exp(decay);  u = beta*(v - f*S k);
- * S = f*S + u k^T;  out = S q.  Contiguous fp32 inputs q, k [batch, seq,
- * key_heads, key_dim] (q already L2-normalised and scaled), v [batch, seq,
- * heads, value_dim], beta and decay [batch, seq, heads]; out [batch, seq,
- * heads, value_dim] in out_dtype.  key_dim 1..256.
+ * S = f*S + u k^T;  out = S q.  fp32 inputs: q, k [batch, seq, key_heads,
+ * key_dim] (q already L2-normalised and scaled) with their token rows ld_qk
+ * elements apart, v [batch, seq, heads, value_dim] with rows ld_v apart
+ * (ld_qk >= key_heads*key_dim, ld_v >= heads*value_dim: contiguous tensors
+ * pass those widths, the column blocks of qdc_delta_prologue's one
+ * [tokens, q|k|v] buffer pass its row length), beta and decay [batch, seq,
+ * heads] contiguous; out [batch, seq, heads, value_dim] contiguous in
+ * out_dtype.  key_dim 1..256.
  */
 int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, const float *k,
                        const float *v, const float *beta, const float *decay, int64_t batch,
                        int64_t seq, int64_t heads, int64_t key_heads, int64_t key_dim,
-                       int64_t value_dim, hipStream_t stream);
+                       int64_t value_dim, int64_t ld_qk, int64_t ld_v, hipStream_t stream);
 
 /*
  * DeltaNet prologue in one pass over the packed projection rows
@@ -333,16 +339,23 @@ int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, const float
  * [channels, taps], tap 0 on the oldest row), SiLU, then per key head
  * q / (sqrt(sum(q^2) + 1e-6) * sqrt(kd)) and k / sqrt(sum(k^2) + 1e-6); v
  * passes through; beta = sigmoid(b), decay = a_decay * softplus(a + dt_bias).
- * Outputs fp32, contiguous: q, k [tokens, kh*kd], v [tokens, vh*vd], beta and
- * decay [tokens, vh].  Replaces causal_depthwise_kernel!, qk_normalize_kernel!
- * and the beta/decay broadcasts (ext/amdgpu_delta.jl:1-33, 83-113, 154-159;
- * generic src/backbone.jl:264-296; CPU src/backbone_cpu.jl:411-427, 501-533).
+ * Outputs fp32: q, k [tokens, kh*kd] with token rows ld_qk elements apart,
+ * v [tokens, vh*vd] with rows ld_v apart (ld_qk >= kh*kd, ld_v >= vh*vd),
+ * beta and decay [tokens, vh] contiguous.  Separate contiguous q, k, v pass
+ * their widths; one [tokens, q|k|v] buffer (q, k, v its column blocks, the
+ * layout the forward uses: each token's outputs one contiguous row) passes
+ * its row length 2*kh*kd + vh*vd for both.  q, k and v may share rows only
+ * as disjoint column blocks (QDC_ERR_ALIAS otherwise).  Replaces
+ * causal_depthwise_kernel!, qk_normalize_kernel! and the beta/decay
+ * broadcasts (ext/amdgpu_delta.jl:1-33, 83-113, 154-159; generic
+ * src/backbone.jl:264-296; CPU src/backbone_cpu.jl:411-427, 501-533).
  */
 int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta, float *decay,
                            const void *proj, int32_t proj_dtype, int64_t ld, const float *conv,
                            int64_t taps, const float *a_decay, const float *dt_bias,
                            int64_t tokens, int64_t seq_len, int64_t key_heads, int64_t key_dim,
-                           int64_t value_heads, int64_t value_dim, hipStream_t stream);
+                           int64_t value_heads, int64_t value_dim, int64_t ld_qk, int64_t ld_v,
+                           hipStream_t stream);
 
 /*
  * Masked, scaled softmax of attention score rows: scores fp32 [batch, heads,

@@ -36,6 +36,7 @@ struct Prologue {
     const float *conv;      // [channels, taps]
     const float *a_decay, *dt_bias;
     float *q, *k, *v, *beta, *decay;
+    int64_t ld_qk, ld_v;    // elements between the token rows of q and k, and of v
     int64_t tokens;
     FastDiv seq;            // sequence length (positions reset per sequence)
     int kh, kd, vh, vd, taps;
@@ -132,9 +133,9 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
 #pragma unroll
         for (int j = 0; j < kTaps; ++j) w[c][j] = live ? a.conv[(c0 + c) * kTaps + j] : 0.0f;
 
-    const int64_t kw = (int64_t)a.kh * a.kd, vw = (int64_t)a.vh * a.vd;
+    const int64_t kw = (int64_t)a.kh * a.kd;
     // this thread's output chunk of token t0 and the stride between tokens
-    const int64_t dstride = is_qk ? kw : vw;
+    const int64_t dstride = is_qk ? a.ld_qk : a.ld_v;
     float *dst = (is_q ? a.q + c0 : is_k ? a.k + (c0 - kw) : a.v + (c0 - 2 * kw)) + t0 * dstride;
     const float qk_mul = is_q ? a.inv_sqrt_kd : 1.0f;
     // A later sequence starts inside the tile only when fewer than kTileT
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_general(Prologue a) {
     if (seg < 2 * a.kh) {  // a q or k head
         const bool is_q = seg < a.kh;
         const int64_t c0 = (int64_t)seg * a.kd;
-        float *dst = is_q ? a.q + t * kw + c0 : a.k + t * kw + (c0 - kw);
+        float *dst = is_q ? a.q + t * a.ld_qk + c0 : a.k + t * a.ld_qk + (c0 - kw);
         float ss = 0.0f;
         for (int i = lane; i < a.kd; i += kWave) {
             const float m = conv_silu(c0 + i);
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_general(Prologue a) {
                                  : 1.0f / __builtin_sqrtf(ss + 1e-6f);
         for (int i = lane; i < a.kd; i += kWave) dst[i] = dst[i] * scale;
     } else if (seg == 2 * a.kh) {  // the v block
-        for (int64_t i = lane; i < vw; i += kWave) a.v[t * vw + i] = conv_silu(2 * kw + i);
+        for (int64_t i = lane; i < vw; i += kWave) a.v[t * a.ld_v + i] = conv_silu(2 * kw + i);
     } else {  // gates
         for (int h = lane; h < a.vh; h += kWave) {
             a.beta[t * a.vh + h] = sigmoid_f(to_f32(proj[t * a.ld + a.b_off + h]));
@@ -231,6 +232,25 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_general(Prologue a) {
                 a.a_decay[h] * softplus_f(to_f32(proj[t * a.ld + a.a_off + h]) + a.dt_bias[h]);
         }
     }
+}
+
+// An output of `width` floats per token row, rows `ld` floats apart.
+struct OutRows {
+    const float *p;
+    int64_t width, ld;
+    int64_t span(int64_t tokens) const { return ((tokens - 1) * ld + width) * 4; }
+};
+
+// Two outputs never write the same float: their spans do not overlap (separate
+// buffers), or they share a row stride and are disjoint column blocks of the
+// same rows (one [tokens, q|k|v] buffer).
+bool disjoint_rows(const OutRows &a, const OutRows &b, int64_t tokens) {
+    if (!overlaps(a.p, a.span(tokens), b.p, b.span(tokens))) return true;
+    if (a.ld != b.ld) return false;
+    const int64_t bytes = (const char *)b.p - (const char *)a.p;
+    if (bytes % 4) return false;
+    const int64_t d = ((bytes / 4) % a.ld + a.ld) % a.ld;  // b's column offset within a's rows
+    return d >= a.width && d + b.width <= a.ld;
 }
 
 template <typename T, int TILE>
@@ -296,7 +316,8 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
                                       const float *conv, int64_t taps, const float *a_decay,
                                       const float *dt_bias, int64_t tokens, int64_t seq_len,
                                       int64_t key_heads, int64_t key_dim, int64_t value_heads,
-                                      int64_t value_dim, hipStream_t stream) {
+                                      int64_t value_dim, int64_t ld_qk, int64_t ld_v,
+                                      hipStream_t stream) {
     if (!valid_dtype(proj_dtype)) return QDC_ERR_DTYPE;
     if (tokens < 0 || seq_len <= 0 || key_heads <= 0 || key_dim <= 0 || value_heads <= 0 ||
         value_dim <= 0 || taps <= 0 || taps > 64)
@@ -304,6 +325,7 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
     const int64_t kw = key_heads * key_dim, vw = value_heads * value_dim;
     const int64_t cq = 2 * kw + vw;
     if (ld < cq + vw + 2 * value_heads) return QDC_ERR_SHAPE;
+    if (ld_qk < kw || ld_v < vw) return QDC_ERR_SHAPE;
     if (tokens == 0) return QDC_OK;
     if (tokens >= ((int64_t)1 << 26) || seq_len >= ((int64_t)1 << 31) || cq >= ((int64_t)1 << 28) ||
         key_heads > 32000)
@@ -312,9 +334,12 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
         return QDC_ERR_NULL;
     const int64_t es = elem_size(proj_dtype);
     const int64_t span_in = ((tokens - 1) * ld + ld) * es;
-    for (const void *o : {(const void *)q, (const void *)k, (const void *)v})
-        if (overlaps(o, tokens * (o == (const void *)v ? vw : kw) * 4, proj, span_in))
-            return QDC_ERR_ALIAS;
+    const OutRows outs[3] = {{q, kw, ld_qk}, {k, kw, ld_qk}, {v, vw, ld_v}};
+    for (int i = 0; i < 3; ++i) {
+        if (overlaps(outs[i].p, outs[i].span(tokens), proj, span_in)) return QDC_ERR_ALIAS;
+        for (int j = i + 1; j < 3; ++j)
+            if (!disjoint_rows(outs[i], outs[j], tokens)) return QDC_ERR_ALIAS;
+    }
     Prologue p{};
     p.proj = proj;
     p.ld = ld;
@@ -328,6 +353,8 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
     p.v = v;
     p.beta = beta;
     p.decay = decay;
+    p.ld_qk = ld_qk;
+    p.ld_v = ld_v;
     p.tokens = tokens;
     p.seq = make_fastdiv((uint32_t)seq_len);
     p.kh = (int)key_heads;
@@ -342,7 +369,8 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
     p.inv_sqrt_kd = 1.0f / p.sqrt_kd;
     // 4-channel pieces: 8-byte (bf16) or 16-byte (fp32) aligned projection rows
     const bool fast = ((uintptr_t)proj % (4 * es)) == 0 && (ld * es) % (4 * es) == 0 &&
-                      aligned16(q) && aligned16(k) && aligned16(v) && cq % 4 == 0;
+                      aligned16(q) && aligned16(k) && aligned16(v) && cq % 4 == 0 &&
+                      ld_qk % 4 == 0 && ld_v % 4 == 0;
     if (proj_dtype == QDC_BF16) return launch<bf16_t>(p, fast, stream);
     return launch<float>(p, fast, stream);
 }

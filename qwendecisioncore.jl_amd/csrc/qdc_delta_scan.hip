@@ -54,6 +54,7 @@ template <int KPL> __device__ __forceinline__ void read_keys(const float *row, i
 struct ScanArgs {
     void *out;
     const float *q, *k, *v, *beta, *decay;
+    int64_t ld_qk, ld_v;  // elements between the token rows of q and k, and of v
     int S, H, KH, KD, vd, groups;
 };
 
@@ -77,10 +78,11 @@ __global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
     const int g = h / a.groups;
     const int row0 = blockIdx.x * RB;            // first value row of the workgroup
     const int KD = a.KD, S = a.S;
-    const int64_t k_tok = (int64_t)a.KH * KD, v_tok = (int64_t)a.H * a.vd;
+    // input rows: q, k every ld_qk, v every ld_v elements; output rows contiguous
+    const int64_t k_tok = a.ld_qk, vi_tok = a.ld_v, v_tok = (int64_t)a.H * a.vd;
     const float *kb = a.k + (int64_t)b * S * k_tok + (int64_t)g * KD;
     const float *qb = a.q + (int64_t)b * S * k_tok + (int64_t)g * KD;
-    const float *vb = a.v + (int64_t)b * S * v_tok + (int64_t)h * a.vd;
+    const float *vb = a.v + (int64_t)b * S * vi_tok + (int64_t)h * a.vd;
     const float *bb = a.beta + (int64_t)b * S * a.H + h;
     const float *db = a.decay + (int64_t)b * S * a.H + h;
     TO *ob = reinterpret_cast<TO *>(a.out) + (int64_t)b * S * v_tok + (int64_t)h * a.vd;
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(kBlock) void delta_scan(ScanArgs a) {
         for (int p = 0; p < V_ITEMS; ++p) {
             const int idx = tid + p * kBlock;
             const int tt = idx / RB, r = idx - tt * RB;
-            rv[p] = (tt < n && row0 + r < a.vd) ? vb[(int64_t)(t0 + tt) * v_tok + row0 + r] : 0.0f;
+            rv[p] = (tt < n && row0 + r < a.vd) ? vb[(int64_t)(t0 + tt) * vi_tok + row0 + r] : 0.0f;
         }
         if (tid < n) {
             rb = bb[(int64_t)(t0 + tid) * a.H];
@@ -313,10 +315,11 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
     const int wrow = 16 * w;                      // this wavefront's rows within the workgroup
     const bool live = row0 + wrow < a.vd;         // value_dim % 16 == 0: whole tile or none
     const int S = a.S;
-    const int64_t k_tok = (int64_t)a.KH * KD, v_tok = (int64_t)a.H * a.vd;
+    // input rows: q, k every ld_qk, v every ld_v elements; output rows contiguous
+    const int64_t k_tok = a.ld_qk, vi_tok = a.ld_v, v_tok = (int64_t)a.H * a.vd;
     const float *kb = a.k + (int64_t)b * S * k_tok + (int64_t)g * KD;
     const float *qb = a.q + (int64_t)b * S * k_tok + (int64_t)g * KD;
-    const float *vb = a.v + (int64_t)b * S * v_tok + (int64_t)h * a.vd + row0;
+    const float *vb = a.v + (int64_t)b * S * vi_tok + (int64_t)h * a.vd + row0;
     const float *bb = a.beta + (int64_t)b * S * a.H + h;
     const float *db = a.decay + (int64_t)b * S * a.H + h;
     TO *ob = reinterpret_cast<TO *>(a.out) + (int64_t)b * S * v_tok + (int64_t)h * a.vd + row0;
@@ -342,7 +345,7 @@ __global__ __launch_bounds__(kBlock * KSPLIT) void delta_scan_chunked(ScanArgs a
             const int tt = tid / 16, r4 = (tid % 16) * 4;
             rv = f32x4{0.f, 0.f, 0.f, 0.f};
             if (tid < kC * kRowsWG / 4 && tt < n && row0 + r4 < a.vd)
-                rv = *reinterpret_cast<const f32x4 *>(vb + (int64_t)(t0 + tt) * v_tok + r4);
+                rv = *reinterpret_cast<const f32x4 *>(vb + (int64_t)(t0 + tt) * vi_tok + r4);
         }
         rs = 0.0f;
         if (tid < kC && tid < n) rs = bb[(int64_t)(t0 + tid) * a.H];
@@ -603,12 +606,14 @@ using namespace qdc;
 extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, const float *k,
                                   const float *v, const float *beta, const float *decay,
                                   int64_t batch, int64_t seq, int64_t heads, int64_t key_heads,
-                                  int64_t key_dim, int64_t value_dim, hipStream_t stream) {
+                                  int64_t key_dim, int64_t value_dim, int64_t ld_qk, int64_t ld_v,
+                                  hipStream_t stream) {
     if (!valid_dtype(out_dtype)) return QDC_ERR_DTYPE;
     if (batch < 0 || seq < 0 || heads <= 0 || key_heads <= 0 || value_dim <= 0 ||
         heads % key_heads)
         return QDC_ERR_SHAPE;
     if (key_dim <= 0 || key_dim > 256) return QDC_ERR_SHAPE;
+    if (ld_qk < key_heads * key_dim || ld_v < heads * value_dim) return QDC_ERR_SHAPE;
     if (batch == 0 || seq == 0) return QDC_OK;
     if (batch > 65535 || heads > 65535 || seq >= ((int64_t)1 << 31) ||
         value_dim >= ((int64_t)1 << 24))
@@ -621,6 +626,8 @@ extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, 
     a.v = v;
     a.beta = beta;
     a.decay = decay;
+    a.ld_qk = ld_qk;
+    a.ld_v = ld_v;
     a.S = (int)seq;
     a.H = (int)heads;
     a.KH = (int)key_heads;
@@ -635,7 +642,7 @@ extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, 
     const dim3 grid((uint32_t)ceil_div(value_dim, rb), (uint32_t)heads, (uint32_t)batch);
     // matrix-core chunked form: key_dim a multiple of 16 (<= 256), value_dim of 16
     if (key_dim % 16 == 0 && value_dim % 16 == 0 && aligned16(q) && aligned16(k) &&
-        aligned16(v)) {
+        aligned16(v) && ld_qk % 4 == 0 && ld_v % 4 == 0) {
         const dim3 cgrid((uint32_t)ceil_div(value_dim, kRowsWG), (uint32_t)heads,
                          (uint32_t)batch);
 #define QDC_CHUNKED(KB, KSPLIT)                                                                \
@@ -655,7 +662,7 @@ extern "C" int32_t qdc_delta_scan(void *out, int32_t out_dtype, const float *q, 
         QDC_CHUNKED(16, 2)
 #undef QDC_CHUNKED
     }
-    const bool vec = aligned16(q) && aligned16(k) && key_dim % 4 == 0;
+    const bool vec = aligned16(q) && aligned16(k) && key_dim % 4 == 0 && ld_qk % 4 == 0;
     const int64_t kpl = ceil_div(key_dim, kGroup);
 #define QDC_SCAN(KPL, R, VEC, TO)                                                              \
     hipLaunchKernelGGL((delta_scan<KPL, R, VEC, TO>), grid, dim3(kBlock), 0, stream, a);      \

@@ -48,7 +48,7 @@ qdc_library_path() = get(ENV, "QDC_HIP_LIBRARY", "libqdc_hip.so")
 # QDC_HIP_VERSION of the header these bindings follow; a library built from
 # another header is refused at load, since a changed signature would pass its
 # arguments in the wrong slots without any error.
-const QDC_HIP_VERSION = "qdc_hip 0.2.1"
+const QDC_HIP_VERSION = "qdc_hip 0.3.0"
 
 function qdc_open()
     handle = Libdl.dlopen(qdc_library_path())
@@ -197,21 +197,22 @@ qdc_swiglu(out, gate, up, tokens, width, ld_gate, ld_up, ld_out, dtype, out_dtyp
           out, gate, up, tokens, width, ld_gate, ld_up, ld_out, dtype, out_dtype, stream)
 
 qdc_delta_scan(out, out_dtype, q, k, v, beta, decay, batch, seq, heads, key_heads, key_dim,
-               value_dim, stream) =
+               value_dim, ld_qk, ld_v, stream) =
     ccall(qdc_sym(:qdc_delta_scan), Int32,
           (Ptr{Cvoid}, Int32, Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Ptr{Float32},
-           Ptr{Float32}, Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
+           Ptr{Float32}, Int64, Int64, Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
           out, out_dtype, q, k, v, beta, decay, batch, seq, heads, key_heads, key_dim,
-          value_dim, stream)
+          value_dim, ld_qk, ld_v, stream)
 
 qdc_delta_prologue(q, k, v, beta, decay, proj, proj_dtype, ld, conv, taps, a_decay, dt_bias,
-                   tokens, seq_len, key_heads, key_dim, value_heads, value_dim, stream) =
+                   tokens, seq_len, key_heads, key_dim, value_heads, value_dim, ld_qk, ld_v,
+                   stream) =
     ccall(qdc_sym(:qdc_delta_prologue), Int32,
           (Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Ptr{Cvoid},
            Int32, Int64, Ptr{Float32}, Int64, Ptr{Float32}, Ptr{Float32}, Int64, Int64, Int64,
-           Int64, Int64, Int64, Ptr{Cvoid}),
+           Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
           q, k, v, beta, decay, proj, proj_dtype, ld, conv, taps, a_decay, dt_bias, tokens,
-          seq_len, key_heads, key_dim, value_heads, value_dim, stream)
+          seq_len, key_heads, key_dim, value_heads, value_dim, ld_qk, ld_v, stream)
 
 qdc_attention_softmax(probs, probs_dtype, scores, mask, batch, heads, queries, keys, q_offset,
                       scale, stream) =
@@ -362,27 +363,31 @@ end
 # are already zero: the convolution + SiLU, the q/k normalisation and the
 # beta/decay broadcasts become one qdc_delta_prologue pass over the packed
 # projection, the recurrence one qdc_delta_scan, and the RMS + SiLU(z) broadcast
-# pair one qdc_gated_rmsnorm reading z in place inside the projection.
+# pair one qdc_gated_rmsnorm reading z in place inside the projection.  q, k and
+# v are the column blocks of one [q|k|v, tokens] buffer, so each token's
+# prologue output is one contiguous column (row stride 2*kh*kd + vh*vd).
 function amdgpu_delta_attention(attention, x::AMDGPU.ROCArray{Float32,2,ROCBuffer}, cfg)
     tokens = size(x, 2)
     kd, kh, vd, vh = cfg.key_dim, cfg.key_heads, cfg.value_dim, cfg.value_heads
     projected = QwenDecisionCore.native_linear(attention.packed_projection, x)
     ld = size(projected, 1)
     qkv_width = size(attention.qkv, 1)
-    q = scratch(Float32, (kd, kh, tokens))
-    k = scratch(Float32, (kd, kh, tokens))
-    v = scratch(Float32, (vd, vh, tokens))
+    qkv_rows = 2 * kh * kd + vh * vd
+    qkv = scratch(Float32, (qkv_rows, tokens))
+    q = qdc_fptr(qkv)
+    k = q + 4 * kh * kd
+    v = q + 8 * kh * kd
     beta = scratch(Float32, (vh, tokens))
     decay = scratch(Float32, (vh, tokens))
-    qdc_check(qdc_delta_prologue(qdc_fptr(q), qdc_fptr(k), qdc_fptr(v), qdc_fptr(beta),
-                                 qdc_fptr(decay), qdc_ptr(projected), QDC_F32, ld,
-                                 qdc_fptr(attention.conv), size(attention.conv, 1),
+    qdc_check(qdc_delta_prologue(q, k, v, qdc_fptr(beta), qdc_fptr(decay), qdc_ptr(projected),
+                                 QDC_F32, ld, qdc_fptr(attention.conv), size(attention.conv, 1),
                                  qdc_fptr(attention.a_decay), qdc_fptr(attention.dt_bias), tokens,
-                                 tokens, kh, kd, vh, vd, qdc_stream()), "delta_prologue")
+                                 tokens, kh, kd, vh, vd, qkv_rows, qkv_rows, qdc_stream()),
+              "delta_prologue")
     result = scratch(Float32, (vd, vh, tokens))
-    qdc_check(qdc_delta_scan(qdc_ptr(result), QDC_F32, qdc_fptr(q), qdc_fptr(k), qdc_fptr(v),
-                             qdc_fptr(beta), qdc_fptr(decay), 1, tokens, vh, kh, kd, vd,
-                             qdc_stream()), "delta_scan")
+    qdc_check(qdc_delta_scan(qdc_ptr(result), QDC_F32, q, k, v, qdc_fptr(beta), qdc_fptr(decay),
+                             1, tokens, vh, kh, kd, vd, qkv_rows, qkv_rows, qdc_stream()),
+              "delta_scan")
     gated = scratch(Float32, (vd * vh, tokens))
     qdc_check(qdc_gated_rmsnorm(qdc_ptr(gated), qdc_ptr(result), qdc_ptr(projected) + 4qkv_width,
                                 qdc_ptr(attention.norm), tokens, vh, vd, vd * vh, ld, vd * vh,

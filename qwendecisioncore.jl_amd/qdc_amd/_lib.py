@@ -49,9 +49,9 @@ SIGNATURES = {
                                  _i32, _i32, _vp]),
     "qdc_swiglu": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     "qdc_delta_scan": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
-                              _i64, _vp]),
+                              _i64, _i64, _i64, _vp]),
     "qdc_delta_prologue": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _vp,
-                                  _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
+                                  _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "qdc_attention_softmax": (_i32, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32,
                                      _vp]),
     "qdc_attention_gate": (_i32, [_vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64,

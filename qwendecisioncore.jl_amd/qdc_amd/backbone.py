@@ -336,9 +336,11 @@ class QwenBackbone:
         kw, vw = kd * kh, vd * vh
         cq = 2 * kw + vw
         proj = self._mm(x, layer["proj"])  # [T, cq + vw + 2*vh (+ zero padding)]
-        # conv + SiLU, q/k L2 norm and the beta/decay gates in one pass
+        # conv + SiLU, q/k L2 norm and the beta/decay gates in one pass; q, k, v
+        # are the column blocks of one [T, q|k|v] buffer (one output row per token)
         q, k, v, beta, decay = ops.delta_prologue(proj, layer["conv"], layer["a_decay"],
-                                                  layer["dt_bias"], S, kh, kd, vh, vd)
+                                                  layer["dt_bias"], S, kh, kd, vh, vd,
+                                                  interleaved=True)
         q, k = q.view(B, S, kh, kd), k.view(B, S, kh, kd)
         v, beta, decay = v.view(B, S, vh, vd), beta.view(B, S, vh), decay.view(B, S, vh)
         # recurrence straight into the model dtype the gated norm reads

@@ -564,21 +564,43 @@ def native_mlp_gate(gate: torch.Tensor, up: torch.Tensor,
     return out
 
 
+def _token_rows(t: torch.Tensor) -> int | None:
+    """Row stride (elements between consecutive tokens) of a ``[B, S, heads, dim]``
+    float32 view whose tokens are rows of ``heads * dim`` contiguous elements
+    (a contiguous tensor, or a column block of wider rows); None otherwise."""
+    B, S, heads, dim = t.shape
+    if t.dtype != torch.float32 or t.stride(3) != 1 or (heads > 1 and t.stride(2) != dim):
+        return None
+    ld = t.stride(1) if S > 1 else (t.stride(0) if B > 1 else heads * dim)
+    if ld < heads * dim or (B > 1 and S > 1 and t.stride(0) != S * ld):
+        return None
+    return ld
+
+
 def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
                decay: torch.Tensor, out_dtype: torch.dtype = torch.float32,
                out: torch.Tensor | None = None) -> torch.Tensor:
     """Gated delta rule recurrence (the DeltaNet "existing path", not a fused
-    row op): contiguous fp32 q, k ``[B, S, KH, kd]``, v ``[B, S, H, vd]``, beta and
-    decay ``[B, S, H]`` -> ``[B, S, H, vd]`` in ``out_dtype`` (or into ``out``)."""
+    row op): fp32 q, k ``[B, S, KH, kd]``, v ``[B, S, H, vd]`` whose tokens are
+    rows of contiguous heads (contiguous tensors, or the column blocks of one
+    ``[T, q|k|v]`` buffer that ``delta_prologue(..., interleaved=True)``
+    returns; q and k with the same row stride), contiguous beta and decay
+    ``[B, S, H]`` -> ``[B, S, H, vd]`` in ``out_dtype`` (or into ``out``)."""
     _device(q, k, v, beta, decay)
-    for t in (q, k, v, beta, decay):
+    for t in (beta, decay):
         if t.dtype != torch.float32 or not t.is_contiguous():
-            raise ValueError("delta_scan inputs must be contiguous float32 tensors")
+            raise ValueError("delta_scan beta and decay must be contiguous float32 tensors")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k and v must be [B, S, heads, dim]")
     B, S, KH, kd = k.shape
     H, vd = v.shape[2], v.shape[3]
     if q.shape != k.shape or v.shape[:2] != (B, S) or beta.shape != (B, S, H) or \
             decay.shape != (B, S, H):
         raise ValueError("inconsistent delta_scan shapes")
+    ld_q, ld_k, ld_v = _token_rows(q), _token_rows(k), _token_rows(v)
+    if ld_q is None or ld_k is None or ld_v is None or ld_q != ld_k:
+        raise ValueError("q, k and v must be float32 rows of contiguous heads, q and k with "
+                         "one row stride")
     if out is None:
         out = torch.empty((B, S, H, vd), dtype=out_dtype, device=q.device)
     _device(q, out)
@@ -587,17 +609,21 @@ def delta_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Te
     out_dtype = out.dtype
     check(lib().qdc_delta_scan(out.data_ptr(), _DTYPES[out_dtype], q.data_ptr(), k.data_ptr(),
                                v.data_ptr(), beta.data_ptr(), decay.data_ptr(), B, S, H, KH, kd,
-                               vd, _stream(q)), "delta_scan")
+                               vd, ld_k, ld_v, _stream(q)), "delta_scan")
     return out
 
 
 def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor,
                    dt_bias: torch.Tensor, seq_len: int, key_heads: int, key_dim: int,
-                   value_heads: int, value_dim: int, out=None):
+                   value_heads: int, value_dim: int, out=None, interleaved: bool = False):
     """DeltaNet prologue on the packed projection ``[T, q|k|v|z|a|b]`` (rows
     contiguous): causal conv + SiLU, q/k L2 norm, beta/decay gates.  Returns fp32
-    ``q, k [T, KH, kd]``, ``v [T, H, vd]``, ``beta, decay [T, H]`` (into ``out``,
-    a tuple of five such contiguous tensors, when given)."""
+    ``q, k [T, KH, kd]``, ``v [T, H, vd]``, ``beta, decay [T, H]``: contiguous
+    tensors, or with ``interleaved`` q, k and v as the column blocks of one
+    ``[T, q|k|v]`` buffer (each token's outputs one contiguous row, the layout
+    the forward uses; ``delta_scan`` reads it as is).  ``out``: a tuple of five
+    tensors of those shapes to write into instead (q, k, v rows of contiguous
+    heads, q and k with one row stride; beta and decay contiguous)."""
     _device(proj, conv, a_decay, dt_bias)
     if proj.dtype not in _DTYPES or proj.dim() != 2 or proj.stride(1) != 1:
         raise ValueError("proj must be a [tokens, width] float32/bfloat16 view with unit column stride")
@@ -618,18 +644,29 @@ def delta_prologue(proj: torch.Tensor, conv: torch.Tensor, a_decay: torch.Tensor
     shapes = [(T, key_heads, key_dim), (T, key_heads, key_dim), (T, value_heads, value_dim),
               (T, value_heads), (T, value_heads)]
     if out is None:
-        out = [torch.empty(sh, dtype=f32, device=dev) for sh in shapes]
-    elif any(o.dtype != f32 or tuple(o.shape) != sh or not o.is_contiguous()
-             for o, sh in zip(out, shapes)):
-        raise ValueError("out must be five contiguous float32 tensors of the output shapes")
+        if interleaved:
+            kw = key_heads * key_dim
+            qkv = torch.empty((T, channels), dtype=f32, device=dev)
+            out = [qkv[:, :kw].view(shapes[0]), qkv[:, kw:2 * kw].view(shapes[1]),
+                   qkv[:, 2 * kw:].view(shapes[2])]
+            out += [torch.empty(sh, dtype=f32, device=dev) for sh in shapes[3:]]
+        else:
+            out = [torch.empty(sh, dtype=f32, device=dev) for sh in shapes]
+    elif any(o.dtype != f32 or tuple(o.shape) != sh for o, sh in zip(out, shapes)) or \
+            not (out[3].is_contiguous() and out[4].is_contiguous()):
+        raise ValueError("out must be five float32 tensors of the output shapes")
     q, k, v, beta, decay = out
     _device(proj, q, k, v, beta, decay)
+    rows = [_token_rows(t.unsqueeze(0)) for t in (q, k, v)]
+    if None in rows or rows[0] != rows[1]:
+        raise ValueError("q, k and v must be rows of contiguous heads, q and k with one row "
+                         "stride")
     ld = proj.stride(0) if T > 1 else proj.shape[1]
     check(lib().qdc_delta_prologue(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
                                    decay.data_ptr(), proj.data_ptr(), _DTYPES[proj.dtype], ld,
                                    conv.data_ptr(), taps, a_decay.data_ptr(), dt_bias.data_ptr(), T,
-                                   seq_len, key_heads, key_dim, value_heads, value_dim,
-                                   _stream(proj)), "delta_prologue")
+                                   seq_len, key_heads, key_dim, value_heads, value_dim, rows[0],
+                                   rows[2], _stream(proj)), "delta_prologue")
     return q, k, v, beta, decay
 
 

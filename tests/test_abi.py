@@ -39,10 +39,11 @@ def test_exports_match_header():
 def test_version_matches_the_header():
     """qdc_version() is the QDC_HIP_VERSION of the header the library was built
     from (0.2.0: out_dtype added to qdc_gated_rmsnorm and qdc_swiglu; 0.2.1:
-    qdc_row_scale and qdc_row_scale_check added)."""
+    qdc_row_scale and qdc_row_scale_check added; 0.3.0: q/k and v row strides
+    added to qdc_delta_prologue and qdc_delta_scan)."""
     m = re.search(r'#define\s+QDC_HIP_VERSION\s+"([^"]+)"', open(HEADER).read())
     assert m and re.fullmatch(r"qdc_hip \d+\.\d+\.\d+", m.group(1))
-    assert _lib.version() == m.group(1) == "qdc_hip 0.2.1"
+    assert _lib.version() == m.group(1) == "qdc_hip 0.3.0"
 
 
 def test_status_strings():
@@ -256,11 +257,14 @@ def test_delta_scan_validation():
     lib = _lib.lib()
     f = lambda *a: lib.qdc_delta_scan(*a, None)  # noqa: E731
     P = FAKE
-    assert f(P, 7, P, P, P, P, P, 1, 4, 2, 1, 128, 128) == -3
-    assert f(P, F32, P, P, P, P, P, 1, 4, 3, 2, 128, 128) == -2  # heads not a multiple
-    assert f(P, F32, P, P, P, P, P, 1, 4, 2, 1, 320, 128) == -2  # key_dim above 256
-    assert f(P, F32, P, None, P, P, P, 1, 4, 2, 1, 128, 128) == -1
-    assert f(None, F32, None, None, None, None, None, 0, 4, 2, 1, 128, 128) == 0
+    # ..., batch, seq, heads, key_heads, key_dim, value_dim, ld_qk, ld_v
+    assert f(P, 7, P, P, P, P, P, 1, 4, 2, 1, 128, 128, 128, 256) == -3
+    assert f(P, F32, P, P, P, P, P, 1, 4, 3, 2, 128, 128, 256, 384) == -2  # heads not a multiple
+    assert f(P, F32, P, P, P, P, P, 1, 4, 2, 1, 320, 128, 320, 256) == -2  # key_dim above 256
+    assert f(P, F32, P, P, P, P, P, 1, 4, 2, 1, 128, 128, 127, 256) == -2  # q/k rows too short
+    assert f(P, F32, P, P, P, P, P, 1, 4, 2, 1, 128, 128, 128, 255) == -2  # v rows too short
+    assert f(P, F32, P, None, P, P, P, 1, 4, 2, 1, 128, 128, 512, 512) == -1
+    assert f(None, F32, None, None, None, None, None, 0, 4, 2, 1, 128, 128, 128, 256) == 0
 
 
 @pytest.mark.timeout(300)
@@ -313,15 +317,16 @@ int main() {
 def test_delta_prologue_validation():
     lib = _lib.lib()
     # q, k, v, beta, decay, proj, dtype, ld, conv, taps, a_decay, dt_bias, tokens, seq,
-    # kh, kd, vh, vd: kh=1 kd=8 vh=2 vd=8 -> qkv 32 channels, row width 32 + 16 + 4 = 52
+    # kh, kd, vh, vd, ld_qk, ld_v: kh=1 kd=8 vh=2 vd=8 -> qkv 32 channels, row width
+    # 32 + 16 + 4 = 52; separate q, k [16, 8] and v [16, 16] outputs
     pro = lambda *a: lib.qdc_delta_prologue(*a, None)  # noqa: E731
     ok = (FAKE, FAKE + 4096, FAKE + 8192, FAKE + 12288, FAKE + 16384, FAKE + 65536, F32, 52,
-          FAKE + 131072, 4, FAKE, FAKE, 16, 8, 1, 8, 2, 8)
+          FAKE + 131072, 4, FAKE, FAKE, 16, 8, 1, 8, 2, 8, 8, 16)
 
     def call(**kw):
         args = list(ok)
         names = ["q", "k", "v", "beta", "decay", "proj", "dtype", "ld", "conv", "taps",
-                 "a_decay", "dt_bias", "tokens", "seq", "kh", "kd", "vh", "vd"]
+                 "a_decay", "dt_bias", "tokens", "seq", "kh", "kd", "vh", "vd", "ld_qk", "ld_v"]
         for key, val in kw.items():
             args[names.index(key)] = val
         return pro(*args)
@@ -337,6 +342,13 @@ def test_delta_prologue_validation():
     assert call(conv=None) == -1
     assert call(tokens=0, q=None, proj=None) == 0
     assert call(v=FAKE + 65536 + 64) == -5   # output inside the projection
+    assert call(ld_qk=7) == -2               # q/k rows narrower than kh*kd
+    assert call(ld_v=15) == -2               # v rows narrower than vh*vd
+    # one [16, q|k|v] buffer of 32-float rows: q, k, v its column blocks
+    assert call(k=FAKE + 28, v=FAKE + 64, ld_qk=32, ld_v=32) == -5  # k overlaps q's columns
+    assert call(k=FAKE + 32, v=FAKE + 64, ld_qk=32, ld_v=24) == -5  # v rows share q's memory
+    assert call(k=FAKE + 32, v=FAKE + 96, ld_qk=32, ld_v=32) == -5  # v wraps into the next row
+    assert call(k=FAKE, ld_qk=8) == -5       # k is q
 
 
 def test_attention_softmax_validation():

@@ -802,6 +802,17 @@ def test_delta_scan(out_dtype, B, S, KH, H, kd, vd, dscale):
     exp = np.stack([forward.delta_recurrence(q[b], k[b], v[b], beta[b], decay[b])
                     for b in range(B)])
     report(f"delta scan {B}x{S} kh{KH} h{H} kd{kd} vd{vd} decay*{dscale}", got, exp, out_dtype)
+    # the same inputs as the column blocks of one [B, S, q|k|v] buffer, the
+    # prologue's layout in the forward (row strides ld_qk = ld_v = the row
+    # length): bit-identical to the contiguous inputs
+    kw, vw = KH * kd, H * vd
+    qkv = torch.from_numpy(np.concatenate([q.reshape(B, S, kw), k.reshape(B, S, kw),
+                                           v.reshape(B, S, vw)], axis=-1)).to(DEV)
+    strided = back(ops.delta_scan(qkv[..., :kw].view(B, S, KH, kd),
+                                  qkv[..., kw:2 * kw].view(B, S, KH, kd),
+                                  qkv[..., 2 * kw:].view(B, S, H, vd), dev(beta, torch.float32),
+                                  dev(decay, torch.float32), out_dtype=out_dtype))
+    assert np.array_equal(strided, got, equal_nan=True)
 
 
 @pytest.mark.parametrize("B,S,KH,H,kd,vd", [(2, 50, 2, 4, 128, 128), (1, 300, 1, 1, 64, 32)])
@@ -882,6 +893,13 @@ def test_delta_prologue(dtype, case):
         e = np.concatenate(e)
         assert g.shape == e.shape, (name, g.shape, e.shape)
         report(f"prologue {name} {case} {dtype}", g, e, torch.float32)
+    # q, k, v written as the column blocks of one [T, q|k|v] buffer (the
+    # forward's layout): the same values, bit for bit
+    il = ops.delta_prologue(d_proj, dev(conv, torch.float32), dev(a_decay, torch.float32),
+                            dev(dt_bias, torch.float32), S, KH, kd, H, vd, interleaved=True)
+    assert il[0].stride(0) == cq and il[1].data_ptr() == il[0].data_ptr() + 4 * kw
+    for name, g, t in zip(("q", "k", "v", "beta", "decay"), got, il):
+        assert np.array_equal(back(t), g, equal_nan=True), name
 
 
 @pytest.mark.parametrize("KH,kd,H,vd,pad", [(1, 8, 1, 8, 2),    # fast kernel
