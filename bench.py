@@ -30,7 +30,10 @@ of the same total bytes, half read and half written, in the same way and in
 several launch shapes (qdc_copy, qdc_copy_grid): `copy_pct_peak` is what the
 fastest single launch of that size reaches (`copy_shape`), and `pct_of_copy`
 the kernel's bandwidth as a share of it (`pct_of_one_chunk_copy` against the
-one-chunk-per-thread shape alone).
+one-chunk-per-thread shape alone).  The residual norms whose two inputs and two
+outputs have the same sizes are also held against a copy of those two streams
+in one launch (qdc_copy_pair, the same launch shapes): `pair_copy_us`,
+`pct_of_pair_copy`.
 
 Inputs are resident in HBM before timing.  Every kernel cycles through
 several input/output buffer sets totalling more than 512 MB, so the 256 MB
@@ -99,9 +102,12 @@ class Kernel:
     """One fused kernel at its benchmark shape with rotating buffer sets."""
 
     def __init__(self, name, symbol, algo_bytes, make_set, launch, shape, dtype, group="hot",
-                 flops=None, launches=None, ceiling=None, workgroups=None):
+                 flops=None, launches=None, ceiling=None, workgroups=None, pair=None):
         self.name, self.symbol, self.algo_bytes = name, symbol, algo_bytes
         self.shape, self.dtype = shape, dtype
+        # (bytes0, bytes1): a kernel that reads two tensors and writes two of the
+        # same sizes is also held against qdc_copy_pair of those two streams
+        self.pair = pair
         # (make_set, launch) of a plain kernel with this kernel's access pattern
         # and bytes, timed beside it as its ceiling (None: the contiguous copy)
         self.ceiling = ceiling
@@ -213,7 +219,8 @@ def build_kernels(dev):
         lambda i: (randn((Tr, Hr), bf), randn((Tr, Hr), bf),
                    torch.empty((Tr, Hr), dtype=bf, device=dev), torch.empty((Tr, Hr), dtype=bf, device=dev)),
         lambda s: ops.native_residual_rms(s[0], s[1], wr, 1e-6, residual=s[2], out=s[3]),
-        [Tr, Hr], "bfloat16", workgroups=Tr // 8))  # 32 lanes x 4 groups per row
+        [Tr, Hr], "bfloat16", workgroups=Tr // 8,  # 32 lanes x 4 groups per row
+        pair=(Tr * Hr * 2, Tr * Hr * 2)))  # x -> residual, mixed -> normalised
 
     # Attention row work of one full-attention layer (8 sequences of 2048, 8 heads).
     # Softmax: the causally visible scores are read (the rest are -floatmax by
@@ -343,7 +350,7 @@ def build_forward_kernels(dev):
                    torch.empty((T, Hd), dtype=f32, device=dev),
                    torch.empty((T, Hd), dtype=f32, device=dev)),
         lambda s: ops.native_residual_rms(s[0], s[1], wf, 1e-6, residual=s[2], out=s[3]),
-        [T, Hd], "float32", group="forward", launches=1))
+        [T, Hd], "float32", group="forward", launches=1, pair=(T * Hd * 4, T * Hd * 4)))
     hd, nh, kv, rd = cfg.head_dim, cfg.heads, cfg.kv_heads, cfg.rotary_dim
     qn, kn = randn((hd,), bf, 0.02), randn((hd,), bf, 0.02)
     tables = ops.rope_tables(S, rd, cfg.rope_theta, dev)
@@ -502,7 +509,9 @@ def copy_ceilings(dev, kernels, steps, warmup):
     read and half written, graph-replayed over rotating buffers like the
     kernels, in every shape of COPY_SHAPES (sharing one set of buffers): what
     a single launch moving that many bytes reaches on this GPU.  Returns
-    {kernel: (fastest copy, random-row copy or None, {shape: copy})}."""
+    {kernel: (fastest copy, random-row copy or None, {shape: copy}, fastest two-stream
+    copy or None, {shape: two-stream copy})}; the two-stream copies (qdc_copy_pair)
+    only for kernels with a `pair`."""
     import torch
     from qdc_amd import ops
     copies = []
@@ -525,6 +534,22 @@ def copy_ceilings(dev, kernels, steps, warmup):
             make_set, launch = k.ceiling
             copies.append(Kernel(f"rows_{k.name}", "copy_rows", k.algo_bytes, make_set, launch,
                                  k.shape, k.dtype))
+        if k.pair is not None:  # two streams, each read and written, in one launch
+            b0, b1 = k.pair
+            pbufs = {}
+
+            def make_pair(i, b0=b0, b1=b1, pbufs=pbufs):
+                if i not in pbufs:
+                    pbufs[i] = tuple(torch.empty(n, dtype=torch.uint8, device=dev)
+                                     for n in (b0, b0, b1, b1))
+                return pbufs[i]
+
+            for cpt, blk in COPY_SHAPES:
+                copies.append(Kernel(
+                    f"pair{cpt}x{blk}_{k.name}", "copy_pair", 2 * (b0 + b1), make_pair,
+                    lambda st, cpt=cpt, blk=blk: ops.device_copy_pair(st[1], st[0], st[3], st[2],
+                                                                      cpt, blk),
+                    [b0, b1], "u8"))
     for i in range(warmup):
         for c in copies:
             c.run(i)
@@ -537,7 +562,10 @@ def copy_ceilings(dev, kernels, steps, warmup):
     for k in kernels:
         shapes = {f"{cpt}x{blk}": by_name[f"copy{cpt}x{blk}_{k.name}"] for cpt, blk in COPY_SHAPES}
         best = min(shapes.values(), key=lambda c: c.avg_ms)
-        out[k.name] = (best, by_name.get(f"rows_{k.name}"), shapes)
+        pairs = {f"{cpt}x{blk}": by_name[f"pair{cpt}x{blk}_{k.name}"] for cpt, blk in COPY_SHAPES
+                 if f"pair{cpt}x{blk}_{k.name}" in by_name}
+        pair = min(pairs.values(), key=lambda c: c.avg_ms) if pairs else None
+        out[k.name] = (best, by_name.get(f"rows_{k.name}"), shapes, pair, pairs)
     return out
 
 
@@ -546,18 +574,19 @@ PAIR_ROUNDS = 3
 
 def paired_ratios(kernels, ceilings, rounds=PAIR_ROUNDS):
     """Each kernel's graph replayed right before its ceilings' graphs (the
-    same-size copy, and the random-row copy where there is one), in `rounds`
+    same-size copy, the random-row copy and the two-stream copy where there are
+    those), in `rounds`
     rounds over all kernels: the median over rounds of ceiling time / kernel
     time.  Back to back, a kernel and its ceiling run in the same clock and
     memory state, which the separate timing phases above do not ensure."""
     import torch
     stream = torch.cuda.current_stream()
-    ratios = {k.name: ([], []) for k in kernels}
+    ratios = {k.name: ([], [], []) for k in kernels}
     for _ in range(rounds):
         marks = []
         for k in kernels:
-            c, rows = ceilings[k.name][:2]
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            c, rows, _, pair = ceilings[k.name][:4]
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
             ev[0].record(stream)
             k.graph.replay()
             ev[1].record(stream)
@@ -566,15 +595,20 @@ def paired_ratios(kernels, ceilings, rounds=PAIR_ROUNDS):
             if rows is not None:
                 rows.graph.replay()
             ev[3].record(stream)
-            marks.append((k, rows is not None, ev))
+            if pair is not None:
+                pair.graph.replay()
+            ev[4].record(stream)
+            marks.append((k, rows is not None, pair is not None, ev))
         torch.cuda.synchronize()
-        for k, has_rows, ev in marks:
+        for k, has_rows, has_pair, ev in marks:
             t_k = ev[0].elapsed_time(ev[1])
             ratios[k.name][0].append(ev[1].elapsed_time(ev[2]) / t_k)
             if has_rows:
                 ratios[k.name][1].append(ev[2].elapsed_time(ev[3]) / t_k)
+            if has_pair:
+                ratios[k.name][2].append(ev[3].elapsed_time(ev[4]) / t_k)
     med = lambda v: sorted(v)[len(v) // 2] if v else None  # noqa: E731
-    return {name: (med(a), med(b)) for name, (a, b) in ratios.items()}
+    return {name: (med(a), med(b), med(c)) for name, (a, b, c) in ratios.items()}
 
 
 CALIB_BYTES = 512 << 20
@@ -1117,6 +1151,8 @@ def summarize_profiles(out_dir, commit):
         ceil_names += [f"copy{cpt}x{blk}_{k}" for cpt, blk in COPY_SHAPES]
         if "ceiling_us" in entry[k]:
             ceil_names.append("rows_" + k)
+        if "pair_copy_us" in entry[k]:
+            ceil_names += [f"pair{cpt}x{blk}_{k}" for cpt, blk in COPY_SHAPES]
     floor_names = ["empty_" + k for k in groups["hot"] if "empty_us" in entry[k]]
 
     runs = _runs(_dispatches(os.path.join(out_dir, "prof_k", "trace_kernel_trace.csv")), steps)
@@ -1210,6 +1246,7 @@ traced bench run (it includes the graph's gap between nodes).
         # the copy shape that was fastest by HIP events in the same run
         cn = f"copy{e.get('copy_shape', '1x256')}_{k}"
         ku, cu, ru, eu = avg(k), avg(cn), avg("rows_" + k), avg("empty_" + k)
+        pu = avg(f"pair{e['pair_copy_shape']}_{k}") if "pair_copy_shape" in e else None
         wg = timed[k][0][0][1] // timed[k][0][0][2]
         cwg = timed[cn][0][0][1] // timed[cn][0][0][2]
         kb, cb = e["bytes"], (e["bytes"] // 2) // 16 * 16 * 2
@@ -1218,7 +1255,10 @@ traced bench run (it includes the graph's gap between nodes).
                      f"{'' if ru is None else f'{ru:.2f}'} | {'' if eu is None else f'{eu:.2f}'} | "
                      f"{100 * kb / ku / 1e3 / PEAK_GBS:.1f} | {100 * cb / cu / 1e3 / PEAK_GBS:.1f} | "
                      f"{100 * (kb / ku) / (cb / cu):.1f} | "
-                     f"{e.get('pct_of_copy_paired', '')} | {e.get('pct_of_ceiling_paired', '')} |")
+                     f"{e.get('pct_of_copy_paired', '')} | {e.get('pct_of_ceiling_paired', '')} | "
+                     + ("|  |  |" if pu is None else
+                        f"{e['pair_copy_shape']} {pu:.2f} | {100 * pu / ku:.1f} | "
+                        f"{e.get('pct_of_pair_copy_paired', '')} |"))
     with open(os.path.join(ROOT, "profiles", "launch_ceilings.md"), "w") as f:
         f.write(f"""# Single-launch ceilings: each fused kernel beside a copy of its bytes and an empty launch of its grid
 
@@ -1233,14 +1273,18 @@ kernel the same run times, in the same way:
 - for the gathers, `qdc_copy_rows`: the same table, the same number of rows read at uniformly
   random places and written contiguously 1, 2 or 3 times (the gather's access pattern and bytes);
 - for the per-kernel configurations of the RMSNorm family and the q/k kernel, `qdc_empty` over
-  the kernel's own grid (workgroups of 256 threads that do nothing): the fixed cost of the launch.
+  the kernel's own grid (workgroups of 256 threads that do nothing): the fixed cost of the launch;
+- for the residual norms whose two inputs and two outputs have the same sizes (the all-bf16
+  per-kernel configuration and the forward's all-fp32 final norm), `qdc_copy_pair`: their two
+  streams, each read and written, copied in one launch in each of the same launch shapes (the
+  fastest shown; "two-stream copy").
 
-The last two columns are the bench line's paired ratios of the same run: the kernel's graph
+The "paired" columns are the bench line's paired ratios of the same run: the kernel's graph
 replayed right before its ceilings' graphs, median of three rounds (HIP events; ceiling time /
 kernel time).
 
-| kernel | MB | workgroups | kernel us | copy shape | copy us | copy workgroups | random-row copy us | empty us (same grid) | kernel % of 8 TB/s | copy % of 8 TB/s | kernel % of copy | paired % of copy | paired % of random-row copy |
-|---|---|---|---|---|---|---|---|---|---|---|---|---|---|
+| kernel | MB | workgroups | kernel us | copy shape | copy us | copy workgroups | random-row copy us | empty us (same grid) | kernel % of 8 TB/s | copy % of 8 TB/s | kernel % of copy | paired % of copy | paired % of random-row copy | two-stream copy shape, us | kernel % of two-stream copy | paired % of two-stream copy |
+|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|
 """ + "\n".join(lrows) + "\n")
 
     # rocprofv3 --stats of the library's kernels
@@ -1534,7 +1578,7 @@ def main():
         t = load_traffic(k.name)
         if t is not None:  # counted in the profiling run named by traffic_source
             e.update(hbm_bytes_counted=t, traffic_per_algorithmic=round(t / k.algo_bytes, 4))
-        c, rows, shapes = ceilings.get(k.name, (None, None, None))
+        c, rows, shapes, pair, pairs = ceilings.get(k.name, (None,) * 5)
         if c is not None:  # the same bytes as one plain streaming copy launch, fastest shape
             copy_gbs = c.algo_bytes / (c.avg_ms / 1e3) / 1e9
             one = shapes["1x256"]
@@ -1550,11 +1594,20 @@ def main():
                      ceiling_pct_peak=round(100 * rows.algo_bytes / (rows.avg_ms / 1e3) / 1e9
                                             / PEAK_GBS, 1),
                      pct_of_ceiling=round(100 * rows.avg_ms / k.avg_ms, 1))
-        pc, prow = paired.get(k.name, (None, None))
+        if pair is not None:  # its two streams as one two-stream copy launch, fastest shape
+            e.update(pair_copy="qdc_copy_pair of the kernel's two streams, each read and written "
+                               "(bytes " + " + ".join(str(b) for b in k.pair) + ")",
+                     pair_copy_us=round(pair.avg_ms * 1e3, 3),
+                     pair_copy_shape=pair.name.split("_", 1)[0][len("pair"):],
+                     pair_copy_us_by_shape={n: round(x.avg_ms * 1e3, 3) for n, x in pairs.items()},
+                     pct_of_pair_copy=round(100 * pair.avg_ms / k.avg_ms, 1))
+        pc, prow, ppair = paired.get(k.name, (None, None, None))
         if pc is not None:  # the kernel and its ceilings replayed back to back
             e.update(pct_of_copy_paired=round(100 * pc, 1))
         if prow is not None:
             e.update(pct_of_ceiling_paired=round(100 * prow, 1))
+        if ppair is not None:
+            e.update(pct_of_pair_copy_paired=round(100 * ppair, 1))
         f = floors.get(k.name)
         if f is not None:  # an empty launch of the same grid
             e.update(workgroups=k.workgroups, empty_us=round(f.avg_ms * 1e3, 3))

@@ -71,9 +71,9 @@ typedef enum {
  * qdc_swiglu take out_dtype before the stream; 0.3.0: qdc_delta_prologue and
  * qdc_delta_scan take the q/k and v row strides ld_qk, ld_v before the
  * stream), the patch number with added entry points (0.2.1: qdc_row_scale,
- * qdc_row_scale_check).
+ * qdc_row_scale_check; 0.3.1: qdc_copy_pair).
  */
-#define QDC_HIP_VERSION "qdc_hip 0.3.0"
+#define QDC_HIP_VERSION "qdc_hip 0.3.1"
 
 /* Library version string ("qdc_hip <major>.<minor>.<patch>"), QDC_HIP_VERSION. */
 const char *qdc_version(void);
@@ -418,6 +418,19 @@ int32_t qdc_copy_grid(void *dst, const void *src, int64_t bytes, int32_t chunks_
  * many as the gather fused with the first bf16 norm) that the benchmark times
  * beside the gathers.
  */
+/*
+ * Two copies in one launch: src0 -> dst0 (bytes0) and src1 -> dst1 (bytes1),
+ * in the launch shapes of qdc_copy_grid; thread t moves its chunks of both
+ * streams at the same offsets, every load before the first store.  No
+ * destination may overlap a source or the other destination.  No counterpart
+ * in the reference: the ceiling of a row kernel that reads two tensors and
+ * writes two (the residual norm: x and the addend in, the residual stream and
+ * the normalised rows out), which the benchmark times beside it.
+ */
+int32_t qdc_copy_pair(void *dst0, const void *src0, int64_t bytes0, void *dst1,
+                      const void *src1, int64_t bytes1, int32_t chunks_per_thread, int32_t block,
+                      hipStream_t stream);
+
 int32_t qdc_copy_rows(void *dst, const void *src, const int32_t *rows, int64_t n_rows,
                       int64_t n_src, int64_t row_bytes, int32_t repeat, hipStream_t stream);
 

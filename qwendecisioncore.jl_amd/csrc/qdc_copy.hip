@@ -22,17 +22,63 @@ __global__ __launch_bounds__(kBlock) void copy_chunks(u32x4 *__restrict__ dst,
 // the k-th load instruction of every thread the k-th run of BLOCK consecutive
 // chunks, so each wavefront instruction stays one contiguous 1 KB span; all
 // loads are issued before the first store.
+// A workgroup wholly inside the buffer (every one but the last, in general)
+// takes the unguarded form, so no load or store sits in a branch of its own.
 template <int CPT, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void copy_grid(u32x4 *__restrict__ dst,
                                                    const u32x4 *__restrict__ src, uint32_t n) {
-    const uint32_t base = blockIdx.x * (CPT * BLOCK) + threadIdx.x;
+    const uint32_t first = blockIdx.x * (CPT * BLOCK), base = first + threadIdx.x;
     u32x4 v[CPT];
+    if (first + CPT * BLOCK <= n) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) v[k] = __builtin_nontemporal_load(src + base + k * BLOCK);
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) __builtin_nontemporal_store(v[k], dst + base + k * BLOCK);
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
         if (base + k * BLOCK < n) v[k] = __builtin_nontemporal_load(src + base + k * BLOCK);
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
         if (base + k * BLOCK < n) __builtin_nontemporal_store(v[k], dst + base + k * BLOCK);
+}
+
+// Two copies in one launch: thread t copies chunk t (and t + BLOCK, ... for CPT
+// chunks, as copy_grid) of stream 0 and of stream 1 where they exist: all of
+// stream 0's loads, then stream 1's, then the stores in the same order (the
+// faster of the two orders measured; the residual norm loads the same way).
+// The access structure of a row kernel that reads two tensors and writes two.
+template <int CPT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void copy_pair(u32x4 *__restrict__ d0,
+                                                   const u32x4 *__restrict__ s0, uint32_t n0,
+                                                   u32x4 *__restrict__ d1,
+                                                   const u32x4 *__restrict__ s1, uint32_t n1) {
+    const uint32_t first = blockIdx.x * (CPT * BLOCK), base = first + threadIdx.x;
+    u32x4 a[CPT], b[CPT];
+    if (first + CPT * BLOCK <= n0 && first + CPT * BLOCK <= n1) {  // wholly inside both
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) a[k] = __builtin_nontemporal_load(s0 + base + k * BLOCK);
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) b[k] = __builtin_nontemporal_load(s1 + base + k * BLOCK);
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) __builtin_nontemporal_store(a[k], d0 + base + k * BLOCK);
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) __builtin_nontemporal_store(b[k], d1 + base + k * BLOCK);
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+        if (base + k * BLOCK < n0) a[k] = __builtin_nontemporal_load(s0 + base + k * BLOCK);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+        if (base + k * BLOCK < n1) b[k] = __builtin_nontemporal_load(s1 + base + k * BLOCK);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+        if (base + k * BLOCK < n0) __builtin_nontemporal_store(a[k], d0 + base + k * BLOCK);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+        if (base + k * BLOCK < n1) __builtin_nontemporal_store(b[k], d1 + base + k * BLOCK);
 }
 
 // chunks * 16 bytes; the grid (chunks rounded up to whole workgroups) stays
@@ -110,6 +156,49 @@ extern "C" int32_t qdc_copy_grid(void *dst, const void *src, int64_t bytes,
     QDC_COPY_GRID(4, 512)
     QDC_COPY_GRID(8, 512)
 #undef QDC_COPY_GRID
+    return QDC_ERR_SHAPE;
+}
+
+extern "C" int32_t qdc_copy_pair(void *dst0, const void *src0, int64_t bytes0, void *dst1,
+                                 const void *src1, int64_t bytes1, int32_t chunks_per_thread,
+                                 int32_t block, hipStream_t stream) {
+    for (const int64_t b : {bytes0, bytes1})
+        if (b < 0 || b % 16 != 0 || b / 16 > kMaxChunks) return QDC_ERR_SHAPE;
+    if (block != 256 && block != 512) return QDC_ERR_SHAPE;
+    if (chunks_per_thread != 1 && chunks_per_thread != 2 && chunks_per_thread != 4 &&
+        chunks_per_thread != 8)
+        return QDC_ERR_SHAPE;
+    if (bytes0 == 0 && bytes1 == 0) return QDC_OK;
+    if ((bytes0 && (!dst0 || !src0)) || (bytes1 && (!dst1 || !src1))) return QDC_ERR_NULL;
+    if ((bytes0 && (!aligned16(dst0) || !aligned16(src0))) ||
+        (bytes1 && (!aligned16(dst1) || !aligned16(src1))))
+        return QDC_ERR_SHAPE;
+    // each destination overlaps neither source nor the other destination
+    if (overlaps(dst0, bytes0, src0, bytes0) || overlaps(dst0, bytes0, src1, bytes1) ||
+        overlaps(dst1, bytes1, src0, bytes0) || overlaps(dst1, bytes1, src1, bytes1) ||
+        overlaps(dst0, bytes0, dst1, bytes1))
+        return QDC_ERR_ALIAS;
+    const int64_t n0 = bytes0 / 16, n1 = bytes1 / 16;
+    const dim3 grid((uint32_t)ceil_div(std::max(n0, n1), (int64_t)chunks_per_thread * block));
+    auto *d0 = static_cast<u32x4 *>(dst0);
+    auto *d1 = static_cast<u32x4 *>(dst1);
+    auto *s0 = static_cast<const u32x4 *>(src0);
+    auto *s1 = static_cast<const u32x4 *>(src1);
+#define QDC_COPY_PAIR(C, B)                                                                      \
+    if (chunks_per_thread == C && block == B) {                                                  \
+        hipLaunchKernelGGL((copy_pair<C, B>), grid, dim3(B), 0, stream, d0, s0, (uint32_t)n0,    \
+                           d1, s1, (uint32_t)n1);                                                \
+        return launch_status();                                                                  \
+    }
+    QDC_COPY_PAIR(1, 256)
+    QDC_COPY_PAIR(2, 256)
+    QDC_COPY_PAIR(4, 256)
+    QDC_COPY_PAIR(8, 256)
+    QDC_COPY_PAIR(1, 512)
+    QDC_COPY_PAIR(2, 512)
+    QDC_COPY_PAIR(4, 512)
+    QDC_COPY_PAIR(8, 512)
+#undef QDC_COPY_PAIR
     return QDC_ERR_SHAPE;
 }
 

@@ -12,11 +12,12 @@
 // gates src/backbone.jl:293-296; AMDGPU causal_depthwise_kernel! /
 // qk_normalize_kernel! and the beta/decay broadcasts, ext/amdgpu_delta.jl:1-33, 83-113, 154-159.
 //
-// Fast path: a thread owns 4 consecutive channels for a tile of 40 (bf16) or 16
+// Fast path: a thread owns 4 consecutive channels for a tile of 12 (bf16) or 16
 // (fp32) consecutive tokens (4 in short launches), loads the tile's rows and the K-1 halo rows before
-// it in one go, then slides a K-tap window down the tile, so each projection row
-// is read once from HBM (the halo comes from L2) and each output chunk is one
-// whole 16-byte store.  The kd/4 lanes of a key head are an aligned lane group,
+// it in one go (branch-free, so each token waits only for its own rows), then
+// slides a K-tap window down the tile, so each projection row is read once
+// from HBM (the halo comes from L2) and each output chunk is one whole 16-byte
+// store.  The kd/4 lanes of a key head are an aligned lane group,
 // so the L2 norm reduces inside the group.  Outputs are fp32
 // (the recurrence reads fp32).  One extra row of blocks computes the gates.
 #include <cmath>
@@ -57,9 +58,14 @@ __device__ __forceinline__ float softplus_f(float x) {
 // and exactly one 16-byte fp32 output chunk, so every load and store
 // instruction of a wavefront covers whole cache lines.  Tokens per thread: the
 // tile's rows plus the kTaps-1 halo rows are all loaded before the first is used.
-// bf16 tiles of 40 tokens measured ~4% faster than 32 or 64 at the 0.8B shapes
-// (more rows in flight per wavefront against occupancy 3 instead of 4).
-template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 40 : 16; }
+// bf16 tiles of 12 tokens (84 VGPRs, 5 waves per SIMD) measured fastest at the
+// 0.8B shapes once the row loads were branch-free: 108.3 us against 108.4-109.9
+// for 8-14 tokens, 110.6-111.3 for 16-20, 113.7 for 24 and 119.2 for 40 (40 was
+// the best of 8-64 while each row load sat in a branch of its own and the first
+// token waited for the whole tile); fp32 tiles of 8 tokens: 143.4 us against
+// 145.4 for 12 and 149.4 for 16 at 16384 tokens, 22.8 against 23.6 and 23.9 at
+// 2048.  The halo rows (3 per tile) come from L2.
+template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 12 : 8; }
 // Short launches (a single sequence of a few hundred tokens) take tiles of 4
 // tokens: more workgroups on the chip and a 4-step chain per thread instead of
 // 40 (the 3 halo rows per tile come from L2).  Each token's arithmetic is the
@@ -117,21 +123,44 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     // for every token of the tile
     const uint32_t s0 = (uint32_t)t0 - fastdiv((uint32_t)t0, a.seq) * a.seq.d;
     const int64_t seq_start = t0 - s0;
-    Raw rows[kRows];
+    // The conv weights first (the first token needs them), then the rows, every
+    // load unconditional so that none sits in a branch of its own and each
+    // token waits only for its own rows.  Row addresses are clamped into the
+    // launch (rows past the last token feed only tokens that are not stored);
+    // the kTaps-1 halo rows before a sequence start are zeroed; a lane past the
+    // last channel reads channel 0 and stores nothing.
+    float w[4][kTaps];
     {
-        const T *p = reinterpret_cast<const T *>(a.proj) + c0 + (t0 - (kTaps - 1)) * a.ld;
+        const u32x4 *cw = reinterpret_cast<const u32x4 *>(a.conv + (int64_t)c0 * kTaps);
 #pragma unroll
-        for (int r = 0; r < kRows; ++r, p += a.ld) {
-            const int64_t t = t0 - (kTaps - 1) + r;
-            rows[r] = Raw{};
-            if (live && t >= seq_start && t < a.tokens) rows[r] = *reinterpret_cast<const Raw *>(p);
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 q = cw[c];
+#pragma unroll
+            for (int j = 0; j < kTaps; ++j) w[c][j] = __uint_as_float(q[j]);
         }
     }
-    float w[4][kTaps];
+    Raw rows[kRows];
+    {
+        const T *proj = reinterpret_cast<const T *>(a.proj) + c0;
+        const int64_t first = t0 - (kTaps - 1);
+        if (first >= 0 && t0 + kTileT <= a.tokens) {  // tile-uniform: every row exists
+            const T *p = proj + first * a.ld;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+            for (int r = 0; r < kRows; ++r, p += a.ld) rows[r] = *reinterpret_cast<const Raw *>(p);
+        } else {
 #pragma unroll
-        for (int j = 0; j < kTaps; ++j) w[c][j] = live ? a.conv[(c0 + c) * kTaps + j] : 0.0f;
+            for (int r = 0; r < kRows; ++r) {
+                const int64_t t = first + r;
+                const int64_t tc = t < 0 ? 0 : (t >= a.tokens ? a.tokens - 1 : t);
+                rows[r] = *reinterpret_cast<const Raw *>(proj + tc * a.ld);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kTaps - 1; ++r) {  // halo rows before the sequence start
+            const uint32_t keep = first + r >= seq_start ? 0xffffffffu : 0u;
+            rows[r] = rows[r] & keep;
+        }
+    }
 
     const int64_t kw = (int64_t)a.kh * a.kd;
     // this thread's output chunk of token t0 and the stride between tokens
@@ -277,12 +306,11 @@ int32_t launch_fast(Prologue q, int lph, hipStream_t stream) {
 }
 
 // Below this many workgroups with the large tiles (well under one per CU of the
-// 256) the launch takes 4-token tiles.  Measured crossover on MI355X, graph-
-// replayed: at the 0.8B DeltaNet dims (bf16, 7 workgroups per tile) 4-token
-// tiles are faster up to 512 tokens (11.0 against 14.6 us; 4.5 against 14.4 at
-// 64) and slower from 1024 (91 and 182 large-tile workgroups); at the 4-layer
-// synthetic dims (fp32, 2 per tile) faster up to 1024 tokens, slower from 2048
-// (128 and 256).
+// 256) the launch takes 4-token tiles.  Measured on MI355X, graph-replayed: at
+// the 0.8B DeltaNet dims (bf16, 7 workgroups per tile) 4-token tiles run 3.9
+// and 4.9 us at 64 and 256 tokens against 6.1 and 6.2 with 12-token tiles (42
+// and 154 large-tile workgroups); at the 4-layer synthetic dims (fp32, 2 per
+// tile) 3.7-4.5 us at 64-512 tokens against 6.1-6.5 with 16-token tiles.
 constexpr int64_t kSmallTileBelow = 160;
 
 template <typename T>
@@ -369,7 +397,7 @@ extern "C" int32_t qdc_delta_prologue(float *q, float *k, float *v, float *beta,
     p.inv_sqrt_kd = 1.0f / p.sqrt_kd;
     // 4-channel pieces: 8-byte (bf16) or 16-byte (fp32) aligned projection rows
     const bool fast = ((uintptr_t)proj % (4 * es)) == 0 && (ld * es) % (4 * es) == 0 &&
-                      aligned16(q) && aligned16(k) && aligned16(v) && cq % 4 == 0 &&
+                      aligned16(q) && aligned16(k) && aligned16(v) && aligned16(conv) && cq % 4 == 0 &&
                       ld_qk % 4 == 0 && ld_v % 4 == 0;
     if (proj_dtype == QDC_BF16) return launch<bf16_t>(p, fast, stream);
     return launch<float>(p, fast, stream);

@@ -48,7 +48,7 @@ qdc_library_path() = get(ENV, "QDC_HIP_LIBRARY", "libqdc_hip.so")
 # QDC_HIP_VERSION of the header these bindings follow; a library built from
 # another header is refused at load, since a changed signature would pass its
 # arguments in the wrong slots without any error.
-const QDC_HIP_VERSION = "qdc_hip 0.3.0"
+const QDC_HIP_VERSION = "qdc_hip 0.3.1"
 
 function qdc_open()
     handle = Libdl.dlopen(qdc_library_path())

@@ -58,6 +58,7 @@ SIGNATURES = {
                                   _i64, _vp]),
     "qdc_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "qdc_copy_grid": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp]),
+    "qdc_copy_pair": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _vp]),
     "qdc_copy_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "qdc_empty": (_i32, [_i64, _vp]),
     "qdc_row_scale": (_i32, [_vp, _vp, _i64, _f32, _f32, _vp]),

@@ -755,6 +755,27 @@ def device_copy(dst: torch.Tensor, src: torch.Tensor, chunks_per_thread: int = 1
     return dst
 
 
+def device_copy_pair(dst0: torch.Tensor, src0: torch.Tensor, dst1: torch.Tensor,
+                     src1: torch.Tensor, chunks_per_thread: int = 1, block: int = 256):
+    """Two plain copies in one launch (``qdc_copy_pair``): ``src0``'s bytes into
+    ``dst0`` and ``src1``'s into ``dst1`` (each pair contiguous, same byte count,
+    a multiple of 16), each thread moving its chunks of both: the ceiling the
+    benchmark sets beside the row kernels that read two tensors and write two."""
+    _device(dst0, src0, dst1, src1)
+    counts = []
+    for d, s in ((dst0, src0), (dst1, src1)):
+        if not d.is_contiguous() or not s.is_contiguous():
+            raise ValueError("copy_pair buffers must be contiguous")
+        n = s.numel() * s.element_size()
+        if d.numel() * d.element_size() != n:
+            raise ValueError("each destination must hold its source's byte count")
+        counts.append(n)
+    check(lib().qdc_copy_pair(dst0.data_ptr(), src0.data_ptr(), counts[0], dst1.data_ptr(),
+                              src1.data_ptr(), counts[1], chunks_per_thread, block,
+                              _stream(src0)), "device_copy_pair")
+    return dst0, dst1
+
+
 def device_copy_rows(dst: torch.Tensor, table: torch.Tensor, rows: torch.Tensor,
                      repeat: int = 1) -> torch.Tensor:
     """``dst[i]`` = ``repeat`` copies of the bytes of ``table[rows[i]]`` (``table``

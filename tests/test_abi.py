@@ -28,7 +28,7 @@ def declared():
 def test_exports_match_header():
     lib = _lib.lib()
     names = declared()
-    assert len(names) == 25, names
+    assert len(names) == 26, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
@@ -40,10 +40,10 @@ def test_version_matches_the_header():
     """qdc_version() is the QDC_HIP_VERSION of the header the library was built
     from (0.2.0: out_dtype added to qdc_gated_rmsnorm and qdc_swiglu; 0.2.1:
     qdc_row_scale and qdc_row_scale_check added; 0.3.0: q/k and v row strides
-    added to qdc_delta_prologue and qdc_delta_scan)."""
+    added to qdc_delta_prologue and qdc_delta_scan; 0.3.1: qdc_copy_pair added)."""
     m = re.search(r'#define\s+QDC_HIP_VERSION\s+"([^"]+)"', open(HEADER).read())
     assert m and re.fullmatch(r"qdc_hip \d+\.\d+\.\d+", m.group(1))
-    assert _lib.version() == m.group(1) == "qdc_hip 0.3.0"
+    assert _lib.version() == m.group(1) == "qdc_hip 0.3.1"
 
 
 def test_status_strings():
@@ -468,6 +468,23 @@ def test_copy_rows_validation():
     assert cr(FAKE + 8, FAKE, FAKE, 4, 10, 32, 1) == -2    # misaligned
     assert cr(FAKE, FAKE + 64, 0x900000, 4, 10, 32, 2) == -5   # dst overlaps the table
     assert cr(None, None, None, 0, 10, 32, 1) == 0
+
+
+def test_copy_pair_validation():
+    lib = _lib.lib()
+    cp = lambda *a: lib.qdc_copy_pair(*a, None)  # noqa: E731
+    A, B, C, D = FAKE, FAKE + (1 << 20), FAKE + (2 << 20), FAKE + (3 << 20)
+    assert cp(A, B, 32, C, D, 16, 3, 256) == -2          # not a launch shape
+    assert cp(A, B, 32, C, D, 16, 1, 128) == -2
+    assert cp(A, B, 24, C, D, 16, 1, 256) == -2          # not a multiple of 16
+    assert cp(A, B, 32, C, D, -16, 1, 256) == -2
+    assert cp(None, B, 32, C, D, 16, 1, 256) == -1
+    assert cp(A, B, 32, C, None, 16, 1, 256) == -1
+    assert cp(None, None, 0, C, D, 0, 1, 256) == 0       # nothing to copy
+    assert cp(A + 8, B, 32, C, D, 16, 1, 256) == -2      # misaligned
+    assert cp(A, A + 16, 32, C, D, 16, 1, 256) == -5     # dst0 overlaps src0
+    assert cp(A, B, 32, C, A + 16, 16, 1, 256) == -5     # src1 inside dst0
+    assert cp(A, B, 32, A + 16, D, 16, 1, 256) == -5     # the destinations overlap
 
 
 def test_empty_validation():

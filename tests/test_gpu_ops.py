@@ -1112,6 +1112,26 @@ def test_device_copy_shapes(cpt, block):
                         torch.empty(32, dtype=torch.uint8, device=DEV), 3, 256)
 
 
+@pytest.mark.parametrize("cpt,block", [(1, 256), (2, 256), (4, 256), (8, 256), (1, 512),
+                                       (4, 512)])
+def test_device_copy_pair(cpt, block):
+    """Both streams of the two-copy ceiling (qdc_copy_pair) arrive byte for byte,
+    with equal and unequal sizes (the shorter stream ending inside a workgroup,
+    or empty) and nothing written past either destination."""
+    from qdc_amd import ops
+    span = cpt * block * 16
+    for n0, n1 in ((span * 3, span * 3), (span * 3 + 4096 + 48, span + 32), (16, span * 2 + 16),
+                   (33_554_432, 33_554_432), (span, 0)):
+        s0 = torch.randint(0, 256, (n0,), dtype=torch.uint8, device=DEV)
+        s1 = torch.randint(0, 256, (n1,), dtype=torch.uint8, device=DEV)
+        d0 = torch.zeros(n0 + 4096, dtype=torch.uint8, device=DEV)
+        d1 = torch.zeros(n1 + 4096, dtype=torch.uint8, device=DEV)
+        ops.device_copy_pair(d0[:n0], s0, d1[:n1], s1, cpt, block)
+        torch.cuda.synchronize()
+        assert torch.equal(d0[:n0], s0) and torch.equal(d1[:n1], s1), (cpt, block, n0, n1)
+        assert not d0[n0:].any() and not d1[n1:].any(), (cpt, block, n0, n1)
+
+
 # ---------------------------------------------------------------- row scale --
 def test_row_scale_check_every_pattern():
     """The row kernels take 1/sqrt(x) from the hardware square root and

@@ -18,8 +18,8 @@ from conftest import ROOT
 HEADER = os.path.join(ROOT, "include", "qdc_hip.h")
 SHIM = os.path.join(ROOT, "qwendecisioncore.jl_amd", "julia", "amdgpu_hip.jl")
 # the benchmark's ceilings and the row-scale self-checks: no reference counterpart
-UNBOUND = {"qdc_copy", "qdc_copy_grid", "qdc_copy_rows", "qdc_empty", "qdc_row_scale",
-           "qdc_row_scale_check"}
+UNBOUND = {"qdc_copy", "qdc_copy_grid", "qdc_copy_pair", "qdc_copy_rows", "qdc_empty",
+           "qdc_row_scale", "qdc_row_scale_check"}
 
 _SCALARS = {"int32_t": "Int32", "int64_t": "Int64", "uint32_t": "UInt32", "float": "Float32",
             "hipStream_t": "Ptr{Cvoid}"}
@@ -108,7 +108,7 @@ def shim_ccalls() -> list:
 
 def test_header_parses():
     protos = header_prototypes()
-    assert len(protos) == 25, sorted(protos)
+    assert len(protos) == 26, sorted(protos)
     assert protos["qdc_version"] == ("Cstring", [])
     assert protos["qdc_check_ids"] == ("Int32", ["Ptr{Int64}", "Int64", "Int64"])
 
