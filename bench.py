@@ -186,8 +186,8 @@ def build_kernels(dev):
         lambda s: ops.prepare_heads(s[0], s[1], qn, kn, tables, rd, 1e-6, seq_len=seq,
                                     q_out=s[2], k_out=s[3]),
         [T, H, KV, hd, rd, seq], "bfloat16",
-        # 16-lane groups of 4 Q heads / 2 K heads, 16 groups per workgroup
-        workgroups=T * H // 4 // 16 + T * KV // 2 // 16))
+        # 16-lane groups of 4 Q heads / 1 K head, 16 groups per workgroup
+        workgroups=T * H // 4 // 16 + T * KV // 16))
 
     vocab, hidden, n = 248320, 1024, 16384
     table = randn((vocab, hidden), bf, 0.02)

@@ -18,21 +18,22 @@
 namespace qdc {
 namespace {
 
-// Q rows take workgroups [0, q_blocks), K rows the rest (block-uniform branch).
-template <typename T, int LPR, int RPGQ, int RPGK>
+// Q rows take workgroups [0, q_blocks), K rows the rest (block-uniform branch);
+// a lane group holds RPGQ heads of a Q token or one K head.
+template <typename T, int LPR, int RPGQ>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_fast(QKArgs<T> a) {
     const int hc = a.half / Elem<T>::kVec;
     if (2 * hc <= LPR && (hc & (hc - 1)) == 0) {
         if ((int64_t)blockIdx.x < a.q_blocks)
             qk_side_contig<T, LPR, RPGQ>(a, a.q, (int64_t)blockIdx.x);
         else
-            qk_side_contig<T, LPR, RPGK>(a, a.k, (int64_t)blockIdx.x - a.q_blocks);
+            qk_side_contig<T, LPR, 1>(a, a.k, (int64_t)blockIdx.x - a.q_blocks);
         return;
     }
     if ((int64_t)blockIdx.x < a.q_blocks)
         qk_side_paired<T, LPR, RPGQ>(a, a.q, (int64_t)blockIdx.x);
     else
-        qk_side_paired<T, LPR, RPGK>(a, a.k, (int64_t)blockIdx.x - a.q_blocks);
+        qk_side_paired<T, LPR, 1>(a, a.k, (int64_t)blockIdx.x - a.q_blocks);
 }
 
 constexpr int kMaxGeneralRotary = 1024;
@@ -89,9 +90,11 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_general(QKArgs<T> a) {
     }
 }
 
-// Heads of one token per lane group: the largest of 4, 2, 1 that divides the
-// side's head count (4 measured ~5% faster than 1 on the 8 + 2 heads of 256
-// in bf16; 8 was slower).
+// Q heads of one token per lane group: the largest of 4, 2, 1 that divides the
+// head count (4 measured ~5% faster than 1 on the 8 + 2 heads of 256 in bf16;
+// 8 was slower).  K rows take one head per lane group: on those shapes 2.5%
+// faster over the launch than both KV heads of a token in one group, since the
+// K workgroups, last in the grid, then hold half the bytes each.
 constexpr int kMaxRowsPerGroup = 4;
 int rows_per_group(int64_t heads) {
     int r = 1;
@@ -99,36 +102,27 @@ int rows_per_group(int64_t heads) {
     return r;
 }
 
-template <typename T, int LPR, int RPGQ, int RPGK>
+template <typename T, int LPR, int RPGQ>
 int32_t launch_fast(QKArgs<T> a, hipStream_t stream) {
     constexpr int64_t gpb = kBlock / LPR;
     a.q_blocks = ceil_div(a.q.rows / RPGQ, gpb);
-    const int64_t blocks = a.q_blocks + ceil_div(a.k.rows / RPGK, gpb);
-    hipLaunchKernelGGL((qk_norm_rope_fast<T, LPR, RPGQ, RPGK>), dim3((uint32_t)blocks),
+    const int64_t blocks = a.q_blocks + ceil_div(a.k.rows, gpb);
+    hipLaunchKernelGGL((qk_norm_rope_fast<T, LPR, RPGQ>), dim3((uint32_t)blocks),
                        dim3(kBlock), 0, stream, a);
     return launch_status();
 }
 
 template <typename T, int LPR>
-int32_t launch_lpr(QKArgs<T> a, int64_t heads, int64_t kv_heads, hipStream_t stream) {
-    const int rq = rows_per_group(heads), rk = rows_per_group(kv_heads);
-#define QDC_QK_R(RQ, RK) \
-    if (rq == RQ && rk == RK) return launch_fast<T, LPR, RQ, RK>(a, stream);
-    QDC_QK_R(1, 1)
-    QDC_QK_R(2, 1)
-    QDC_QK_R(1, 2)
-    QDC_QK_R(2, 2)
-    QDC_QK_R(4, 1)
-    QDC_QK_R(4, 2)
-    QDC_QK_R(1, 4)
-    QDC_QK_R(2, 4)
-    QDC_QK_R(4, 4)
-#undef QDC_QK_R
-    return QDC_ERR_SHAPE;  // unreachable: rows_per_group stays within the instantiated set
+int32_t launch_lpr(QKArgs<T> a, int64_t heads, hipStream_t stream) {
+    switch (rows_per_group(heads)) {
+        case 4: return launch_fast<T, LPR, 4>(a, stream);
+        case 2: return launch_fast<T, LPR, 2>(a, stream);
+        default: return launch_fast<T, LPR, 1>(a, stream);
+    }
 }
 
 template <typename T>
-int32_t launch(QKArgs<T> a, int64_t heads, int64_t kv_heads, bool fast, hipStream_t stream) {
+int32_t launch(QKArgs<T> a, int64_t heads, bool fast, hipStream_t stream) {
     constexpr int V = Elem<T>::kVec;
     const int64_t chunks = a.dim / V;
     // two chunks per lane: LPR = chunks / 2 lanes per row, a power of two <= 64
@@ -136,13 +130,13 @@ int32_t launch(QKArgs<T> a, int64_t heads, int64_t kv_heads, bool fast, hipStrea
     if (fast && a.dim % V == 0 && a.half % V == 0 && chunks >= 2 && chunks % 2 == 0 && lpr <= kWave &&
         (lpr & (lpr - 1)) == 0) {
         switch (lpr) {
-            case 1: return launch_lpr<T, 1>(a, heads, kv_heads, stream);
-            case 2: return launch_lpr<T, 2>(a, heads, kv_heads, stream);
-            case 4: return launch_lpr<T, 4>(a, heads, kv_heads, stream);
-            case 8: return launch_lpr<T, 8>(a, heads, kv_heads, stream);
-            case 16: return launch_lpr<T, 16>(a, heads, kv_heads, stream);
-            case 32: return launch_lpr<T, 32>(a, heads, kv_heads, stream);
-            case 64: return launch_lpr<T, 64>(a, heads, kv_heads, stream);
+            case 1: return launch_lpr<T, 1>(a, heads, stream);
+            case 2: return launch_lpr<T, 2>(a, heads, stream);
+            case 4: return launch_lpr<T, 4>(a, heads, stream);
+            case 8: return launch_lpr<T, 8>(a, heads, stream);
+            case 16: return launch_lpr<T, 16>(a, heads, stream);
+            case 32: return launch_lpr<T, 32>(a, heads, stream);
+            case 64: return launch_lpr<T, 64>(a, heads, stream);
             default:
                 break;
         }
@@ -287,7 +281,7 @@ int32_t qk_norm_rope(void *q_out, void *k_out, const void *q_in, const void *k_i
         a.half = (int32_t)(rotary_dim / 2);
         a.dim = (int32_t)head_dim;
         a.eps = eps;
-        return launch<T>(a, heads, kv_heads, fast, stream);
+        return launch<T>(a, heads, fast, stream);
     };
     if (dtype == QDC_BF16) return fill((bf16_t *)nullptr);
     return fill((float *)nullptr);
