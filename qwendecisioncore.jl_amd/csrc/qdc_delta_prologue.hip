@@ -19,7 +19,8 @@
 // from HBM (the halo comes from L2) and each output chunk is one whole 16-byte
 // store.  The kd/4 lanes of a key head are an aligned lane group,
 // so the L2 norm reduces inside the group.  Outputs are fp32
-// (the recurrence reads fp32).  One extra row of blocks computes the gates.
+// (the recurrence reads fp32).  Blocks of 32 tokens after the channel blocks
+// compute the gates.
 #include <cmath>
 #include <type_traits>
 
@@ -43,7 +44,8 @@ struct Prologue {
     int kh, kd, vh, vd, taps;
     int chunks;             // qkv channels / 4
     int qk_chunks;          // 2*kh*kd / 4
-    uint32_t blocks_per_tile;  // fast path: channel blocks + 1 gates block
+    uint32_t blocks_per_tile;  // fast path: channel blocks per tile
+    uint32_t chan_blocks;      // fast path: tiles x blocks_per_tile; the gates blocks follow
     float sqrt_kd, inv_sqrt_kd;
 };
 
@@ -71,6 +73,13 @@ template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 12 : 8;
 // 40 (the 3 halo rows per tile come from L2).  Each token's arithmetic is the
 // same in either tile, so the outputs are bit-identical.
 constexpr int kSmallTile = 4;
+// Tokens per gates block.  The gates (beta, decay: 2 heads-wide columns in,
+// 2 out per token) take their own blocks at the end of the grid instead of one
+// block beside each tile's channel blocks: 3-4% faster at 2048 tokens and
+// 0.5-1% at 16384 (0.8B dims), 20% at 2048 tokens of the 2-key-head synthetic
+// dims, where the per-tile gates block was every other workgroup; 16-64 tokens
+// measured alike, 128 slower (longer tail).
+constexpr int kGateTokens = 32;
 
 template <typename T> struct Raw4;  // 4 channels of one projection row
 template <> struct Raw4<bf16_t> {
@@ -92,15 +101,13 @@ template <typename T, int LPH, int kTileT>
 __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     using Raw = typename Raw4<T>::type;
     constexpr int kRows = kTileT + kTaps - 1;  // rows t0-3 .. t0+tile-1
-    // One-dimensional grid of tiles x channel blocks in plain order (the last
-    // block of a tile computes the gates).  Dealing each XCD a contiguous run of
-    // tiles, so halo rows hit the same L2, measured 0-2% slower on MI355X.
-    const uint32_t nblk = a.blocks_per_tile;
-    const uint32_t tile = blockIdx.x / nblk, cblk = blockIdx.x % nblk;
-    const int64_t t0 = (int64_t)tile * kTileT;
-    if (cblk == nblk - 1) {  // the gates block of this tile
-        for (int i = threadIdx.x; i < kTileT * a.vh; i += kBlock) {
-            const int64_t t = t0 + i / a.vh;
+    // One-dimensional grid: tiles x channel blocks in plain order, then the
+    // gates blocks, kGateTokens tokens each.  Dealing each XCD a contiguous run
+    // of tiles, so halo rows hit the same L2, measured 0-2% slower on MI355X.
+    if (blockIdx.x >= a.chan_blocks) {
+        const int64_t g0 = (int64_t)(blockIdx.x - a.chan_blocks) * kGateTokens;
+        for (int i = threadIdx.x; i < kGateTokens * a.vh; i += kBlock) {
+            const int64_t t = g0 + i / a.vh;
             const int h = i % a.vh;
             if (t >= a.tokens) continue;
             const T *row = reinterpret_cast<const T *>(a.proj) + t * a.ld;
@@ -111,6 +118,9 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
         }
         return;
     }
+    const uint32_t nblk = a.blocks_per_tile;
+    const uint32_t tile = blockIdx.x / nblk, cblk = blockIdx.x % nblk;
+    const int64_t t0 = (int64_t)tile * kTileT;
     const int ci = cblk * kBlock + threadIdx.x;  // quad of 4 channels
     const bool live = ci < a.chunks;
     const int c0 = (live ? ci : 0) * 4;
@@ -284,7 +294,8 @@ bool disjoint_rows(const OutRows &a, const OutRows &b, int64_t tokens) {
 
 template <typename T, int TILE>
 int32_t launch_fast(Prologue q, int lph, hipStream_t stream) {
-    const int64_t blocks = ceil_div(q.tokens, TILE) * q.blocks_per_tile;
+    q.chan_blocks = (uint32_t)(ceil_div(q.tokens, TILE) * q.blocks_per_tile);
+    const int64_t blocks = (int64_t)q.chan_blocks + ceil_div(q.tokens, (int64_t)kGateTokens);
     const dim3 grid((uint32_t)blocks);
 #define QDC_PRO(L)                                                                               \
     case L:                                                                                      \
@@ -306,8 +317,9 @@ int32_t launch_fast(Prologue q, int lph, hipStream_t stream) {
 }
 
 // Below this many workgroups with the large tiles (well under one per CU of the
-// 256) the launch takes 4-token tiles.  Measured on MI355X, graph-replayed: at
-// the 0.8B DeltaNet dims (bf16, 7 workgroups per tile) 4-token tiles run 3.9
+// 256; counted as channel blocks plus one gates block per tile, the grid these
+// measurements had) the launch takes 4-token tiles.  Measured on MI355X,
+// graph-replayed: at the 0.8B DeltaNet dims (bf16, 7 workgroups per tile) 4-token tiles run 3.9
 // and 4.9 us at 64 and 256 tokens against 6.1 and 6.2 with 12-token tiles (42
 // and 154 large-tile workgroups); at the 4-layer synthetic dims (fp32, 2 per
 // tile) 3.7-4.5 us at 64-512 tokens against 6.1-6.5 with 16-token tiles.
@@ -316,10 +328,11 @@ constexpr int64_t kSmallTileBelow = 160;
 template <typename T>
 int32_t launch(const Prologue &p, bool fast, hipStream_t stream) {
     const int lph = p.kd / 4;
-    const int64_t bpt = ceil_div(p.chunks, kBlock) + 1;
-    const int64_t big_blocks = ceil_div(p.tokens, tile_for<T>()) * bpt;
-    const bool small = big_blocks < kSmallTileBelow;
-    const int64_t fast_blocks = small ? ceil_div(p.tokens, kSmallTile) * bpt : big_blocks;
+    const int64_t bpt = ceil_div(p.chunks, kBlock);
+    const int64_t big_tiles = ceil_div(p.tokens, tile_for<T>());
+    const bool small = big_tiles * (bpt + 1) < kSmallTileBelow;
+    const int64_t fast_blocks = (small ? ceil_div(p.tokens, kSmallTile) : big_tiles) * bpt +
+                                ceil_div(p.tokens, (int64_t)kGateTokens);
     // the fast grid is one-dimensional: fewer than 2^32 work-items
     if (fast && p.kd % 4 == 0 && p.vd % 4 == 0 && p.taps == kTaps && lph <= kWave &&
         (lph & (lph - 1)) == 0 && fast_blocks * kBlock < ((int64_t)1 << 32)) {
