@@ -12,12 +12,12 @@
 // gates src/backbone.jl:293-296; AMDGPU causal_depthwise_kernel! /
 // qk_normalize_kernel! and the beta/decay broadcasts, ext/amdgpu_delta.jl:1-33, 83-113, 154-159.
 //
-// Fast path: a thread owns 4 consecutive channels for a tile of 12 (bf16) or 16
+// Fast path: a thread owns 4 consecutive channels for a tile of 12 (bf16) or 8
 // (fp32) consecutive tokens (4 in short launches), loads the tile's rows and the K-1 halo rows before
 // it in one go (branch-free, so each token waits only for its own rows), then
 // slides a K-tap window down the tile, so each projection row is read once
-// from HBM (the halo comes from L2) and each output chunk is one whole 16-byte
-// store.  The kd/4 lanes of a key head are an aligned lane group,
+// from HBM (the halo rows again from a cache: tiles are dealt to the XCDs in
+// runs of two) and each output chunk is one whole 16-byte store.  The kd/4 lanes of a key head are an aligned lane group,
 // so the L2 norm reduces inside the group.  Outputs are fp32
 // (the recurrence reads fp32).  Blocks of 32 tokens after the channel blocks
 // compute the gates.
@@ -45,7 +45,9 @@ struct Prologue {
     int chunks;             // qkv channels / 4
     int qk_chunks;          // 2*kh*kd / 4
     uint32_t blocks_per_tile;  // fast path: channel blocks per tile
-    uint32_t chan_blocks;      // fast path: tiles x blocks_per_tile; the gates blocks follow
+    uint32_t chan_blocks;      // fast path: channel workgroups (tiles padded to whole XCD runs)
+                               // x blocks_per_tile; the gates blocks follow
+    uint32_t tiles;            // fast path: tiles of the launch
     float sqrt_kd, inv_sqrt_kd;
 };
 
@@ -80,6 +82,14 @@ constexpr int kSmallTile = 4;
 // dims, where the per-tile gates block was every other workgroup; 16-64 tokens
 // measured alike, 128 slower (longer tail).
 constexpr int kGateTokens = 32;
+// Consecutive tiles per XCD run.  Runs of 2 halve the halo rows fetched into
+// L2 from outside (read traffic 1.13x instead of 1.26x the algorithmic reads
+// at 16384 tokens, 0.8B dims) at the same time in bf16 (2% faster in fp32);
+// runs of 4 and 8 measured 1.5% and 3.5% slower in bf16.  Leaving the halo rows
+// out altogether (a probe: zeros instead of loads) changed the time by under
+// 0.3%: those L2 fills hit the last-level cache, they cost counted traffic,
+// not time.
+constexpr uint32_t kXcdRun = 2;
 
 template <typename T> struct Raw4;  // 4 channels of one projection row
 template <> struct Raw4<bf16_t> {
@@ -101,9 +111,8 @@ template <typename T, int LPH, int kTileT>
 __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
     using Raw = typename Raw4<T>::type;
     constexpr int kRows = kTileT + kTaps - 1;  // rows t0-3 .. t0+tile-1
-    // One-dimensional grid: tiles x channel blocks in plain order, then the
-    // gates blocks, kGateTokens tokens each.  Dealing each XCD a contiguous run
-    // of tiles, so halo rows hit the same L2, measured 0-2% slower on MI355X.
+    // One-dimensional grid: the channel workgroups, then the gates blocks,
+    // kGateTokens tokens each.
     if (blockIdx.x >= a.chan_blocks) {
         const int64_t g0 = (int64_t)(blockIdx.x - a.chan_blocks) * kGateTokens;
         for (int i = threadIdx.x; i < kGateTokens * a.vh; i += kBlock) {
@@ -118,8 +127,16 @@ __global__ __launch_bounds__(kBlock) void delta_prologue_fast(Prologue a) {
         }
         return;
     }
+    // Workgroup i runs on XCD i % 8 (the hardware deals workgroups round-robin
+    // over the 8 XCDs).  XCD x takes runs of kXcdRun consecutive tiles, each
+    // tile's channel blocks in a row, so the later tiles of a run find their
+    // halo rows in this XCD's L2, loaded there by the tile before.
     const uint32_t nblk = a.blocks_per_tile;
-    const uint32_t tile = blockIdx.x / nblk, cblk = blockIdx.x % nblk;
+    const uint32_t x = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    const uint32_t per_run = kXcdRun * nblk;
+    const uint32_t run = slot / per_run, r = slot - run * per_run;
+    const uint32_t tile = (run * 8u + x) * kXcdRun + r / nblk, cblk = r % nblk;
+    if (tile >= a.tiles) return;  // padding of the last runs
     const int64_t t0 = (int64_t)tile * kTileT;
     const int ci = cblk * kBlock + threadIdx.x;  // quad of 4 channels
     const bool live = ci < a.chunks;
@@ -294,7 +311,8 @@ bool disjoint_rows(const OutRows &a, const OutRows &b, int64_t tokens) {
 
 template <typename T, int TILE>
 int32_t launch_fast(Prologue q, int lph, hipStream_t stream) {
-    q.chan_blocks = (uint32_t)(ceil_div(q.tokens, TILE) * q.blocks_per_tile);
+    q.tiles = (uint32_t)ceil_div(q.tokens, TILE);
+    q.chan_blocks = (uint32_t)(ceil_div(q.tiles, 8 * kXcdRun) * 8 * kXcdRun * q.blocks_per_tile);
     const int64_t blocks = (int64_t)q.chan_blocks + ceil_div(q.tokens, (int64_t)kGateTokens);
     const dim3 grid((uint32_t)blocks);
 #define QDC_PRO(L)                                                                               \
@@ -331,8 +349,8 @@ int32_t launch(const Prologue &p, bool fast, hipStream_t stream) {
     const int64_t bpt = ceil_div(p.chunks, kBlock);
     const int64_t big_tiles = ceil_div(p.tokens, tile_for<T>());
     const bool small = big_tiles * (bpt + 1) < kSmallTileBelow;
-    const int64_t fast_blocks = (small ? ceil_div(p.tokens, kSmallTile) : big_tiles) * bpt +
-                                ceil_div(p.tokens, (int64_t)kGateTokens);
+    const int64_t runs = ceil_div(small ? ceil_div(p.tokens, kSmallTile) : big_tiles, 8 * kXcdRun);
+    const int64_t fast_blocks = runs * 8 * kXcdRun * bpt + ceil_div(p.tokens, (int64_t)kGateTokens);
     // the fast grid is one-dimensional: fewer than 2^32 work-items
     if (fast && p.kd % 4 == 0 && p.vd % 4 == 0 && p.taps == kTaps && lph <= kWave &&
         (lph & (lph - 1)) == 0 && fast_blocks * kBlock < ((int64_t)1 << 32)) {
