@@ -848,7 +848,7 @@ def test_delta_scan_chunked_matches_recurrent(B, S, KH, H, kd, vd):
 # ------------------------------------------------ DeltaNet prologue ----------
 # (B, S, KH, kd, H, vd, taps, pad): pad > 0 widens the row stride by pad elements
 PROLOGUE_CASES = [
-    (2, 1024, 16, 128, 16, 128, 4, 0),   # Qwen3.5-0.8B DeltaNet dims: 40/16-token tiles
+    (2, 1024, 16, 128, 16, 128, 4, 0),   # Qwen3.5-0.8B DeltaNet dims: 12/8-token tiles
     (1, 200, 16, 128, 16, 128, 4, 0),    # the same dims, one short sequence: 4-token tiles
     (2, 37, 2, 128, 4, 128, 4, 0),       # sequences break inside a (4-token) tile
     (3, 5, 1, 64, 2, 32, 4, 8),          # strided rows
