@@ -64,7 +64,8 @@ __device__ __forceinline__ float softplus_f(float x) {
 // tile's rows plus the kTaps-1 halo rows are all loaded before the first is used.
 // bf16 tiles of 12 tokens (84 VGPRs, 5 waves per SIMD) measured fastest at the
 // 0.8B shapes once the row loads were branch-free: 108.3 us against 108.4-109.9
-// for 8-14 tokens, 110.6-111.3 for 16-20, 113.7 for 24 and 119.2 for 40 (40 was
+// for 8-14 tokens, 110.6-111.3 for 16-20, 113.7 for 24 and 119.2 for 40 (and,
+// with the XCD runs below, 4 and 6 tokens 123.5 and 111.0 against 106.9; 40 was
 // the best of 8-64 while each row load sat in a branch of its own and the first
 // token waited for the whole tile); fp32 tiles of 8 tokens: 143.4 us against
 // 145.4 for 12 and 149.4 for 16 at 16384 tokens, 22.8 against 23.6 and 23.9 at
