@@ -69,7 +69,7 @@ __device__ __forceinline__ float softplus_f(float x) {
 // the best of 8-64 while each row load sat in a branch of its own and the first
 // token waited for the whole tile); fp32 tiles of 8 tokens: 143.4 us against
 // 145.4 for 12 and 149.4 for 16 at 16384 tokens, 22.8 against 23.6 and 23.9 at
-// 2048.  The halo rows (3 per tile) come from L2.
+// 2048.  The halo rows (3 per tile) come from L2 or the last-level cache.
 template <typename T> constexpr int tile_for() { return sizeof(T) == 2 ? 12 : 8; }
 // Short launches (a single sequence of a few hundred tokens) take tiles of 4
 // tokens: more workgroups on the chip and a 4-step chain per thread instead of
